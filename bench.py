@@ -1,0 +1,373 @@
+#!/usr/bin/env python3
+"""Throughput of the fused GGUF dequantize-and-multiply path on one MI355X.
+
+Headline workload (the JSON line's `value`): one decode token (M = 1) through all 80 layers
+of a Llama-3-70B Q4_K_M model whose weights are distinct random tensors resident in HBM
+(q/k/v/o/gate/up in Q4_K, down in Q6_K; 43.35 GB).  A step issues the 7 projections of
+every layer (560 GEMVs) back to back on one stream through `qmm_gemm_batch`; `value` is
+algorithmic bytes (packed weights + fp32 activations read once + fp32 outputs written once)
+per second over the timed steps.
+
+The `roofline` object covers the dominant kernel (the Q4_K GEMV serving gate/up,
+28672 x 8192): HIP events recorded around each of its launches inside the timed region give
+its average duration.  `cpu_baseline` times the in-repo NumPy restatement of the reference's
+CPU path (dequantize to fp16, then fp32 matmul) on a bounded sample.  `extra` holds the other
+configurations (8B Q8_0 / Q4_K_M layers, the 8B Q6_K lm_head, 70B at M = 4, the Q4_0
+4096 x 4096 case), each on rotated weight copies larger than the 256 MB MALL.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-extra] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import platform
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(REPO, "gfx1150-inference_amd")
+for _p in (PKG, os.path.join(REPO, "oracle")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_DENSE_PEAK_TFLOPS = 2500.0
+
+Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k"}
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def layer_specs(hidden, inter, kv, main, down):
+    """(name, type, N, K, input) of the 7 projections of one transformer layer."""
+    return [("q", main, hidden, hidden, "h"), ("k", main, kv, hidden, "h"), ("v", main, kv, hidden, "h"),
+            ("o", main, hidden, hidden, "h"), ("gate", main, inter, hidden, "h"), ("up", main, inter, hidden, "h"),
+            ("down", down, hidden, inter, "f")]
+
+
+def weight_bytes(t, n, k):
+    qk, bb = BLOCK[t]
+    return n * (k // qk) * bb
+
+
+class Hip:
+    """hipEvent helpers from the HIP runtime already loaded by torch (same runtime as libqmm)."""
+
+    def __init__(self):
+        self.lib = ctypes.CDLL("libamdhip64.so.7")
+        self.lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.lib.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+
+    def event(self):
+        e = ctypes.c_void_p()
+        rc = self.lib.hipEventCreate(ctypes.byref(e))
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreate failed ({rc})")
+        return e.value
+
+    def record(self, e, stream):
+        if self.lib.hipEventRecord(e, stream) != 0:
+            raise RuntimeError("hipEventRecord failed")
+
+    def elapsed_ms(self, a, b):
+        ms = ctypes.c_float()
+        if self.lib.hipEventElapsedTime(ctypes.byref(ms), a, b) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def destroy(self, e):
+        self.lib.hipEventDestroy(e)
+
+
+def make_weight(torch, t, n, k, gen, dev):
+    """Random packed weight with the benchmark distributions, generated on the GPU."""
+    qk, bb = BLOCK[t]
+    nb = n * (k // qk)
+    w = torch.randint(0, 256, (nb, bb), dtype=torch.uint8, device=dev, generator=gen)
+
+    def f16_field(scale):
+        return (torch.randn(nb, device=dev, generator=gen).abs() * scale).half().view(torch.uint8).view(nb, 2)
+
+    if t == Q4_0:
+        w[:, 0:2] = f16_field(0.02)
+    elif t == Q8_0:
+        w[:, 0:2] = f16_field(0.01)
+        w[:, 2:34] = torch.randint(-127, 128, (nb, 32), dtype=torch.int8, device=dev, generator=gen).view(torch.uint8)
+    elif t == Q4_K:
+        w[:, 0:2] = f16_field(0.01)
+        w[:, 2:4] = f16_field(0.01)
+    else:
+        w[:, 208:210] = f16_field(0.01)
+    return w.view(-1)
+
+
+class Workload:
+    """Weights, activations and the qmm_gemm_desc list of one step."""
+
+    def __init__(self, torch, qmm, name, specs_per_layer, layers, M, dev, gen, dominant=None):
+        self.torch, self.qmm, self.name, self.M = torch, qmm, name, M
+        self.weights, self.descs_py = [], []
+        self.inputs, self.outputs = {}, {}
+        widths = {}
+        for specs in specs_per_layer:
+            for (_, _, n, k, inp) in specs:
+                widths[inp] = k
+        for inp, k in widths.items():
+            self.inputs[inp] = torch.randn((M, k), device=dev, generator=gen, dtype=torch.float32)
+        self.algo_bytes = 0
+        self.weight_bytes = 0
+        self.flops = 0
+        self.dominant_idx = []
+        for layer in range(layers):
+            specs = specs_per_layer[layer % len(specs_per_layer)]
+            for (pname, t, n, k, inp) in specs:
+                w = make_weight(torch, t, n, k, gen, dev)
+                self.weights.append(w)
+                key = (pname, n)
+                if key not in self.outputs:
+                    self.outputs[key] = torch.empty((M, n), device=dev, dtype=torch.float32)
+                if dominant is not None and (t, n, k) == dominant:
+                    self.dominant_idx.append(len(self.descs_py))
+                self.descs_py.append((t, self.inputs[inp], w, self.outputs[key], n, k))
+                self.weight_bytes += weight_bytes(t, n, k)
+                self.algo_bytes += weight_bytes(t, n, k) + 4 * M * k + 4 * M * n
+                self.flops += 2 * M * n * k
+        self.dominant = dominant
+
+    def descs(self, events=None):
+        """ctypes array of GemmDesc; `events` maps desc index -> (ev_before, ev_after)."""
+        qmm = self.qmm
+        arr = (qmm.GemmDesc * len(self.descs_py))()
+        for i, (t, a, w, c, n, k) in enumerate(self.descs_py):
+            d = arr[i]
+            d.ggml_type, d.A, d.a_dtype, d.W, d.C, d.c_dtype = t, a.data_ptr(), qmm.DTYPE_F32, w.data_ptr(), \
+                c.data_ptr(), qmm.DTYPE_F32
+            d.M, d.N, d.K = self.M, n, k
+            ev = events.get(i) if events else None
+            d.ev_before, d.ev_after = (ev if ev else (None, None))
+        return arr
+
+    def free(self):
+        self.weights.clear()
+        self.descs_py.clear()
+
+
+def run_workload(torch, qmm, hip, wl, steps, warmup, time_dominant=False):
+    stream = torch.cuda.current_stream().cuda_stream
+    plain = wl.descs()
+    for _ in range(warmup):
+        qmm.check(qmm.lib().qmm_gemm_batch(plain, len(plain), stream))
+    torch.cuda.synchronize()
+    step_arrays, dom_events = [], []
+    for _ in range(steps):
+        events = {}
+        if time_dominant:
+            for i in wl.dominant_idx:
+                events[i] = (hip.event(), hip.event())
+            dom_events.extend(events.values())
+        step_arrays.append(wl.descs(events) if events else plain)
+    t_start, t_end = hip.event(), hip.event()
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    hip.record(t_start, stream)
+    for arr in step_arrays:
+        qmm.check(qmm.lib().qmm_gemm_batch(arr, len(arr), stream))
+    hip.record(t_end, stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    total_ms = hip.elapsed_ms(t_start, t_end)
+    dom_ms = [hip.elapsed_ms(a, b) for a, b in dom_events]
+    for e in [t_start, t_end] + [x for pair in dom_events for x in pair]:
+        hip.destroy(e)
+    return total_ms / steps, wall, dom_ms
+
+
+def cpu_baseline_70b(rows_fraction=0.25, seed=0):
+    """NumPy restatement of the reference CPU path (dequantize -> fp16 -> fp32 matmul) on the
+    first quarter of the rows of each of the 7 matrices of one 70B layer, M = 1."""
+    import numpy as np
+
+    import gguf_oracle as O
+
+    rng = np.random.default_rng(seed)
+    specs = layer_specs(8192, 28672, 1024, Q4_K, Q6_K)
+    xs = {"h": rng.standard_normal((1, 8192)).astype(np.float32),
+          "f": rng.standard_normal((1, 28672)).astype(np.float32)}
+    mats = []
+    for (_, t, n, k, inp) in specs:
+        rows = max(1, int(n * rows_fraction))
+        mats.append((t, rows, k, O.synth_weights(t, rows, k, rng), inp))
+    t0 = time.perf_counter()
+    nbytes = 0
+    for (t, rows, k, raw, inp) in mats:
+        W = O.dequantize_f16(t, raw, rows * k).reshape(rows, k).astype(np.float32)
+        _ = xs[inp] @ W.T
+        nbytes += raw.nbytes + 4 * k + 4 * rows
+    dt = time.perf_counter() - t0
+    threads = os.environ.get("OMP_NUM_THREADS") or os.environ.get("OPENBLAS_NUM_THREADS")
+    return {
+        "value": round(nbytes / dt / 1e9, 4),
+        "unit": "GB/s",
+        "cores": len(os.sched_getaffinity(0)),
+        "kind": "port",
+        "sample": (f"one Llama-3-70B Q4_K_M layer, first {int(rows_fraction * 100)}% of the rows of each of the "
+                   f"7 matrices ({nbytes / 1e6:.0f} MB packed), M=1: NumPy dequantize to fp16 (single thread) "
+                   f"then fp32 matmul (BLAS threads={threads or 'default'}); {dt:.1f} s; "
+                   f"CPU {platform.processor() or platform.machine()}"),
+        "ms_per_token_extrapolated_80_layers": round(dt / rows_fraction * 80 * 1e3, 1),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=80)
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported; this build measures one GPU "
+              "(the hot path shards by weight rows, see DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import qmm
+
+    dev = torch.device("cuda:0")
+    hip = Hip()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    props = torch.cuda.get_device_properties(dev)
+    log(f"device {props.name} {getattr(props, 'gcnArchName', '')} CUs={props.multi_processor_count}")
+
+    # ---- headline: Llama-3-70B Q4_K_M, M=1, 80 distinct layers -----------------------------
+    t0 = time.perf_counter()
+    specs70 = layer_specs(8192, 28672, 1024, Q4_K, Q6_K)
+    dominant = (Q4_K, 28672, 8192)
+    wl = Workload(torch, qmm, "70b", [specs70], args.layers, 1, dev, gen, dominant=dominant)
+    torch.cuda.synchronize()
+    log(f"70B weights ready: {wl.weight_bytes / 1e9:.2f} GB in {time.perf_counter() - t0:.1f} s")
+    ms, wall, dom_ms = run_workload(torch, qmm, hip, wl, args.steps, args.warmup, time_dominant=True)
+    gbs = wl.algo_bytes / (ms * 1e-3) / 1e9
+    log(f"70B M=1: {ms:.3f} ms/token, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM peak), "
+        f"wall {wall:.3f} s for {args.steps} steps")
+    dom_bytes = weight_bytes(Q4_K, 28672, 8192) + 4 * 8192 + 4 * 28672
+    dom_avg_ms = sum(dom_ms) / len(dom_ms)
+    dom_gbs = dom_bytes / (dom_avg_ms * 1e-3) / 1e9
+    log(f"dominant kernel (Q4_K 28672x8192 GEMV): {dom_avg_ms * 1e3:.2f} us avg over {len(dom_ms)} launches, "
+        f"{dom_gbs:.1f} GB/s")
+
+    traffic = None
+    tfile = os.path.join(REPO, "profiles", "gemv_q4_k_28672x8192_traffic.json")
+    if os.path.exists(tfile):
+        with open(tfile) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    extra = {}
+    if not args.no_extra:
+        # 70B at M = 4 on the same resident weights.
+        wl4 = Workload.__new__(Workload)
+        wl4.__dict__.update(wl.__dict__)
+        wl4.M = 4
+        wl4.inputs = {k: torch.randn((4, v.shape[1]), device=dev, generator=gen) for k, v in wl.inputs.items()}
+        wl4.outputs = {k: torch.empty((4, v.shape[1]), device=dev) for k, v in wl.outputs.items()}
+        remap_in = {id(wl.inputs[k]): wl4.inputs[k] for k in wl.inputs}
+        remap_out = {id(wl.outputs[k]): wl4.outputs[k] for k in wl.outputs}
+        wl4.descs_py = [(t, remap_in[id(a)], w, remap_out[id(c)], n, k) for (t, a, w, c, n, k) in wl.descs_py]
+        wl4.algo_bytes = sum(weight_bytes(t, n, k) + 16 * k + 16 * n for (t, _, _, _, n, k) in wl4.descs_py)
+        ms4, _, _ = run_workload(torch, qmm, hip, wl4, max(3, args.steps // 2), 2)
+        extra["70b_q4_k_m_m4"] = {"GB/s": round(wl4.algo_bytes / (ms4 * 1e-3) / 1e9, 1), "ms_per_token": round(ms4, 3),
+                                  "frac_hbm": round(wl4.algo_bytes / (ms4 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        log(f"70B M=4: {ms4:.3f} ms/step, {extra['70b_q4_k_m_m4']['GB/s']} GB/s")
+    wl.free()
+    del wl
+    torch.cuda.empty_cache()
+
+    if not args.no_extra:
+        # 8B layers rotated over enough copies to exceed the 256 MB MALL (>= 1.8 GB).
+        for key, main_t, down_t, copies in (("8b_q8_0_layer_m1", Q8_0, Q8_0, 8), ("8b_q4_k_m_layer_m1", Q4_K, Q6_K, 14)):
+            w8 = Workload(torch, qmm, key, [layer_specs(4096, 14336, 1024, main_t, down_t)], copies, 1, dev, gen)
+            ms8, _, _ = run_workload(torch, qmm, hip, w8, args.steps, args.warmup)
+            per_layer_us = ms8 * 1e3 / copies
+            g = w8.algo_bytes / (ms8 * 1e-3) / 1e9
+            extra[key] = {"GB/s": round(g, 1), "us_per_layer": round(per_layer_us, 2), "frac_hbm": round(g / HBM_PEAK_GBS, 4),
+                          "tokens_per_s_equiv_32_layers": round(1e6 / (per_layer_us * 32), 1),
+                          "footprint_GB": round(w8.weight_bytes / 1e9, 2)}
+            log(f"{key}: {extra[key]}")
+            w8.free()
+            del w8
+            torch.cuda.empty_cache()
+        lm = Workload(torch, qmm, "lm_head", [[("lm_head", Q6_K, 128256, 4096, "h")]], 4, 1, dev, gen)
+        msl, _, _ = run_workload(torch, qmm, hip, lm, args.steps, args.warmup)
+        g = lm.algo_bytes / (msl * 1e-3) / 1e9
+        extra["8b_q6_k_lm_head_m1"] = {"GB/s": round(g, 1), "us": round(msl * 1e3 / 4, 2), "frac_hbm": round(g / HBM_PEAK_GBS, 4)}
+        log(f"lm_head: {extra['8b_q6_k_lm_head_m1']}")
+        lm.free()
+        del lm
+        q40 = Workload(torch, qmm, "q4_0", [[("w", Q4_0, 4096, 4096, "h")]], 128, 1, dev, gen)
+        msq, _, _ = run_workload(torch, qmm, hip, q40, args.steps, args.warmup)
+        g = q40.algo_bytes / (msq * 1e-3) / 1e9
+        extra["q4_0_4096x4096_m1"] = {"GB/s": round(g, 1), "us": round(msq * 1e3 / 128, 2),
+                                      "note": "128 distinct copies (1.2 GB) streamed back to back"}
+        log(f"q4_0: {extra['q4_0_4096x4096_m1']}")
+        q40.free()
+        del q40
+        torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline (NumPy restatement of the reference CPU path) ...")
+        cpu = cpu_baseline_70b()
+        log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} cores")
+
+    line = {
+        "metric": "Q4_K/Q6_K GEMV GB/s (% of HBM peak) at 8B/70B shapes; prefill TFLOP/s",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32 activations, Q4_K/Q6_K weights, fp32 accumulate",
+        "data": "synthetic: random packed blocks (fp16 scales |N(0,1)|*0.01), x ~ N(0,1)",
+        "config": {"workload": "llama3-70b-q4_k_m-decode-m1-80-layers", "layers": args.layers, "M": 1,
+                   "hidden": 8192, "intermediate": 28672, "kv_dim": 1024,
+                   "weights_GB": round(wl_bytes_gb(args.layers), 2), "gemvs_per_step": 7 * args.layers,
+                   "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                   "tokens_per_s": round(1e3 / ms, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "gemv_kernel<FmtQ4K> (Q4_K 28672x8192, M=1)",
+                     "avg_us": round(dom_avg_ms * 1e3, 3), "launches": len(dom_ms),
+                     "algorithmic_bytes_per_launch": dom_bytes},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def wl_bytes_gb(layers):
+    s = layer_specs(8192, 28672, 1024, Q4_K, Q6_K)
+    return layers * sum(weight_bytes(t, n, k) for (_, t, n, k, _) in s) / 1e9
+
+
+if __name__ == "__main__":
+    main()

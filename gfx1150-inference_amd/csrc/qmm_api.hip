@@ -1,0 +1,260 @@
+// C ABI of libqmm_gfx950.so (declared in include/qmm.h): argument validation, kernel dispatch
+// and the host-pointer copy-in / compute / copy-out entry points.
+//
+// Error conventions follow the reference launchers (src/kernels/dequantize.hip:7-15, 734-736,
+// 771-773): a shape the block format cannot represent is QMM_ERR_INVALID_ARGUMENT (the
+// reference's std::invalid_argument), a HIP failure is QMM_ERR_HIP (std::runtime_error).
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "qmm_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+    return fail(QMM_ERR_HIP, std::string("HIP error in ") + where + " - " + hipGetErrorString(e));
+}
+
+const char* type_name(int t) {
+    switch (t) {
+        case QMM_TYPE_Q4_0: return "Q4_0";
+        case QMM_TYPE_Q8_0: return "Q8_0";
+        case QMM_TYPE_Q4_K: return "Q4_K";
+        case QMM_TYPE_Q6_K: return "Q6_K";
+        default: return "unknown";
+    }
+}
+
+bool known_type(int t) {
+    return t == QMM_TYPE_Q4_0 || t == QMM_TYPE_Q8_0 || t == QMM_TYPE_Q4_K || t == QMM_TYPE_Q6_K;
+}
+
+int check_gemm_args(int t, const void* A, int a_dtype, const void* W, void* C, int c_dtype, int M, int N,
+                    int K) {
+    if (!known_type(t)) return fail(QMM_ERR_INVALID_ARGUMENT, "Unsupported ggml_type " + std::to_string(t) + ".");
+    if (a_dtype != QMM_DTYPE_F32 && a_dtype != QMM_DTYPE_F16)
+        return fail(QMM_ERR_INVALID_ARGUMENT, "a_dtype must be QMM_DTYPE_F32 or QMM_DTYPE_F16.");
+    if (c_dtype != QMM_DTYPE_F32 && c_dtype != QMM_DTYPE_F16)
+        return fail(QMM_ERR_INVALID_ARGUMENT, "c_dtype must be QMM_DTYPE_F32 or QMM_DTYPE_F16.");
+    const int qk = qmm::block_elems(t);
+    if (K <= 0 || K % qk != 0)
+        return fail(QMM_ERR_INVALID_ARGUMENT, std::string("K dimension must be a positive multiple of ") +
+                                                  std::to_string(qk) + " for " + type_name(t) + " matmul.");
+    if (M < 0 || N < 0) return fail(QMM_ERR_INVALID_ARGUMENT, "M and N must be non-negative.");
+    if (M > 0 && N > 0 && (A == nullptr || W == nullptr || C == nullptr))
+        return fail(QMM_ERR_INVALID_ARGUMENT, "A, W and C must be non-null device pointers.");
+    return QMM_OK;
+}
+
+int check_dequant_args(int t, const void* W, void* out, int out_dtype, int64_t n, bool device_out) {
+    if (!known_type(t)) return fail(QMM_ERR_INVALID_ARGUMENT, "Unsupported ggml_type " + std::to_string(t) + ".");
+    if (out_dtype != QMM_DTYPE_F32 && out_dtype != QMM_DTYPE_F16 && out_dtype != QMM_DTYPE_BF16)
+        return fail(QMM_ERR_INVALID_ARGUMENT, "out_dtype must be QMM_DTYPE_F32, QMM_DTYPE_F16 or QMM_DTYPE_BF16.");
+    const int qk = qmm::block_elems(t);
+    if (n < 0 || n % qk != 0)
+        return fail(QMM_ERR_INVALID_ARGUMENT, std::string("num_elements must be a multiple of ") +
+                                                  std::to_string(qk) + " for " + type_name(t) + " dequantization.");
+    if (n > 0 && (W == nullptr || out == nullptr))
+        return fail(QMM_ERR_INVALID_ARGUMENT, "W and out must be non-null device pointers.");
+    if (device_out && n > 0 && (reinterpret_cast<uintptr_t>(out) & 15u) != 0)
+        return fail(QMM_ERR_INVALID_ARGUMENT, "out must be 16-byte aligned.");
+    return QMM_OK;
+}
+
+int gemm_impl(int t, const void* A, int a_dtype, const void* W, void* C, int c_dtype, int M, int N, int K,
+              hipStream_t stream) {
+    int rc = check_gemm_args(t, A, a_dtype, W, C, c_dtype, M, N, K);
+    if (rc != QMM_OK) return rc;
+    if (M == 0 || N == 0) return QMM_OK;
+    hipError_t e;
+    if (M >= qmm::kGemvMaxM && qmm::gemm_prefill_supported(t, a_dtype, c_dtype, M, N, K, A, W, C))
+        e = qmm::launch_gemm_prefill(t, A, a_dtype, W, C, c_dtype, M, N, K, stream);
+    else
+        e = qmm::launch_gemv(t, A, a_dtype, W, C, c_dtype, M, N, K, stream);
+    if (e != hipSuccess) return hip_fail(e, "qmm_gemm kernel launch");
+    return QMM_OK;
+}
+
+// Grow-only per-device workspace for the host-pointer API (the reference's Q4Workspace,
+// src/kernels/dequantize.hip:689-725).
+struct Workspace {
+    void* buf[3] = {nullptr, nullptr, nullptr};
+    size_t cap[3] = {0, 0, 0};
+};
+
+std::mutex g_ws_mutex;
+std::unordered_map<int, Workspace> g_ws;
+
+hipError_t ws_ensure(Workspace& ws, const size_t need[3]) {
+    for (int i = 0; i < 3; ++i) {
+        if (need[i] <= ws.cap[i]) continue;
+        if (ws.buf[i]) {
+            hipError_t e = hipFree(ws.buf[i]);
+            ws.buf[i] = nullptr;
+            ws.cap[i] = 0;
+            if (e != hipSuccess) return e;
+        }
+        hipError_t e = hipMalloc(&ws.buf[i], need[i]);
+        if (e != hipSuccess) {
+            ws.buf[i] = nullptr;
+            return e;
+        }
+        ws.cap[i] = need[i];
+    }
+    return hipSuccess;
+}
+
+int matmul_host(int t, const void* hA, const void* hB, void* hC, int M, int N, int K) {
+    int rc = check_gemm_args(t, hA, QMM_DTYPE_F16, hB, hC, QMM_DTYPE_F16, M, N, K);
+    if (rc != QMM_OK) return rc;
+    if (M == 0 || N == 0) return QMM_OK;
+    const size_t sa = static_cast<size_t>(M) * K * 2;
+    const size_t sb = static_cast<size_t>(N) * (K / qmm::block_elems(t)) * qmm::block_bytes(t);
+    const size_t sc = static_cast<size_t>(M) * N * 2;
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    Workspace& ws = g_ws[dev];
+    const size_t need[3] = {sa, sb, sc};
+    if ((e = ws_ensure(ws, need)) != hipSuccess) return hip_fail(e, "workspace hipMalloc");
+    if ((e = hipMemcpy(ws.buf[0], hA, sa, hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "hipMemcpy A");
+    if ((e = hipMemcpy(ws.buf[1], hB, sb, hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "hipMemcpy B");
+    rc = gemm_impl(t, ws.buf[0], QMM_DTYPE_F16, ws.buf[1], ws.buf[2], QMM_DTYPE_F16, M, N, K, nullptr);
+    if (rc != QMM_OK) return rc;
+    if ((e = hipMemcpy(hC, ws.buf[2], sc, hipMemcpyDeviceToHost)) != hipSuccess) return hip_fail(e, "hipMemcpy C");
+    return QMM_OK;
+}
+
+int dequant_host(int t, const void* hq, void* hout, int num_elements) {
+    int rc = check_dequant_args(t, hq, hout, QMM_DTYPE_F16, num_elements, false);
+    if (rc != QMM_OK) return rc;
+    if (num_elements == 0) return QMM_OK;
+    const size_t si = static_cast<size_t>(num_elements / qmm::block_elems(t)) * qmm::block_bytes(t);
+    const size_t so = static_cast<size_t>(num_elements) * 2;
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    Workspace& ws = g_ws[dev];
+    const size_t need[3] = {si, so, 0};
+    if ((e = ws_ensure(ws, need)) != hipSuccess) return hip_fail(e, "workspace hipMalloc");
+    if ((e = hipMemcpy(ws.buf[0], hq, si, hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "hipMemcpy q");
+    if ((e = qmm::launch_dequantize(t, ws.buf[0], ws.buf[1], QMM_DTYPE_F16, num_elements, nullptr)) != hipSuccess)
+        return hip_fail(e, "dequantize kernel launch");
+    if ((e = hipMemcpy(hout, ws.buf[1], so, hipMemcpyDeviceToHost)) != hipSuccess) return hip_fail(e, "hipMemcpy out");
+    return QMM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* qmm_last_error(void) { return g_last_error.c_str(); }
+
+int qmm_version(void) { return 1000; }
+
+int qmm_gemv_max_m(void) { return qmm::kGemvMaxM; }
+
+size_t qmm_weight_bytes(int ggml_type, int64_t n, int64_t k) {
+    if (!known_type(ggml_type) || n < 0 || k < 0) return 0;
+    const int qk = qmm::block_elems(ggml_type);
+    if (k % qk != 0) return 0;
+    return static_cast<size_t>(n) * static_cast<size_t>(k / qk) * static_cast<size_t>(qmm::block_bytes(ggml_type));
+}
+
+int qmm_gemm(int ggml_type, const void* A, int a_dtype, const void* W, void* C, int c_dtype, int M, int N, int K,
+             void* stream) {
+    return gemm_impl(ggml_type, A, a_dtype, W, C, c_dtype, M, N, K, static_cast<hipStream_t>(stream));
+}
+
+int qmm_gemm_batch(const qmm_gemm_desc* descs, int count, void* stream) {
+    if (count < 0 || (count > 0 && descs == nullptr))
+        return fail(QMM_ERR_INVALID_ARGUMENT, "descs must hold count >= 0 descriptors.");
+    for (int i = 0; i < count; ++i) {
+        const qmm_gemm_desc& d = descs[i];
+        int rc = check_gemm_args(d.ggml_type, d.A, d.a_dtype, d.W, d.C, d.c_dtype, d.M, d.N, d.K);
+        if (rc != QMM_OK) return fail(rc, "descriptor " + std::to_string(i) + ": " + g_last_error);
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int i = 0; i < count; ++i) {
+        const qmm_gemm_desc& d = descs[i];
+        hipError_t e;
+        if (d.ev_before && (e = hipEventRecord(static_cast<hipEvent_t>(d.ev_before), s)) != hipSuccess)
+            return hip_fail(e, "hipEventRecord");
+        int rc = gemm_impl(d.ggml_type, d.A, d.a_dtype, d.W, d.C, d.c_dtype, d.M, d.N, d.K, s);
+        if (rc != QMM_OK) return rc;
+        if (d.ev_after && (e = hipEventRecord(static_cast<hipEvent_t>(d.ev_after), s)) != hipSuccess)
+            return hip_fail(e, "hipEventRecord");
+    }
+    return QMM_OK;
+}
+
+int qmm_dequantize(int ggml_type, const void* W, void* out, int out_dtype, int64_t num_elements, void* stream) {
+    int rc = check_dequant_args(ggml_type, W, out, out_dtype, num_elements, true);
+    if (rc != QMM_OK) return rc;
+    if (num_elements == 0) return QMM_OK;
+    hipError_t e = qmm::launch_dequantize(ggml_type, W, out, out_dtype, num_elements,
+                                          static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "qmm_dequantize kernel launch");
+    return QMM_OK;
+}
+
+int qmm_matmul_q4_0_device(const void* a, const void* b, void* c, int M, int N, int K, void* s) {
+    return qmm_gemm(QMM_TYPE_Q4_0, a, QMM_DTYPE_F16, b, c, QMM_DTYPE_F16, M, N, K, s);
+}
+int qmm_matmul_q8_0_device(const void* a, const void* b, void* c, int M, int N, int K, void* s) {
+    return qmm_gemm(QMM_TYPE_Q8_0, a, QMM_DTYPE_F16, b, c, QMM_DTYPE_F16, M, N, K, s);
+}
+int qmm_matmul_q4_k_device(const void* a, const void* b, void* c, int M, int N, int K, void* s) {
+    return qmm_gemm(QMM_TYPE_Q4_K, a, QMM_DTYPE_F16, b, c, QMM_DTYPE_F16, M, N, K, s);
+}
+int qmm_matmul_q6_k_device(const void* a, const void* b, void* c, int M, int N, int K, void* s) {
+    return qmm_gemm(QMM_TYPE_Q6_K, a, QMM_DTYPE_F16, b, c, QMM_DTYPE_F16, M, N, K, s);
+}
+
+int qmm_matmul_q4_0_host(const void* a, const void* b, void* c, int M, int N, int K) {
+    return matmul_host(QMM_TYPE_Q4_0, a, b, c, M, N, K);
+}
+int qmm_matmul_q8_0_host(const void* a, const void* b, void* c, int M, int N, int K) {
+    return matmul_host(QMM_TYPE_Q8_0, a, b, c, M, N, K);
+}
+int qmm_matmul_q4_k_host(const void* a, const void* b, void* c, int M, int N, int K) {
+    return matmul_host(QMM_TYPE_Q4_K, a, b, c, M, N, K);
+}
+int qmm_matmul_q6_k_host(const void* a, const void* b, void* c, int M, int N, int K) {
+    return matmul_host(QMM_TYPE_Q6_K, a, b, c, M, N, K);
+}
+
+int qmm_dequantize_q4_0_host(const void* q, void* out, int n) { return dequant_host(QMM_TYPE_Q4_0, q, out, n); }
+int qmm_dequantize_q8_0_host(const void* q, void* out, int n) { return dequant_host(QMM_TYPE_Q8_0, q, out, n); }
+int qmm_dequantize_q4_k_host(const void* q, void* out, int n) { return dequant_host(QMM_TYPE_Q4_K, q, out, n); }
+int qmm_dequantize_q6_k_host(const void* q, void* out, int n) { return dequant_host(QMM_TYPE_Q6_K, q, out, n); }
+
+int qmm_release_workspace(void) {
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    for (auto& kv : g_ws) {
+        if ((e = hipSetDevice(kv.first)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+        for (int i = 0; i < 3; ++i) {
+            if (kv.second.buf[i]) (void)hipFree(kv.second.buf[i]);
+            kv.second.buf[i] = nullptr;
+            kv.second.cap[i] = 0;
+        }
+    }
+    g_ws.clear();
+    if ((e = hipSetDevice(cur)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+    return QMM_OK;
+}
+
+}  // extern "C"

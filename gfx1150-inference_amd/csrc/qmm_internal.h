@@ -1,0 +1,57 @@
+// Internal declarations shared by the HIP translation units of libqmm_gfx950.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "qmm.h"
+
+namespace qmm {
+
+// GGUF block geometry (reference src/kernels/dequantize.h:6-22).
+constexpr int kQK4_0 = 32, kBytesQ4_0 = 18;
+constexpr int kQK8_0 = 32, kBytesQ8_0 = 34;
+constexpr int kQK_K = 256, kBytesQ4_K = 144, kBytesQ6_K = 210;
+
+// Every GEMV wave walks K in windows of 2048 weights: 64 lanes x 32-weight slots.
+constexpr int kWave = 64;
+constexpr int kWindow = 2048;
+constexpr int kSlot = 32;
+
+// M below this runs the GEMV family (bit-identical per row for every M);
+// M at or above it runs the MFMA prefill GEMM.
+constexpr int kGemvMaxM = 32;
+
+inline int block_elems(int t) {
+    switch (t) {
+        case QMM_TYPE_Q4_0: return kQK4_0;
+        case QMM_TYPE_Q8_0: return kQK8_0;
+        case QMM_TYPE_Q4_K: return kQK_K;
+        case QMM_TYPE_Q6_K: return kQK_K;
+        default: return 0;
+    }
+}
+
+inline int block_bytes(int t) {
+    switch (t) {
+        case QMM_TYPE_Q4_0: return kBytesQ4_0;
+        case QMM_TYPE_Q8_0: return kBytesQ8_0;
+        case QMM_TYPE_Q4_K: return kBytesQ4_K;
+        case QMM_TYPE_Q6_K: return kBytesQ6_K;
+        default: return 0;
+    }
+}
+
+// Kernel launchers (validated arguments; return a hipError_t from the launch).
+hipError_t launch_gemv(int ggml_type, const void* A, int a_dtype, const void* W, void* C,
+                       int c_dtype, int M, int N, int K, hipStream_t stream);
+hipError_t launch_gemm_prefill(int ggml_type, const void* A, int a_dtype, const void* W, void* C,
+                               int c_dtype, int M, int N, int K, hipStream_t stream);
+bool gemm_prefill_supported(int ggml_type, int a_dtype, int c_dtype, int M, int N, int K,
+                            const void* A, const void* W, const void* C);
+hipError_t launch_dequantize(int ggml_type, const void* W, void* out, int out_dtype,
+                             int64_t num_elements, hipStream_t stream);
+
+}  // namespace qmm

@@ -1,0 +1,194 @@
+"""Host-side Python interface to ``libqmm_gfx950.so`` for device-resident buffers.
+
+This is the device-pointer counterpart of the drop-in ``matmul_module`` (which keeps the
+reference's host-array API).  Every call goes through the C ABI declared in
+``include/qmm.h``; PyTorch is used only to own device memory and to supply the current
+HIP stream.  There is no CPU fallback: if the library is missing, importing this module
+raises ``ImportError``.
+
+Weight type ids are the GGMLType integers of the reference (``src/gguf_parser.py:22-36``);
+device launchers mirror ``launch_matmul_q*_device`` (``src/kernels/dequantize.h:98-132``)
+and raise ``ValueError`` / ``RuntimeError`` where the reference throws
+``std::invalid_argument`` / ``std::runtime_error``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+from typing import Optional
+
+_PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+_REPO_DIR = os.path.dirname(_PKG_DIR)
+LIB_PATH = os.path.join(_PKG_DIR, "libqmm_gfx950.so")
+HEADER_PATH = os.path.join(_REPO_DIR, "include", "qmm.h")
+
+GGML_F16 = 1
+GGML_Q4_0 = 2
+GGML_Q8_0 = 8
+GGML_Q4_K = 12
+GGML_Q6_K = 14
+
+# (block_elems, block_bytes) of every supported type (src/kernels/dequantize.h:6-22).
+BLOCK_INFO = {GGML_Q4_0: (32, 18), GGML_Q8_0: (32, 34), GGML_Q4_K: (256, 144), GGML_Q6_K: (256, 210)}
+
+QMM_OK = 0
+QMM_ERR_INVALID_ARGUMENT = 1
+QMM_ERR_UNSUPPORTED = 2
+QMM_ERR_HIP = 3
+
+DTYPE_F32 = 0
+DTYPE_F16 = 1
+DTYPE_BF16 = 2
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(
+        f"{LIB_PATH} is not built; run `python gfx1150-inference_amd/build_ext.py` "
+        "(or __graft_entry__.build()) first. There is no CPU fallback.")
+
+# In a process that also uses PyTorch, torch must load its HIP runtime first: the library's
+# libamdhip64.so.7 dependency then binds to that already-loaded runtime instead of bringing a
+# second HIP/HSA runtime into the process.
+try:
+    import torch  # noqa: F401
+except ImportError:
+    pass
+
+_lib = ctypes.CDLL(LIB_PATH)
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+
+
+class GemmDesc(ctypes.Structure):
+    """Mirror of qmm_gemm_desc (include/qmm.h)."""
+
+    _fields_ = [("ggml_type", _i), ("A", _vp), ("a_dtype", _i), ("W", _vp), ("C", _vp), ("c_dtype", _i),
+                ("M", _i), ("N", _i), ("K", _i), ("ev_before", _vp), ("ev_after", _vp)]
+
+_SIGNATURES = {
+    "qmm_last_error": (ctypes.c_char_p, []),
+    "qmm_version": (_i, []),
+    "qmm_gemv_max_m": (_i, []),
+    "qmm_weight_bytes": (ctypes.c_size_t, [_i, _i64, _i64]),
+    "qmm_gemm": (_i, [_i, _vp, _i, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "qmm_dequantize": (_i, [_i, _vp, _vp, _i, _i64, _vp]),
+    "qmm_gemm_batch": (_i, [ctypes.POINTER(GemmDesc), _i, _vp]),
+    "qmm_release_workspace": (_i, []),
+}
+for _t in ("q4_0", "q8_0", "q4_k", "q6_k"):
+    _SIGNATURES[f"qmm_matmul_{_t}_device"] = (_i, [_vp, _vp, _vp, _i, _i, _i, _vp])
+    _SIGNATURES[f"qmm_matmul_{_t}_host"] = (_i, [_vp, _vp, _vp, _i, _i, _i])
+    _SIGNATURES[f"qmm_dequantize_{_t}_host"] = (_i, [_vp, _vp, _i])
+
+for _name, (_res, _args) in _SIGNATURES.items():
+    _fn = getattr(_lib, _name)
+    _fn.restype = _res
+    _fn.argtypes = _args
+
+
+def lib() -> ctypes.CDLL:
+    return _lib
+
+
+def header_symbols() -> list:
+    """Function names declared in include/qmm.h (used to check the exported ABI)."""
+    text = open(HEADER_PATH).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*|int|size_t)\s+(qmm_\w+)\s*\(", text, re.M)))
+
+
+def last_error() -> str:
+    return _lib.qmm_last_error().decode()
+
+
+def check(rc: int) -> None:
+    if rc == QMM_OK:
+        return
+    msg = last_error()
+    if rc == QMM_ERR_INVALID_ARGUMENT:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def weight_bytes(ggml_type: int, n: int, k: int) -> int:
+    return int(_lib.qmm_weight_bytes(ggml_type, n, k))
+
+
+def gemv_max_m() -> int:
+    return int(_lib.qmm_gemv_max_m())
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _stream_handle(stream=None) -> Optional[int]:
+    torch = _torch()
+    s = torch.cuda.current_stream() if stream is None else stream
+    return s.cuda_stream
+
+
+def _dtype_code(t) -> int:
+    torch = _torch()
+    if t == torch.float32:
+        return DTYPE_F32
+    if t == torch.float16:
+        return DTYPE_F16
+    if t == torch.bfloat16:
+        return DTYPE_BF16
+    raise ValueError(f"unsupported dtype {t}")
+
+
+def gemm(ggml_type: int, A, W, N: int, K: int, out=None, out_dtype=None, stream=None):
+    """C[M, N] = A[M, K] @ dequant(W)[N, K]^T on the GPU (device tensors, asynchronous)."""
+    torch = _torch()
+    if A.dim() != 2 or A.shape[1] != K or not A.is_contiguous():
+        raise ValueError("A must be a contiguous [M, K] device tensor")
+    if W.dtype != torch.uint8 or not W.is_contiguous():
+        raise ValueError("W must be a contiguous uint8 device tensor")
+    if W.numel() < weight_bytes(ggml_type, N, K):
+        raise ValueError("W is smaller than N * (K / block) * block_bytes")
+    M = A.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype or torch.float32, device=A.device)
+    elif out.shape != (M, N) or not out.is_contiguous():
+        raise ValueError("out must be a contiguous [M, N] device tensor")
+    check(_lib.qmm_gemm(ggml_type, A.data_ptr(), _dtype_code(A.dtype), W.data_ptr(), out.data_ptr(),
+                        _dtype_code(out.dtype), M, N, K, _stream_handle(stream)))
+    return out
+
+
+def gemm_batch(descs, stream=None) -> None:
+    """Launch a ctypes array of GemmDesc back to back on `stream` (one C call)."""
+    check(_lib.qmm_gemm_batch(descs, len(descs), _stream_handle(stream)))
+
+
+def dequantize(ggml_type: int, W, num_elements: int, out=None, out_dtype=None, stream=None):
+    """dequant(W) -> [num_elements] device tensor (fp16 / bf16 / fp32), bit-exact."""
+    torch = _torch()
+    if out is None:
+        out = torch.empty((num_elements,), dtype=out_dtype or torch.float16, device=W.device)
+    check(_lib.qmm_dequantize(ggml_type, W.data_ptr(), out.data_ptr(), _dtype_code(out.dtype),
+                              num_elements, _stream_handle(stream)))
+    return out
+
+
+def _device_launcher(name):
+    fn = getattr(_lib, name)
+
+    def launch(d_A_fp16, d_B, d_C_fp16, M: int, N: int, K: int, stream=None) -> None:
+        check(fn(d_A_fp16.data_ptr(), d_B.data_ptr(), d_C_fp16.data_ptr(), M, N, K, _stream_handle(stream)))
+
+    launch.__name__ = name
+    launch.__doc__ = (f"{name}: fp16 A [M,K], packed B [N,K], fp16 C [M,N] device tensors "
+                      "(launch_matmul_*_device of src/kernels/dequantize.h:98-132).")
+    return launch
+
+
+matmul_q4_0_device = _device_launcher("qmm_matmul_q4_0_device")
+matmul_q8_0_device = _device_launcher("qmm_matmul_q8_0_device")
+matmul_q4_k_device = _device_launcher("qmm_matmul_q4_k_device")
+matmul_q6_k_device = _device_launcher("qmm_matmul_q6_k_device")

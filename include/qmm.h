@@ -1,0 +1,144 @@
+/*
+ * qmm.h - C ABI of libqmm_gfx950.so: fused dequantize-and-multiply over GGUF
+ * Q4_0 / Q8_0 / Q4_K / Q6_K weight blocks on MI355X (gfx950).
+ *
+ * Conventions
+ *   - Weights are N x K, row-major, packed in native GGUF blocks along K
+ *     (GGUF ne[0] = K; reference src/gguf_parser.py:89-101).  C = A @ W^T.
+ *   - Every function returns a qmm_status; on failure qmm_last_error() returns a
+ *     thread-local message.  No C++ exception crosses this boundary.
+ *   - `stream` is a hipStream_t passed as an opaque pointer (NULL = the null
+ *     stream).  Device-pointer entry points are asynchronous on that stream.
+ *   - Type ids are the GGMLType integers (reference src/gguf_parser.py:22-36):
+ *     1 = F16, 2 = Q4_0, 8 = Q8_0, 12 = Q4_K, 14 = Q6_K.
+ *   - Activation/output dtypes: QMM_DTYPE_F32, QMM_DTYPE_F16 (IEEE binary16),
+ *     QMM_DTYPE_BF16 (dequantize output only).
+ */
+#ifndef QMM_H
+#define QMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum qmm_status {
+    QMM_OK = 0,
+    QMM_ERR_INVALID_ARGUMENT = 1, /* maps to the reference's std::invalid_argument / ValueError */
+    QMM_ERR_UNSUPPORTED = 2,      /* valid request this build does not implement */
+    QMM_ERR_HIP = 3               /* HIP runtime error; maps to std::runtime_error / RuntimeError */
+};
+
+enum qmm_ggml_type {
+    QMM_TYPE_F16 = 1,
+    QMM_TYPE_Q4_0 = 2,
+    QMM_TYPE_Q8_0 = 8,
+    QMM_TYPE_Q4_K = 12,
+    QMM_TYPE_Q6_K = 14
+};
+
+enum qmm_dtype {
+    QMM_DTYPE_F32 = 0,
+    QMM_DTYPE_F16 = 1,
+    QMM_DTYPE_BF16 = 2
+};
+
+/* Thread-local message of the last failed call on this thread ("" if none). */
+const char* qmm_last_error(void);
+
+/* ABI version of this library (major * 1000 + minor). */
+int qmm_version(void);
+
+/* Packed byte size of an N x K weight; 0 if K is not a multiple of the block size.
+ * Replaces weight_bytes_for_type (reference src/kernels/attention.hip:553-570). */
+size_t qmm_weight_bytes(int ggml_type, int64_t n, int64_t k);
+
+/* ---------------------------------------------------------------------------------
+ * Device-pointer API (primary).
+ * --------------------------------------------------------------------------------- */
+
+/* C[M,N] (c_dtype) = A[M,K] (a_dtype) @ dequant(W)[N,K]^T with fp32 accumulation.
+ * M < QMM_GEMV_MAX_M runs the bandwidth-bound GEMV family, whose row m result is
+ * bit-identical for every M; larger M runs the bf16-MFMA prefill GEMM.
+ * Generalises launch_matmul_q{4_0,8_0,4_k,6_k}_device (reference
+ * src/kernels/dequantize.h:98-132, dispatch at dequantize.hip:778/896/1014/1132). */
+int qmm_gemm(int ggml_type, const void* A, int a_dtype, const void* W, void* C, int c_dtype,
+             int M, int N, int K, void* stream);
+
+/* One GEMM of a batch.  ev_before / ev_after are optional hipEvent_t handles (NULL = none)
+ * recorded on the batch's stream immediately before / after this GEMM's kernel. */
+typedef struct qmm_gemm_desc {
+    int ggml_type;
+    const void* A;
+    int a_dtype;
+    const void* W;
+    void* C;
+    int c_dtype;
+    int M, N, K;
+    void* ev_before;
+    void* ev_after;
+} qmm_gemm_desc;
+
+/* Validates every descriptor, then launches them back to back on `stream` in order
+ * (no host synchronisation).  Replaces the per-projection launches of the reference's
+ * device-resident layer pipeline (src/kernels/attention.hip:650-687, project_on_device
+ * :572-599) for callers that keep weights resident. */
+int qmm_gemm_batch(const qmm_gemm_desc* descs, int count, void* stream);
+
+/* dequant(W) -> out[num_elements] in out_dtype (F16, BF16 or F32), bit-exact.
+ * Generalises dequantize_{q4_0,q8_0,q4_k,q6_k}_kernel launches
+ * (reference src/kernels/dequantize.hip:68-88, 213-229, 335-371, 508-544). */
+int qmm_dequantize(int ggml_type, const void* W, void* out, int out_dtype,
+                   int64_t num_elements, void* stream);
+
+/* Largest M served by the GEMV family (exclusive bound), and the prefill threshold. */
+int qmm_gemv_max_m(void);
+
+/* Per-type device launchers with the reference's argument meaning: fp16 A [M,K],
+ * packed B [N,K], fp16 C [M,N], all device pointers, on `stream`.
+ * Replace launch_matmul_q4_0_device / _q8_0_ / _q4_k_ / _q6_k_device
+ * (reference src/kernels/dequantize.h:98-132, dequantize.hip:764-818, 882-936,
+ * 1000-1054, 1118-1172). */
+int qmm_matmul_q4_0_device(const void* d_A_fp16, const void* d_B_q4, void* d_C_fp16,
+                           int M, int N, int K, void* stream);
+int qmm_matmul_q8_0_device(const void* d_A_fp16, const void* d_B_q8, void* d_C_fp16,
+                           int M, int N, int K, void* stream);
+int qmm_matmul_q4_k_device(const void* d_A_fp16, const void* d_B_q4k, void* d_C_fp16,
+                           int M, int N, int K, void* stream);
+int qmm_matmul_q6_k_device(const void* d_A_fp16, const void* d_B_q6k, void* d_C_fp16,
+                           int M, int N, int K, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Host-pointer API: the reference's synchronous copy-in / compute / copy-out
+ * semantics through a grow-only device workspace.
+ * --------------------------------------------------------------------------------- */
+
+/* Replace launch_matmul_q{4_0,8_0,4_k,6_k} (reference src/kernels/dequantize.h:34-41,
+ * 51-58, 69-76, 86-93; dequantize.hip:820-845, 938-963, 1056-1081, 1174-1199). */
+int qmm_matmul_q4_0_host(const void* h_A_fp16, const void* h_B_q4, void* h_C_fp16,
+                         int M, int N, int K);
+int qmm_matmul_q8_0_host(const void* h_A_fp16, const void* h_B_q8, void* h_C_fp16,
+                         int M, int N, int K);
+int qmm_matmul_q4_k_host(const void* h_A_fp16, const void* h_B_q4k, void* h_C_fp16,
+                         int M, int N, int K);
+int qmm_matmul_q6_k_host(const void* h_A_fp16, const void* h_B_q6k, void* h_C_fp16,
+                         int M, int N, int K);
+
+/* Replace launch_dequantize_q{4_0,8_0,4_k,6_k} (reference src/kernels/dequantize.h:25-29,
+ * 44-48, 62-66, 79-83; dequantize.hip:729-762, 847-880, 965-998, 1083-1116). */
+int qmm_dequantize_q4_0_host(const void* h_q4, void* h_fp16_out, int num_elements);
+int qmm_dequantize_q8_0_host(const void* h_q8, void* h_fp16_out, int num_elements);
+int qmm_dequantize_q4_k_host(const void* h_q4k, void* h_fp16_out, int num_elements);
+int qmm_dequantize_q6_k_host(const void* h_q6k, void* h_fp16_out, int num_elements);
+
+/* Release the host-API workspace (the reference frees its static Q4Workspace at exit,
+ * dequantize.hip:715-719). Safe to call at any time; the next host call re-grows it. */
+int qmm_release_workspace(void);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* QMM_H */

@@ -1,0 +1,320 @@
+"""GPU parity of the HIP path against the oracle (run on an MI355X; every call goes through the
+C ABI of libqmm_gfx950.so).
+
+Bars (tolerances are written into each check):
+* dequantize: bit-exact against the oracle in fp16, bf16 and fp32;
+* GEMV (M < qmm_gemv_max_m): max_i|y_i - y64_i| / max_i|y64_i| <= 1e-3 against fp64 on the
+  exact weights, and the reference tests' own absolute tolerances against the reference
+  formula (fp16-rounded weights, fp32 matmul);
+* row results bit-identical for every M in the GEMV range (the reference's invariant,
+  tests/test_phase5_scale.py:274-310, 371-379);
+* full 8B / 70B shapes: sampled rows against fp64, linearity in x.
+"""
+
+import os
+import zlib
+
+import numpy as np
+import pytest
+
+import gguf_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [O.GGML_Q4_0, O.GGML_Q8_0, O.GGML_Q4_K, O.GGML_Q6_K]
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "kat_blocks.npz")
+GEMV_TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def dev(cuda):
+    import qmm  # noqa: F401  (fails loudly if the library is not built)
+    return cuda
+
+
+def to_dev(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def gemm(t, A_np, raw_np, N, K, dev, a_dtype="f32", c_dtype="f32"):
+    import torch
+    import qmm
+    A = to_dev(A_np.astype(np.float32 if a_dtype == "f32" else np.float16), dev)
+    W = to_dev(raw_np, dev)
+    C = qmm.gemm(t, A, W, N, K, out_dtype=torch.float32 if c_dtype == "f32" else torch.float16)
+    torch.cuda.synchronize()
+    return C.float().cpu().numpy().astype(np.float64)
+
+
+# ------------------------------------------------------------------------------ dequantize
+
+@pytest.mark.parametrize("t", TYPES)
+def test_dequant_kat_bit_exact(dev, t):
+    import torch
+    import qmm
+    kat = np.load(GOLDEN, allow_pickle=False)
+    name = O.TYPE_NAMES[t]
+    raw, n = kat[f"{name}_raw"], kat[f"{name}_w64"].size
+    W = to_dev(raw, dev)
+    f16 = qmm.dequantize(t, W, n, out_dtype=torch.float16).cpu().numpy()
+    f32 = qmm.dequantize(t, W, n, out_dtype=torch.float32).cpu().numpy()
+    np.testing.assert_array_equal(f16.view(np.uint16), kat[f"{name}_f16"].view(np.uint16))
+    np.testing.assert_array_equal(f32.view(np.uint32), kat[f"{name}_f32"].view(np.uint32))
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("out", ["f16", "bf16", "f32"])
+def test_dequant_synthetic_bit_exact(dev, t, out):
+    import torch
+    import qmm
+    rng = np.random.default_rng(100 + t)
+    qk, bb = O.BLOCK_INFO[t]
+    n = 96 * 4096
+    raw = O.synth_weights(t, 96, 4096, rng)
+    dt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[out]
+    got = qmm.dequantize(t, to_dev(raw, dev), n, out_dtype=dt)
+    torch.cuda.synchronize()
+    f32 = O.DEQUANT_F32[t](raw, n)
+    if out == "f16":
+        np.testing.assert_array_equal(got.cpu().numpy().view(np.uint16), f32.astype(np.float16).view(np.uint16))
+    elif out == "bf16":
+        np.testing.assert_array_equal(got.view(torch.int16).cpu().numpy().view(np.uint16), O.f32_to_bf16_bits(f32))
+    else:
+        np.testing.assert_array_equal(got.cpu().numpy().view(np.uint32), f32.view(np.uint32))
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_dequant_random_bytes_nan_aware(dev, t):
+    import torch
+    import qmm
+    rng = np.random.default_rng(7 + t)
+    qk, bb = O.BLOCK_INFO[t]
+    raw = rng.integers(0, 256, size=512 * bb, dtype=np.uint8)
+    got = qmm.dequantize(t, to_dev(raw, dev), 512 * qk, out_dtype=torch.float32).cpu().numpy()
+    ref = O.DEQUANT_F32[t](raw, 512 * qk)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    np.testing.assert_array_equal(got[ok].view(np.uint32), ref[ok].view(np.uint32))
+
+
+def test_dequantize_q4_0_reference_case(dev):
+    # tests/test_gguf_and_q4.py:94-112: 1M elements, seed 42, x ~ N(0,1) * 0.1; documented exact.
+    import matmul_module
+    rng = np.random.default_rng(42)
+    n = 1024 * 1024
+    q4 = O.quantize_q4_0(rng.standard_normal(n, dtype=np.float32) * 0.1)
+    out = np.zeros(n, dtype=np.float16)
+    matmul_module.dequantize_q4_0(q4, out, n)
+    np.testing.assert_array_equal(out.view(np.uint16), O.dequantize_f16(O.GGML_Q4_0, q4, n).view(np.uint16))
+
+
+@pytest.mark.parametrize("t,seed", [(O.GGML_Q8_0, 501), (O.GGML_Q4_K, 502), (O.GGML_Q6_K, 611)])
+def test_dequantize_host_api_reference_cases(dev, t, seed):
+    # tests/test_phase5_scale.py:42-102, 347-356: GPU dequant vs CPU reference (ours: exact).
+    import matmul_module
+    rng = np.random.default_rng(seed)
+    n = {O.GGML_Q8_0: 4096 * 32, O.GGML_Q4_K: 256 * 256, O.GGML_Q6_K: 512 * 256}[t]
+    q = O.QUANTIZE[t](rng.standard_normal(n, dtype=np.float32) * 0.4)
+    out = np.empty(n, dtype=np.float16)
+    getattr(matmul_module, f"dequantize_{O.TYPE_NAMES[t]}")(q, out, n)
+    np.testing.assert_array_equal(out.view(np.uint16), O.dequantize_f16(t, q, n).view(np.uint16))
+
+
+# ------------------------------------------------------------------------------ GEMV
+
+GEMV_SHAPES = {
+    O.GGML_Q4_0: [(512, 4096), (300, 2304), (64, 256)],          # full windows, tail window, tiny
+    O.GGML_Q8_0: [(512, 4096), (300, 2304), (64, 256)],
+    O.GGML_Q4_K: [(512, 4096), (300, 2304), (96, 256)],
+    O.GGML_Q6_K: [(512, 4096), (257, 6144), (96, 512)],          # 512: fallback (K % 2048 != 0)
+}
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_gemv_vs_fp64(dev, t, M):
+    rng = np.random.default_rng(1000 * t + M)
+    for N, K in GEMV_SHAPES[t]:
+        raw = O.synth_weights(t, N, K, rng)
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        y64 = O.matmul_f64(t, x, raw, N, K)
+        y = gemm(t, x, raw, N, K, dev)
+        err = O.max_rel_err(y, y64)
+        assert err <= GEMV_TOL, (O.TYPE_NAMES[t], M, N, K, err)
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("a_dtype,c_dtype", [("f16", "f16"), ("f16", "f32"), ("f32", "f16")])
+def test_gemv_dtypes(dev, t, a_dtype, c_dtype):
+    rng = np.random.default_rng(77 + t)
+    N, K = GEMV_SHAPES[t][0]
+    raw = O.synth_weights(t, N, K, rng)
+    x = rng.standard_normal((2, K)).astype(np.float32)
+    xa = x.astype(np.float16).astype(np.float32) if a_dtype == "f16" else x
+    y64 = O.matmul_f64(t, xa, raw, N, K)
+    y = gemm(t, x, raw, N, K, dev, a_dtype=a_dtype, c_dtype=c_dtype)
+    assert O.max_rel_err(y, y64) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_gemv_rows_bit_identical_across_m(dev, t):
+    import qmm
+    rng = np.random.default_rng(601 + t)
+    for N, K in GEMV_SHAPES[t][:2] + GEMV_SHAPES[t][-1:]:
+        raw = O.synth_weights(t, N, K, rng)
+        Mmax = min(qmm.gemv_max_m() - 1, 31)
+        x = rng.standard_normal((Mmax, K)).astype(np.float32)
+        single = np.stack([gemm(t, x[m:m + 1], raw, N, K, dev)[0] for m in range(Mmax)])
+        for M in (2, 3, 4, 7, 16, Mmax):
+            y = gemm(t, x[:M], raw, N, K, dev)
+            np.testing.assert_array_equal(y, single[:M], err_msg=f"{O.TYPE_NAMES[t]} M={M} N={N} K={K}")
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_golden_gemv(dev, t):
+    kat = np.load(GOLDEN, allow_pickle=False)
+    name = O.TYPE_NAMES[t]
+    n_rows, k = (int(v) for v in kat[f"{name}_gemv_n"])
+    y = gemm(t, kat[f"{name}_gemv_x"], kat[f"{name}_raw"], n_rows, k, dev)
+    assert O.max_rel_err(y, kat[f"{name}_gemv_y64"]) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_gemv_unaligned_weights_fallback(dev, t):
+    import torch
+    import qmm
+    rng = np.random.default_rng(31 + t)
+    N, K = 64, 2048
+    raw = O.synth_weights(t, N, K, rng)
+    buf = torch.zeros(raw.size + 16, dtype=torch.uint8, device=dev)
+    buf[2:2 + raw.size] = to_dev(raw, dev)
+    W = buf[2:2 + raw.size]  # 2-byte aligned: the byte-load fallback must serve it
+    x = rng.standard_normal((3, K)).astype(np.float32)
+    y = qmm.gemm(t, to_dev(x, dev), W, N, K).cpu().numpy().astype(np.float64)
+    assert O.max_rel_err(y, O.matmul_f64(t, x, raw, N, K)) <= GEMV_TOL
+
+
+# --------------------------------------------------- the reference's own test cases (host API)
+
+def _ref_matmul_case(dev, t, seed, shapes, scale, tol, quant=True):
+    import matmul_module
+    fn = getattr(matmul_module, f"matmul_{O.TYPE_NAMES[t]}")
+    rng = np.random.default_rng(seed)
+    for M, N, K in shapes:
+        s = scale if scale is not None else 1.0 / np.sqrt(K)
+        A = (rng.standard_normal((M, K), dtype=np.float32) * s).astype(np.float16)
+        B = O.QUANTIZE[t](rng.standard_normal((N, K), dtype=np.float32) * s)
+        C = np.zeros((M, N), dtype=np.float16)
+        fn(A, B, C, M, N, K)
+        C_ref = O.matmul_reference(t, A, B, N, K).astype(np.float16)
+        err = float(np.max(np.abs(C.astype(np.float32) - C_ref.astype(np.float32))))
+        assert err < tol, (O.TYPE_NAMES[t], M, N, K, err)
+        assert O.max_rel_err(C.astype(np.float64), O.matmul_f64(t, A.astype(np.float32), B, N, K)) <= GEMV_TOL
+
+
+def test_fused_matmul_q4_0_reference_case(dev):
+    # tests/test_gguf_and_q4.py:115-148 (seed 99, abs < 1e-3).
+    _ref_matmul_case(dev, O.GGML_Q4_0, 99, [(1, 4096, 4096), (16, 2048, 2048)], None, 1e-3)
+
+
+def test_matmul_q8_0_reference_case(dev):
+    # tests/test_phase5_scale.py:42-69 (seed 501, x 0.2, abs < 1e-2).
+    _ref_matmul_case(dev, O.GGML_Q8_0, 501, [(1, 512, 1024), (8, 256, 512)], 0.2, 1e-2)
+
+
+def test_matmul_q4_k_reference_case(dev):
+    # tests/test_phase5_scale.py:72-102 (seed 502, x 0.1, abs < 2e-2, incl. K = 8192).
+    _ref_matmul_case(dev, O.GGML_Q4_K, 502, [(1, 256, 512), (8, 256, 512), (1, 1024, 8192)], 0.1, 2e-2)
+
+
+def test_matmul_q6_k_reference_case(dev):
+    # tests/test_phase5_scale.py:358-369 (seed 611, N=64, K=512, M in {1,4,7}, abs < 5e-2).
+    _ref_matmul_case(dev, O.GGML_Q6_K, 611, [(1, 64, 512), (4, 64, 512), (7, 64, 512)], 0.2, 5e-2)
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_prefill_tile_equals_m1_reference_case(dev, t):
+    # tests/test_phase5_scale.py:274-310 / 371-379: M in {4, 7, 16} bit-identical to M = 1 calls.
+    import matmul_module
+    fn = getattr(matmul_module, f"matmul_{O.TYPE_NAMES[t]}")
+    rng = np.random.default_rng(601)
+    N, K = (128, 256) if t != O.GGML_Q6_K else (64, 512)
+    w = O.QUANTIZE[t](rng.standard_normal((N, K), dtype=np.float32) * 0.2)
+    for M in (4, 7, 16):
+        A = (rng.standard_normal((M, K), dtype=np.float32) * 0.2).astype(np.float16)
+        c_all = np.empty((M, N), dtype=np.float16)
+        fn(A, w, c_all, M, N, K)
+        c_one = np.empty((M, N), dtype=np.float16)
+        for m in range(M):
+            row = np.empty((1, N), dtype=np.float16)
+            fn(np.ascontiguousarray(A[m:m + 1]), w, row, 1, N, K)
+            c_one[m] = row[0]
+        np.testing.assert_array_equal(c_all.view(np.uint16), c_one.view(np.uint16))
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_device_launchers_fp16(dev, t):
+    import torch
+    import qmm
+    rng = np.random.default_rng(5 + t)
+    N, K = 256, 4096
+    raw = O.synth_weights(t, N, K, rng)
+    A = rng.standard_normal((3, K)).astype(np.float16)
+    C = torch.empty((3, N), dtype=torch.float16, device=dev)
+    getattr(qmm, f"matmul_{O.TYPE_NAMES[t]}_device")(to_dev(A, dev), to_dev(raw, dev), C, 3, N, K)
+    torch.cuda.synchronize()
+    y = C.float().cpu().numpy().astype(np.float64)
+    assert O.max_rel_err(y, O.matmul_f64(t, A.astype(np.float32), raw, N, K)) <= GEMV_TOL
+
+
+def test_empty_and_invalid_on_device(dev):
+    import torch
+    import qmm
+    A = torch.zeros((0, 256), device=dev)
+    W = torch.zeros(144 * 4, dtype=torch.uint8, device=dev)
+    C = qmm.gemm(O.GGML_Q4_K, A, W, 4, 256)
+    assert C.shape == (0, 4)
+    with pytest.raises(ValueError):
+        qmm.gemm(O.GGML_Q4_K, torch.zeros((1, 200), device=dev), W, 4, 200)
+
+
+# ------------------------------------------------------------------ full-size shapes
+
+FULL_SHAPES = [
+    ("8b_q8_0_gate", O.GGML_Q8_0, 14336, 4096),
+    ("8b_q4_k_q", O.GGML_Q4_K, 4096, 4096),
+    ("8b_q6_k_down", O.GGML_Q6_K, 4096, 14336),
+    ("8b_q6_k_lm_head", O.GGML_Q6_K, 128256, 4096),
+    ("70b_q4_k_gate", O.GGML_Q4_K, 28672, 8192),
+    ("70b_q4_k_kv", O.GGML_Q4_K, 1024, 8192),
+    ("70b_q6_k_down", O.GGML_Q6_K, 8192, 28672),
+    ("4k_q4_0", O.GGML_Q4_0, 4096, 4096),
+]
+
+
+@pytest.mark.parametrize("name,t,N,K", FULL_SHAPES)
+@pytest.mark.parametrize("M", [1, 4])
+def test_full_size_sampled_rows_and_linearity(dev, name, t, N, K, M):
+    import torch
+    import qmm
+    rng = np.random.default_rng(zlib.crc32(name.encode()) + M)
+    raw = O.synth_weights(t, N, K, rng)
+    W = to_dev(raw, dev)
+    x1 = rng.standard_normal((M, K)).astype(np.float32)
+    x2 = rng.standard_normal((M, K)).astype(np.float32)
+    y1 = qmm.gemm(t, to_dev(x1, dev), W, N, K)
+    y2 = qmm.gemm(t, to_dev(x2, dev), W, N, K)
+    y3 = qmm.gemm(t, to_dev((2.0 * x1 - 0.5 * x2).astype(np.float32), dev), W, N, K)
+    torch.cuda.synchronize()
+    y1, y2, y3 = (v.cpu().numpy().astype(np.float64) for v in (y1, y2, y3))
+    # sampled rows against the fp64 oracle (row bytes are contiguous in the packed matrix)
+    rows = np.sort(rng.choice(N, size=48, replace=False))
+    rb = O.weight_bytes(t, 1, K)
+    sub = np.concatenate([raw[r * rb:(r + 1) * rb] for r in rows])
+    y64 = O.matmul_f64(t, x1, sub, rows.size, K)
+    assert O.max_rel_err(y1[:, rows], y64) <= GEMV_TOL
+    # linearity in x, to fp32 accumulation accuracy
+    lin = 2.0 * y1 - 0.5 * y2
+    assert np.max(np.abs(y3 - lin)) <= 1e-4 * np.max(np.abs(lin))
+    assert np.all(np.isfinite(y1))
