@@ -27,8 +27,8 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
         for (int i = 0; i < 16; ++i) {
             uint32_t lo, hi;
             if constexpr (OUT == QMM_DTYPE_F16) {
-                lo = __half_as_ushort(__float2half_rn(w[2 * i]));
-                hi = __half_as_ushort(__float2half_rn(w[2 * i + 1]));
+                lo = float_to_half_bits(w[2 * i]);
+                hi = float_to_half_bits(w[2 * i + 1]);
             } else {
                 lo = float_to_bf16_bits(w[2 * i]);
                 hi = float_to_bf16_bits(w[2 * i + 1]);

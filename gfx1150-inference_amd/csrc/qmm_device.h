@@ -17,6 +17,14 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
     return v;
 }
 
+// fp32 -> fp16 bits, round to nearest even, signed zeros and subnormals kept.  The value is
+// hidden from the optimiser first: otherwise fp16(a * b) is folded into
+// v_fma_mixlo_f16(a, b, +0), which turns a -0 product into +0.
+__device__ __forceinline__ uint16_t float_to_half_bits(float f) {
+    __asm__("" : "+v"(f));
+    return __half_as_ushort(__float2half_rn(f));
+}
+
 // Byte `i` (0..3) of a dword as an exact float (v_cvt_f32_ubyte{0..3}).
 __device__ __forceinline__ float ubyte_to_float(uint32_t v, int i) {
     return static_cast<float>((v >> (8 * i)) & 0xFFu);

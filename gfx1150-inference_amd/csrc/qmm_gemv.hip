@@ -135,11 +135,14 @@ struct FmtQ6K {
         s.q[5] = ((a1 >> 4) & 0x0F0F0F0Fu) | (h1 & 0x30303030u);
         s.q[6] = ((b0 >> 4) & 0x0F0F0F0Fu) | ((h0 >> 2) & 0x30303030u);
         s.q[7] = ((b1 >> 4) & 0x0F0F0F0Fu) | ((h1 >> 2) & 0x30303030u);
+        // Signed sub-scales through int8_t casts: __builtin_amdgcn_sbfe with a lane-variable
+        // offset was lowered with an unsigned int->float conversion, turning negative
+        // scales into ~4e9.
         const int is8 = 8 * (qq >> 1);
-        const float sc0 = static_cast<float>(__builtin_amdgcn_sbfe(static_cast<int>(s0), is8, 8));
-        const float sc1 = static_cast<float>(__builtin_amdgcn_sbfe(static_cast<int>(s0), is8 + 16, 8));
-        const float sc2 = static_cast<float>(__builtin_amdgcn_sbfe(static_cast<int>(s1), is8, 8));
-        const float sc3 = static_cast<float>(__builtin_amdgcn_sbfe(static_cast<int>(s1), is8 + 16, 8));
+        const float sc0 = static_cast<float>(static_cast<int8_t>(s0 >> is8));
+        const float sc1 = static_cast<float>(static_cast<int8_t>(s0 >> (is8 + 16)));
+        const float sc2 = static_cast<float>(static_cast<int8_t>(s1 >> is8));
+        const float sc3 = static_cast<float>(static_cast<int8_t>(s1 >> (is8 + 16)));
         s.a[0] = d * sc0; s.a[1] = d * sc1; s.a[2] = d * sc2; s.a[3] = d * sc3;
 #pragma unroll
         for (int g = 0; g < 4; ++g) s.b[g] = 32.0f * s.a[g];  // codes enter unsigned (q + 32)
@@ -265,7 +268,9 @@ __device__ __forceinline__ void store_out(TC* p, float v);
 template <>
 __device__ __forceinline__ void store_out<float>(float* p, float v) { *p = v; }
 template <>
-__device__ __forceinline__ void store_out<__half>(__half* p, float v) { *p = __float2half(v); }
+__device__ __forceinline__ void store_out<__half>(__half* p, float v) {
+    *reinterpret_cast<uint16_t*>(p) = float_to_half_bits(v);
+}
 
 template <class F, int MR, int YT, typename TA, typename TC>
 __global__ __launch_bounds__(kWave * kWavesPerBlock)
