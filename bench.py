@@ -193,6 +193,41 @@ def run_workload(torch, qmm, hip, wl, steps, warmup, time_dominant=False):
     return total_ms / steps, wall, dom_ms
 
 
+def run_prefill(torch, qmm, hip, gen, dev, steps, warmup):
+    """Llama-3-8B prefill GEMMs at M = 512 fp32 activations: gate and up (Q4_K 14336 x 4096) and
+    down (Q6_K 4096 x 14336), each on the bf16-MFMA path; TFLOP/s = 2*M*N*K / kernel time."""
+    M = 512
+    stream = torch.cuda.current_stream().cuda_stream
+    res = {}
+    for name, t, n, k in (("gate_q4_k_14336x4096", Q4_K, 14336, 4096), ("up_q4_k_14336x4096", Q4_K, 14336, 4096),
+                          ("down_q6_k_4096x14336", Q6_K, 4096, 14336)):
+        w = make_weight(torch, t, n, k, gen, dev)
+        x = torch.randn((M, k), device=dev, generator=gen)
+        c = torch.empty((M, n), device=dev)
+
+        def launch():
+            qmm.check(qmm.lib().qmm_gemm(t, x.data_ptr(), qmm.DTYPE_F32, w.data_ptr(), c.data_ptr(), qmm.DTYPE_F32,
+                                         M, n, k, stream))
+
+        for _ in range(warmup):
+            launch()
+        torch.cuda.synchronize()
+        a, b = hip.event(), hip.event()
+        hip.record(a, stream)
+        for _ in range(steps):
+            launch()
+        hip.record(b, stream)
+        torch.cuda.synchronize()
+        us = hip.elapsed_ms(a, b) * 1e3 / steps
+        hip.destroy(a)
+        hip.destroy(b)
+        tf = 2.0 * M * n * k / (us * 1e-6) / 1e12
+        res[name] = {"us": round(us, 2), "TFLOP/s": round(tf, 1), "frac_bf16_peak": round(tf / BF16_DENSE_PEAK_TFLOPS, 4)}
+        log(f"prefill M=512 {name}: {us:.1f} us, {tf:.1f} TFLOP/s ({tf / BF16_DENSE_PEAK_TFLOPS * 100:.1f}% of bf16 peak)")
+        del w, x, c
+    return res
+
+
 def cpu_baseline_70b(rows_fraction=0.25, seed=0):
     """NumPy restatement of the reference CPU path (dequantize -> fp16 -> fp32 matmul) on the
     first quarter of the rows of each of the 7 matrices of one 70B layer, M = 1."""
@@ -312,6 +347,8 @@ def main():
             w8.free()
             del w8
             torch.cuda.empty_cache()
+        extra["8b_prefill_m512"] = run_prefill(torch, qmm, hip, gen, dev, max(3, args.steps // 2), 2)
+        torch.cuda.empty_cache()
         lm = Workload(torch, qmm, "lm_head", [[("lm_head", Q6_K, 128256, 4096, "h")]], 4, 1, dev, gen)
         msl, _, _ = run_workload(torch, qmm, hip, lm, args.steps, args.warmup)
         g = lm.algo_bytes / (msl * 1e-3) / 1e9

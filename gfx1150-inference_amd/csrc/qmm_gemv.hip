@@ -272,21 +272,44 @@ __device__ __forceinline__ void store_out<__half>(__half* p, float v) {
     *reinterpret_cast<uint16_t*>(p) = float_to_half_bits(v);
 }
 
-template <class F, int MR, int YT, typename TA, typename TC>
+// Weight bytes of one window for the YT rows of a wave, as loaded by one lane.
+template <class F, int YT>
+struct WinBuf {
+    static constexpr int kRaw = F::kStaged ? F::kLoads : 2;
+    u32x4 raw[YT][kRaw];
+};
+
+// Activations of one window for one lane: 4 runs of 8 consecutive k per A row.
+template <int MR>
+struct XBuf {
+    float x[MR][32];
+};
+
+// One wave computes YT consecutive output rows over a K-slice; KS waves of a workgroup
+// split the windows of the same rows round-robin (window w goes to wave w % KS) and their
+// partial sums are added through LDS in wave order.  Window w + KS's weight bytes (and, for
+// one A row, its activations) are loaded while window w is being multiplied.
+template <class F, int MR, int YT, int KS, typename TA, typename TC>
 __global__ __launch_bounds__(kWave * kWavesPerBlock)
 void gemv_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W, TC* __restrict__ C,
                  int M, int N, int K, int a_vec) {
     constexpr int G = F::kGroups;
     constexpr int RPG = 4 / G;  // runs per group
     constexpr int kPieces = F::kWindowBytes / 16;
-    constexpr int kRaw = F::kStaged ? F::kLoads : 2;
+    constexpr int kRaw = WinBuf<F, YT>::kRaw;
     constexpr int kLdsWords = F::kStaged ? ((F::kWindowBytes + 16 + 15) / 16) * 4 : 4;
+    constexpr int kRowGroups = kWavesPerBlock / KS;
+    constexpr bool kPrefetchX = MR == 1;
+    static_assert(kWavesPerBlock % KS == 0, "KS must divide the waves of a block");
     __shared__ __align__(16) uint32_t lds_all[kWavesPerBlock][kLdsWords];
+    __shared__ float red[KS > 1 ? kWavesPerBlock : 1][MR * YT];
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = threadIdx.x / kWave;
-    const int row0 = (blockIdx.x * kWavesPerBlock + wv) * YT;
-    if (row0 >= N) return;  // wave-uniform
+    const int rg = wv / KS;
+    const int ks = wv - rg * KS;
+    const int row0 = (blockIdx.x * kRowGroups + rg) * YT;
+    const bool active = row0 < N;  // wave-uniform; idle waves still join the K-split reduction
     const int m0 = blockIdx.y * MR;
     const int mrows = min(MR, M - m0);
     const uint32_t row_bytes = static_cast<uint32_t>(K / F::kQK) * F::kBlockBytes;
@@ -320,16 +343,34 @@ void gemv_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W, TC* __
 #pragma unroll
         for (int y = 0; y < YT; ++y) acc[m][y] = 0.0f;
 
-    auto window = [&](int w, auto tail_tag) {
+    auto load_x = [&](XBuf<MR>& xb, int w, auto tail_tag) {
+        constexpr bool kTail = decltype(tail_tag)::value;
+        const int k0 = w * kWindow;
+        const bool lv = kTail ? F::lane_valid(lane, k0, K) : true;
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int o = kTail ? (lv ? off[r] : 0) : off[r];
+                load_run8<TA>(xrow[m] + k0 + o, vec, &xb.x[m][8 * r]);
+                if constexpr (kTail) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) xb.x[m][8 * r + i] = lv ? xb.x[m][8 * r + i] : 0.0f;
+                }
+            }
+        }
+    };
+
+    // Issues the loads of window w: the weight bytes of the YT rows, then the activations.
+    auto load = [&](WinBuf<F, YT>& b, XBuf<MR>& xb, int w, auto tail_tag) {
         constexpr bool kTail = decltype(tail_tag)::value;
         const int k0 = w * kWindow;
         const uint32_t wb = static_cast<uint32_t>(w) * F::kWindowBytes;
-        bool lv = true;
         uint32_t lo[kRaw];
 #pragma unroll
         for (int j = 0; j < kRaw; ++j) lo[j] = loff[j];
         if constexpr (kTail) {
-            lv = F::lane_valid(lane, k0, K);
+            const bool lv = F::lane_valid(lane, k0, K);
             const int valid_pieces = static_cast<int>((K - k0) / F::kQK) * F::kBlockBytes / 16;
 #pragma unroll
             for (int j = 0; j < kRaw; ++j) {
@@ -337,37 +378,31 @@ void gemv_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W, TC* __
                 else lo[j] = lv ? loff[j] : (j == 0 ? 0u : 16u);
             }
         }
-
-        // Weight bytes of the YT rows first (longest latency), then activations.
-        u32x4 raw[YT][kRaw];
 #pragma unroll
         for (int y = 0; y < YT; ++y)
 #pragma unroll
             for (int j = 0; j < kRaw; ++j)
-                raw[y][j] = *reinterpret_cast<const u32x4*>(W + (rowoff[y] + wb + lo[j]));
+                b.raw[y][j] = *reinterpret_cast<const u32x4*>(W + (rowoff[y] + wb + lo[j]));
+        if constexpr (kPrefetchX) load_x(xb, w, tail_tag);
+    };
 
-        float x[MR][32];
+    auto compute = [&](const WinBuf<F, YT>& b, const XBuf<MR>& xpre, int w, auto tail_tag) {
+        constexpr bool kTail = decltype(tail_tag)::value;
+        const bool lv = kTail ? F::lane_valid(lane, w * kWindow, K) : true;
+        XBuf<MR> xl;
+        if constexpr (!kPrefetchX) load_x(xl, w, tail_tag);
+        const XBuf<MR>& xb = kPrefetchX ? xpre : xl;
         float sx[MR][G];
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int o = kTail ? (lv ? off[r] : 0) : off[r];
-                load_run8<TA>(xrow[m] + k0 + o, vec, &x[m][8 * r]);
-                if constexpr (kTail) {
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) x[m][8 * r + i] = lv ? x[m][8 * r + i] : 0.0f;
-                }
-            }
-#pragma unroll
             for (int g = 0; g < G; ++g) {
-                float t = x[m][8 * RPG * g];
+                float t = xb.x[m][8 * RPG * g];
 #pragma unroll
-                for (int i = 1; i < 8 * RPG; ++i) t += x[m][8 * RPG * g + i];
+                for (int i = 1; i < 8 * RPG; ++i) t += xb.x[m][8 * RPG * g + i];
                 sx[m][g] = t;
             }
         }
-
 #pragma unroll
         for (int y = 0; y < YT; ++y) {
             Slot<G> s;
@@ -375,11 +410,11 @@ void gemv_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W, TC* __
                 wave_lds_sync();
 #pragma unroll
                 for (int j = 0; j < kRaw; ++j)
-                    reinterpret_cast<u32x4*>(lds32)[min(lane + kWave * j, kPieces - 1)] = raw[y][j];
+                    reinterpret_cast<u32x4*>(lds32)[min(lane + kWave * j, kPieces - 1)] = b.raw[y][j];
                 wave_lds_sync();
                 s = F::decode(lds32, lane);
             } else {
-                s = F::decode(raw[y], lane);
+                s = F::decode(b.raw[y], lane);
             }
             if constexpr (kTail) {
 #pragma unroll
@@ -398,7 +433,7 @@ void gemv_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W, TC* __
                 for (int g = 0; g < G; ++g) {
                     float t = 0.0f;
 #pragma unroll
-                    for (int i = 0; i < 8 * RPG; ++i) t = __fmaf_rn(x[m][8 * RPG * g + i], c[8 * RPG * g + i], t);
+                    for (int i = 0; i < 8 * RPG; ++i) t = __fmaf_rn(xb.x[m][8 * RPG * g + i], c[8 * RPG * g + i], t);
                     a = __fmaf_rn(s.a[g], t, a);
                     a = __fmaf_rn(-s.b[g], sx[m][g], a);
                 }
@@ -408,16 +443,63 @@ void gemv_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W, TC* __
     };
 
     const int nfull = K / kWindow;
-    for (int w = 0; w < nfull; ++w) window(w, std::false_type{});
-    if (K % kWindow != 0) window(nfull, std::true_type{});
+    if (active) {
+        int w = ks;
+        if (w < nfull) {
+            WinBuf<F, YT> b0, b1;
+            XBuf<MR> x0, x1;
+            load(b0, x0, w, std::false_type{});
+            while (true) {
+                if (w + KS < nfull) load(b1, x1, w + KS, std::false_type{});
+                compute(b0, x0, w, std::false_type{});
+                w += KS;
+                if (w >= nfull) break;
+                if (w + KS < nfull) load(b0, x0, w + KS, std::false_type{});
+                compute(b1, x1, w, std::false_type{});
+                w += KS;
+                if (w >= nfull) break;
+            }
+        }
+        if (K % kWindow != 0 && nfull % KS == ks) {
+            WinBuf<F, YT> bt;
+            XBuf<MR> xt;
+            load(bt, xt, nfull, std::true_type{});
+            compute(bt, xt, nfull, std::true_type{});
+        }
+    }
 
+    float v[MR][YT];
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {
+    for (int m = 0; m < MR; ++m)
 #pragma unroll
-        for (int y = 0; y < YT; ++y) {
-            const float v = wave_sum_to_lane63(acc[m][y]);
-            if (lane == kWave - 1 && m < mrows && row0 + y < N)
-                store_out<TC>(C + static_cast<size_t>(m0 + m) * N + row0 + y, v);
+        for (int y = 0; y < YT; ++y) v[m][y] = wave_sum_to_lane63(acc[m][y]);
+    if constexpr (KS == 1) {
+        if (active && lane == kWave - 1) {
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+                for (int y = 0; y < YT; ++y)
+                    if (m < mrows && row0 + y < N) store_out<TC>(C + static_cast<size_t>(m0 + m) * N + row0 + y, v[m][y]);
+        }
+    } else {
+        if (lane == kWave - 1) {
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+                for (int y = 0; y < YT; ++y) red[wv][m * YT + y] = v[m][y];
+        }
+        __syncthreads();
+        if (active && ks == 0 && lane == kWave - 1) {
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+#pragma unroll
+                for (int y = 0; y < YT; ++y) {
+                    float t = red[wv][m * YT + y];
+#pragma unroll
+                    for (int j = 1; j < KS; ++j) t += red[wv + j][m * YT + y];
+                    if (m < mrows && row0 + y < N) store_out<TC>(C + static_cast<size_t>(m0 + m) * N + row0 + y, t);
+                }
+            }
         }
     }
 }
@@ -455,12 +537,13 @@ void gemv_fallback_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ 
     if (lane == kWave - 1) store_out<TC>(C + static_cast<size_t>(m) * N + n, acc);
 }
 
-template <class F, int MR, int YT, typename TA, typename TC>
+template <class F, int MR, int YT, int KS, typename TA, typename TC>
 hipError_t launch_fast(const void* A, const void* W, void* C, int M, int N, int K, bool a_vec,
                        hipStream_t stream) {
+    constexpr int kRowsPerBlock = (kWavesPerBlock / KS) * YT;
     const dim3 block(kWave * kWavesPerBlock);
-    const dim3 grid((N + kWavesPerBlock * YT - 1) / (kWavesPerBlock * YT), (M + MR - 1) / MR);
-    hipLaunchKernelGGL((gemv_kernel<F, MR, YT, TA, TC>), grid, block, 0, stream,
+    const dim3 grid((N + kRowsPerBlock - 1) / kRowsPerBlock, (M + MR - 1) / MR);
+    hipLaunchKernelGGL((gemv_kernel<F, MR, YT, KS, TA, TC>), grid, block, 0, stream,
                        static_cast<const TA*>(A), static_cast<const uint8_t*>(W), static_cast<TC*>(C),
                        M, N, K, a_vec ? 1 : 0);
     return hipGetLastError();
@@ -468,7 +551,6 @@ hipError_t launch_fast(const void* A, const void* W, void* C, int M, int N, int 
 
 // Rows per wave: enough waves to cover the chip several times over.
 inline int pick_yt(int N) {
-    if (N >= 8 * 2048) return 8;
     if (N >= 4 * 2048) return 4;
     if (N >= 2 * 2048) return 2;
     return 1;
@@ -480,25 +562,22 @@ hipError_t dispatch_fast(const void* A, const void* W, void* C, int M, int N, in
     const int yt = pick_yt(N);
     if (M == 1) {
         switch (yt) {
-            case 8: return launch_fast<F, 1, 8, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-            case 4: return launch_fast<F, 1, 4, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-            case 2: return launch_fast<F, 1, 2, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-            default: return launch_fast<F, 1, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+            case 4: return launch_fast<F, 1, 4, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+            case 2: return launch_fast<F, 1, 2, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+            default: return launch_fast<F, 1, 1, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
         }
     }
     if (M == 2) {
         switch (yt) {
-            case 8: return launch_fast<F, 2, 4, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-            case 4: return launch_fast<F, 2, 4, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-            case 2: return launch_fast<F, 2, 2, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-            default: return launch_fast<F, 2, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+            case 4: return launch_fast<F, 2, 4, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+            case 2: return launch_fast<F, 2, 2, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+            default: return launch_fast<F, 2, 1, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
         }
     }
     switch (yt) {
-        case 8: return launch_fast<F, 4, 4, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-        case 4: return launch_fast<F, 4, 4, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-        case 2: return launch_fast<F, 4, 2, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-        default: return launch_fast<F, 4, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+        case 4: return launch_fast<F, 4, 4, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+        case 2: return launch_fast<F, 4, 2, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+        default: return launch_fast<F, 4, 1, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
     }
 }
 

@@ -267,6 +267,18 @@ def matmul_f64(ggml_type: int, A: np.ndarray, raw: np.ndarray, N: int, K: int) -
     return np.asarray(A, dtype=np.float64).reshape(-1, K) @ W.T
 
 
+def matmul_bf16_operands(ggml_type: int, A: np.ndarray, raw: np.ndarray, N: int, K: int) -> np.ndarray:
+    """fp64 product of bf16-rounded operands: bf16(A) @ bf16(dequant_f32(W)).T.
+
+    This is the exact value a bf16-MFMA GEMM with fp32 accumulation approximates (only its
+    accumulation rounds), so it pins the prefill kernel's dequantization and k ordering far more
+    tightly than the fp64 tolerance does.
+    """
+    Wb = bf16_bits_to_f32(f32_to_bf16_bits(DEQUANT_F32[ggml_type](raw, N * K))).reshape(N, K)
+    Ab = bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(A, dtype=np.float32).reshape(-1, K)))
+    return Ab.astype(np.float64) @ Wb.astype(np.float64).T
+
+
 def max_rel_err(y: np.ndarray, y64: np.ndarray) -> float:
     """max_i |y_i - y64_i| / max_i |y64_i| (the tolerance metric for GEMV and GEMM)."""
     y = np.asarray(y, dtype=np.float64)

@@ -1,0 +1,116 @@
+"""GPU parity of the bf16-MFMA prefill GEMM (M >= qmm_gemv_max_m) through the C ABI.
+
+Bars (written into each check):
+* max_i|y_i - y64_i| / max_i|y64_i| <= 1e-2 against fp64 on the exact weights (bf16 operands);
+* max_i|y_i - yb_i| / max_i|yb_i| <= 1e-5 against the fp64 product of the bf16-rounded operands
+  (only fp32 accumulation differs), which pins dequantization, scales and the k ordering;
+* edge shapes: M, N not multiples of the 128 x 256 tile, K tails of 32 for Q4_0 / Q8_0,
+  fp16 and fp32 activations and outputs; the Llama-3-8B prefill shapes (M = 512) on sampled rows.
+"""
+
+import zlib
+
+import numpy as np
+import pytest
+
+import gguf_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [O.GGML_Q4_0, O.GGML_Q8_0, O.GGML_Q4_K, O.GGML_Q6_K]
+TOL_F64 = 1e-2
+TOL_BF16 = 1e-5
+
+
+@pytest.fixture(scope="module")
+def dev(cuda):
+    import qmm  # noqa: F401
+    return cuda
+
+
+def to_dev(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def run(t, x, raw, N, K, dev, a16=False, c16=False):
+    import torch
+    import qmm
+    A = to_dev(x.astype(np.float16 if a16 else np.float32), dev)
+    C = qmm.gemm(t, A, to_dev(raw, dev), N, K, out_dtype=torch.float16 if c16 else torch.float32)
+    torch.cuda.synchronize()
+    return C.float().cpu().numpy().astype(np.float64)
+
+
+def shapes(t):
+    if t in (O.GGML_Q4_K, O.GGML_Q6_K):
+        return [(32, 256, 512), (128, 512, 2048), (200, 300, 1024), (129, 257, 256)]
+    return [(32, 256, 512), (128, 512, 2048), (200, 300, 544), (129, 257, 96), (40, 64, 32)]
+
+
+def test_prefill_threshold(dev):
+    import qmm
+    assert qmm.gemv_max_m() == 32
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_prefill_vs_fp64_and_bf16_operands(dev, t):
+    rng = np.random.default_rng(4000 + t)
+    for M, N, K in shapes(t):
+        raw = O.synth_weights(t, N, K, rng)
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        y = run(t, x, raw, N, K, dev)
+        assert O.max_rel_err(y, O.matmul_f64(t, x, raw, N, K)) <= TOL_F64, (O.TYPE_NAMES[t], M, N, K)
+        assert O.max_rel_err(y, O.matmul_bf16_operands(t, x, raw, N, K)) <= TOL_BF16, (O.TYPE_NAMES[t], M, N, K)
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("a16,c16", [(True, True), (True, False), (False, True)])
+def test_prefill_dtypes(dev, t, a16, c16):
+    rng = np.random.default_rng(4100 + t)
+    M, N, K = 96, 320, 1024
+    raw = O.synth_weights(t, N, K, rng)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    xa = x.astype(np.float16).astype(np.float32) if a16 else x
+    y = run(t, x, raw, N, K, dev, a16=a16, c16=c16)
+    tol_b = 1e-3 if c16 else TOL_BF16  # fp16 output rounding: 2^-11 relative
+    assert O.max_rel_err(y, O.matmul_f64(t, xa, raw, N, K)) <= TOL_F64
+    assert O.max_rel_err(y, O.matmul_bf16_operands(t, xa, raw, N, K)) <= tol_b
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_prefill_reference_quantizer_inputs(dev, t):
+    # Inputs built like the reference's own tests (quantize_*_cpu of N(0,1)-scaled weights),
+    # at a prefill-sized M.
+    rng = np.random.default_rng(4200 + t)
+    M, N, K = 64, 256, 1024
+    A = (rng.standard_normal((M, K), dtype=np.float32) * 0.2).astype(np.float16)
+    B = O.QUANTIZE[t](rng.standard_normal((N, K), dtype=np.float32) * 0.2)
+    y = run(t, A.astype(np.float32), B, N, K, dev, a16=True, c16=True)
+    assert O.max_rel_err(y, O.matmul_f64(t, A.astype(np.float32), B, N, K)) <= TOL_F64
+
+
+PREFILL_FULL = [
+    ("8b_q4_k_gate", O.GGML_Q4_K, 14336, 4096),
+    ("8b_q6_k_down", O.GGML_Q6_K, 4096, 14336),
+    ("8b_q8_0_up", O.GGML_Q8_0, 14336, 4096),
+]
+
+
+@pytest.mark.parametrize("name,t,N,K", PREFILL_FULL)
+def test_prefill_full_size_m512(dev, name, t, N, K):
+    import torch
+    import qmm
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    M = 512
+    raw = O.synth_weights(t, N, K, rng)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    y = qmm.gemm(t, to_dev(x, dev), to_dev(raw, dev), N, K)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy().astype(np.float64)
+    assert np.all(np.isfinite(y))
+    rows = np.sort(rng.choice(N, size=32, replace=False))
+    rb = O.weight_bytes(t, 1, K)
+    sub = np.concatenate([raw[r * rb:(r + 1) * rb] for r in rows])
+    assert O.max_rel_err(y[:, rows], O.matmul_f64(t, x, sub, rows.size, K)) <= TOL_F64
+    assert O.max_rel_err(y[:, rows], O.matmul_bf16_operands(t, x, sub, rows.size, K)) <= TOL_BF16
