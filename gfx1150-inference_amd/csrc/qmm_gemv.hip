@@ -2,266 +2,443 @@
 //
 // MI355X design (replaces the reference's wave32 one-output-per-wave kernels,
 // src/kernels/dequantize.hip:97-148, 152-210, 232-332, 377-505, 549-685):
-//   * A wave owns YT consecutive weight rows and walks K in windows of 2048 weights.
-//     In every window each of the 64 lanes owns a fixed 32-weight slot (four runs of
-//     8 contiguous k), so one wave-wide 16-byte load per row covers a contiguous,
-//     16-byte-aligned stretch of the packed row (coalesced HBM streaming).
-//   * The lane's 32 activations (per A row) are loaded once per window and reused for
-//     all YT rows; per-run sums of x are hoisted so block offsets/mins cost one FMA.
-//   * Q4_K rows are read straight from HBM (144-byte super-blocks are 16-byte aligned);
-//     Q6_K / Q8_0 / Q4_0 windows (1680 / 2176 / 1152 bytes) are staged through a
-//     wave-private LDS buffer and re-sliced per lane.
-//   * fp32 accumulation with explicit FMAs in a fixed order: the result of row m does not
-//     depend on M, on YT or on the grid, so every M < kGemvMaxM is bit-identical to M=1
-//     (the reference's prefill-vs-M=1 invariant, tests/test_phase5_scale.py:274-310).
-//   * The cross-lane reduction is a fixed DPP sequence (no atomics; deterministic).
+//   * K is walked in windows of 4096 weights.  In every window each of the 64 lanes of a wave
+//     owns a fixed 64-weight slot of the packed row (a Q4_K 32-byte qs chunk, a Q6_K
+//     (half, 16-column) slice, two Q8_0 / Q4_0 blocks) and streams it with 16-byte loads.
+//   * A workgroup of NW waves owns NW * YT consecutive weight rows.  The window's activations
+//     are staged once per workgroup into LDS as fp16 pairs, already in each lane's slot order,
+//     together with per-16-k sums of the same fp16 values; the next window is staged and the
+//     next window's weight bytes are loaded while the current window is multiplied.
+//   * Codes are never converted one by one: a single v_and_or_b32 / v_perm_b32 turns two codes
+//     q into the fp16 pair (1024 + q) (0x6400 | q), and v_dot2_f32_f16 multiplies two of them by
+//     two activations and accumulates in fp32.  Per group g of the slot,
+//         sum_k x_k * w_k = a_g * S_g - B_g * sx_g,   S_g = sum_k x_k * (1024 + q_k),
+//     where sx_g is the sum of the group's fp16 activations and B_g folds the 1024 offset, the
+//     format's code offset and the Q4_K min.  All products are exact; only fp32 sums round.
+//   * fp32 activations are rounded to fp16 once, when staged (|x| must stay below 65504).
+//   * The arithmetic of row (m, n) is the same instruction sequence for every M, YT and grid,
+//     so every M < kGemvMaxM is bit-identical to M = 1 (the reference's prefill-vs-M=1
+//     invariant, tests/test_phase5_scale.py:274-310); the cross-lane reduction is a fixed DPP
+//     sequence (no atomics, deterministic).
+#include <mutex>
+#include <string>
 #include <type_traits>
+#include <unordered_map>
 
 #include "qmm_device.h"
 
 namespace qmm {
 namespace {
 
-constexpr int kWavesPerBlock = 4;
-
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
 
-// Decoded 32-weight slot of one row: code bytes (run r uses q[2r], q[2r+1]) and per-group
-// scale a / offset b; contribution = sum_g a[g] * (sum_{runs in g} x*code) - b[g] * sum x.
-template <int G>
-struct Slot {
-    uint32_t q[8];
-    float a[G];
-    float b[G];
+constexpr int kGemvWindow = 4096;   // weights per row per window (64 lanes x 64)
+constexpr int kChunks = 8;          // 8-weight activation chunks per lane slot
+
+// Tuning: minimum waves per SIMD the register allocator must allow (0 = unconstrained), and
+// the rows per wave of the M = 1 and M = 2 kernels for large N.
+#ifndef QMM_GEMV_MIN_WAVES
+#define QMM_GEMV_MIN_WAVES 0
+#endif
+#ifndef QMM_GEMV_YT_BIG
+#define QMM_GEMV_YT_BIG 1
+#endif
+#ifndef QMM_GEMV_NW
+#define QMM_GEMV_NW 8
+#endif
+
+// Register-resident constants (v_and_or_b32 on gfx9 takes no literal operands).
+struct Consts {
+    uint32_t mg;   // 0x64006400: fp16 pair (1024, 1024)
+    uint32_t m0f;  // 0x000F000F
+    uint32_t mf0;  // 0x00F000F0
+    uint32_t m3f;  // 0x003F003F
+    uint32_t m3f0; // 0x03F003F0
+    uint32_t mff;  // 0x00FF00FF
 };
 
-// ------------------------------------------------------------------------------------
-// Q4_K: 8 super-blocks per window, lane = (sb = lane/8, piece p = lane%8 of the 128 qs bytes).
-// ------------------------------------------------------------------------------------
-struct FmtQ4K {
+__device__ __forceinline__ uint32_t keep_v(uint32_t v) {
+    __asm__("" : "+v"(v));
+    return v;
+}
+__device__ __forceinline__ uint32_t keep_s(uint32_t v) {
+    __asm__("" : "+s"(v));
+    return v;
+}
+
+__device__ __forceinline__ Consts make_consts() {
+    Consts c;
+    c.mg = keep_v(0x64006400u);
+    c.m0f = keep_s(0x000F000Fu);
+    c.mf0 = keep_s(0x00F000F0u);
+    c.m3f = keep_s(0x003F003Fu);
+    c.m3f0 = keep_s(0x03F003F0u);
+    c.mff = keep_s(0x00FF00FFu);
+    return c;
+}
+
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t orv) { return (v & mask) | orv; }
+
+__device__ __forceinline__ float dot2(uint32_t x, uint32_t c, float acc) {
+    h16x2 a, b;
+    __builtin_memcpy(&a, &x, 4);
+    __builtin_memcpy(&b, &c, 4);
+    return __builtin_amdgcn_fdot2(a, b, acc, false);
+}
+
+__device__ __forceinline__ u32x4 ldg16(const uint8_t* p) {
+    u32x4 v;
+    __builtin_memcpy(&v, p, 16);  // any alignment: global_load_dwordx4
+    return v;
+}
+__device__ __forceinline__ uint32_t ldg_u16(const uint8_t* p) {
+    uint16_t v;
+    __builtin_memcpy(&v, p, 2);
+    return v;
+}
+
+// ------------------------------------------------------------------------------------------
+// Formats.  Each defines the lane slot of a 4096-weight window:
+//   xk(lane, cj): first k (relative to the window) of activation chunk cj (8 consecutive k);
+//   load(): the slot's packed bytes of one row (addresses clamped to valid bytes);
+//   chunk_codes(): the 4 fp16 code pairs of chunk cj, matching activation pairs
+//                  (k0,k2), (k1,k3), (k4,k6), (k5,k7) of the chunk;
+//   group_scales(): per group g (chunks 8g/G .. 8(g+1)/G - 1), a_g and B_g.
+// ------------------------------------------------------------------------------------------
+
+// Q4_K: lane = (super-block sb = lane/4, qs chunk c = lane%4): 64 weights, k = 64*lane + 0..63.
+// Groups: g0 = sub-block 2c (low nibbles, chunks 0-3), g1 = sub-block 2c+1 (high nibbles, 4-7).
+struct GQ4K {
     static constexpr int kType = QMM_TYPE_Q4_K;
     static constexpr int kQK = kQK_K;
     static constexpr int kBlockBytes = kBytesQ4_K;
-    static constexpr int kWindowBytes = 8 * kBytesQ4_K;
-    static constexpr bool kStaged = false;
-    static constexpr int kGroups = 2;  // runs {0,1} lo nibbles, {2,3} hi nibbles
-    static constexpr int kLoads = 2;   // header + 16 qs bytes
-
-    __device__ static void runs(int lane, int off[4]) {
-        const int sb = lane >> 3, p = lane & 7;
-        const int base = 256 * sb + 64 * (p >> 1) + 16 * (p & 1);
-        off[0] = base; off[1] = base + 8; off[2] = base + 32; off[3] = base + 40;
+    static constexpr int kWinBytes = 16 * kBytesQ4_K;  // 2304
+    static constexpr int kG = 2;
+    static constexpr bool kAligned = true;
+    struct Raw {
+        u32x4 h, q0, q1;
+    };
+    __device__ static int xk(int lane, int cj) { return 64 * lane + 8 * cj; }
+    // Only whole super-blocks exist (K % 256 == 0): a lane is valid or not as a whole.
+    __device__ static bool group_valid(int lane, int, int kwin_valid) { return 64 * lane < kwin_valid; }
+    __device__ static Raw load(const uint8_t* win, int lane, int kwin_valid) {
+        const int sb = lane >> 2, c = lane & 3;
+        const bool v = 64 * lane < kwin_valid;
+        const uint8_t* p = win + (v ? sb * kBytesQ4_K : 0);
+        const int qo = v ? 16 + 32 * c : 16;
+        Raw r;
+        r.h = *reinterpret_cast<const u32x4*>(p);
+        r.q0 = *reinterpret_cast<const u32x4*>(p + qo);
+        r.q1 = *reinterpret_cast<const u32x4*>(p + qo + 16);
+        return r;
     }
-    __device__ static bool lane_valid(int lane, int k0, int K) { return k0 + 256 * (lane >> 3) < K; }
-
-    // Loads: raw[0] = 16-byte header of the lane's super-block, raw[1] = its qs bytes 16p..16p+15.
-
-    // Every lane decodes (scale, min) of sub-block j = p; lanes p, p^1 share chunk p/2 and
-    // pick sub-blocks 2c (= p&~1) and 2c+1 (= p|1) from their quad with DPP.
-    __device__ static Slot<2> decode(const u32x4 raw[2], int lane) {
-        const u32x4 h = raw[0];
-        const u32x4 v = raw[1];
-        const int p = lane & 7;
-        const int s8 = 8 * (p & 3);
-        const uint32_t sc_lo = (h.y >> s8) & 63u;
-        const uint32_t m_lo = (h.z >> s8) & 63u;
-        const uint32_t sc_hi = ((h.w >> s8) & 15u) | (((h.y >> (s8 + 6)) & 3u) << 4);
-        const uint32_t m_hi = ((h.w >> (s8 + 4)) & 15u) | (((h.z >> (s8 + 6)) & 3u) << 4);
-        const uint32_t sc = p < 4 ? sc_lo : sc_hi;
-        const uint32_t m = p < 4 ? m_lo : m_hi;
-        const float d = half_bits_to_float(h.x);
-        const float dmin = half_bits_to_float(h.x >> 16);
-        const float scale = d * static_cast<float>(sc);
-        const float mn = dmin * static_cast<float>(m);
-        Slot<2> s;
-        s.a[0] = dpp_quad(scale, 0xA0);
-        s.a[1] = dpp_quad(scale, 0xF5) * 0.0625f;  // hi nibbles enter as 16*q
-        s.b[0] = dpp_quad(mn, 0xA0);
-        s.b[1] = dpp_quad(mn, 0xF5);
-        s.q[0] = v.x & 0x0F0F0F0Fu; s.q[1] = v.y & 0x0F0F0F0Fu;
-        s.q[2] = v.z & 0x0F0F0F0Fu; s.q[3] = v.w & 0x0F0F0F0Fu;
-        s.q[4] = v.x & 0xF0F0F0F0u; s.q[5] = v.y & 0xF0F0F0F0u;
-        s.q[6] = v.z & 0xF0F0F0F0u; s.q[7] = v.w & 0xF0F0F0F0u;
-        return s;
+    __device__ static void chunk_codes(const Raw& r, int cj, const Consts& K, uint32_t out[4]) {
+        const int j = 2 * (cj & 3);
+        const u32x4& q = j < 4 ? r.q0 : r.q1;
+        const uint32_t dlo = (j & 2) ? q.z : q.x;
+        const uint32_t dhi = (j & 2) ? q.w : q.y;
+        const uint32_t m = cj < 4 ? K.m0f : K.mf0;
+        out[0] = and_or(dlo, m, K.mg);
+        out[1] = and_or(dlo >> 8, m, K.mg);
+        out[2] = and_or(dhi, m, K.mg);
+        out[3] = and_or(dhi >> 8, m, K.mg);
+    }
+    // Sub-block j's (scale, min) (reference get_scale_min_k4, src/kernels/dequantize.hip:52-65).
+    __device__ static void group_scales(const Raw& r, int lane, bool valid, float a[kG], float B[kG]) {
+        const int c = lane & 3;
+        const float d = half_bits_to_float(r.h.x);
+        const float dmin = half_bits_to_float(r.h.x >> 16);
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            // both packings are decoded and selected (no lane-divergent branch)
+            const int sh = 8 * ((2 * c + g) & 3);
+            const uint32_t sc_lo = (r.h.y >> sh) & 63u;
+            const uint32_t mn_lo = (r.h.z >> sh) & 63u;
+            const uint32_t sc_hi = ((r.h.w >> sh) & 15u) | (((r.h.y >> (sh + 6)) & 3u) << 4);
+            const uint32_t mn_hi = ((r.h.w >> (sh + 4)) & 15u) | (((r.h.z >> (sh + 6)) & 3u) << 4);
+            const uint32_t sc = c < 2 ? sc_lo : sc_hi;
+            const uint32_t mn = c < 2 ? mn_lo : mn_hi;
+            const float s = d * static_cast<float>(sc);   // exact (fp16 x 6-bit)
+            const float b = dmin * static_cast<float>(mn);
+            // low nibbles enter as 1024 + q, high nibbles as 1024 + 16q
+            const float ag = g == 0 ? s : s * 0.0625f;
+            a[g] = valid ? ag : 0.0f;
+            B[g] = valid ? __fmaf_rn(1024.0f, ag, b) : 0.0f;
+        }
     }
 };
 
-// Reads the 8 bytes at LDS byte offset o (o even); `odd` says o % 4 == 2.
-__device__ __forceinline__ void lds_read8(const uint32_t* lds32, int o, bool odd, uint32_t& lo, uint32_t& hi) {
-    const int b = (o - (odd ? 2 : 0)) >> 2;
-    const uint32_t d0 = lds32[b], d1 = lds32[b + 1], d2 = lds32[b + 2];
-    lo = odd ? __builtin_amdgcn_alignbyte(d1, d0, 2) : d0;
-    hi = odd ? __builtin_amdgcn_alignbyte(d2, d1, 2) : d1;
-}
-
-// ------------------------------------------------------------------------------------
-// Q6_K: 8 super-blocks (1680 B) per window; lane = (sb = lane/8, half n, quarter qq):
-// 8 values l = 8qq..8qq+7 of each of the four 32-wide groups t of half n.
-// ------------------------------------------------------------------------------------
-struct FmtQ6K {
+// Q6_K: lane = (super-block sb = lane/4, half n = (lane/2)%2, column half h = lane%2): weights
+// l = 16h..16h+15 of the four 32-wide groups t of half n: k = 256sb + 128n + 32t + 16h + (0..15).
+// Groups: t = 0..3 (chunks 2t, 2t+1), one int8 sub-scale each.
+struct GQ6K {
     static constexpr int kType = QMM_TYPE_Q6_K;
     static constexpr int kQK = kQK_K;
     static constexpr int kBlockBytes = kBytesQ6_K;
-    static constexpr int kWindowBytes = 8 * kBytesQ6_K;  // 1680 = 105 x 16
-    static constexpr bool kStaged = true;
-    static constexpr int kGroups = 4;
-    static constexpr int kLoads = (kWindowBytes / 16 + 63) / 64;
-
-    __device__ static void runs(int lane, int off[4]) {
-        const int sb = lane >> 3, n = (lane >> 2) & 1, qq = lane & 3;
-        const int base = 256 * sb + 128 * n + 8 * qq;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) off[t] = base + 32 * t;
+    static constexpr int kWinBytes = 16 * kBytesQ6_K;  // 3360
+    static constexpr int kG = 4;
+    static constexpr bool kAligned = false;
+    struct Raw {
+        u32x4 la, lb, qh;
+        uint32_t s0, s1, d;
+    };
+    __device__ static int xk(int lane, int cj) {
+        const int sb = lane >> 2, n = (lane >> 1) & 1, h = lane & 1;
+        return 256 * sb + 128 * n + 16 * h + 32 * (cj >> 1) + 8 * (cj & 1);
     }
-    __device__ static bool lane_valid(int lane, int k0, int K) { return k0 + 256 * (lane >> 3) < K; }
-
-    __device__ static Slot<4> decode(const uint32_t* lds32, int lane) {
-        const int sb = lane >> 3, n = (lane >> 2) & 1, qq = lane & 3;
-        const int o = 210 * sb;
-        const bool odd = (sb & 1) != 0;
-        uint32_t a0, a1, b0, b1, h0, h1, s0, s1;
-        lds_read8(lds32, o + 64 * n + 8 * qq, odd, a0, a1);
-        lds_read8(lds32, o + 64 * n + 32 + 8 * qq, odd, b0, b1);
-        lds_read8(lds32, o + 128 + 32 * n + 8 * qq, odd, h0, h1);
-        lds_read8(lds32, o + 192 + 8 * n, odd, s0, s1);
-        const uint32_t dw = lds32[(o + 208 - (odd ? 2 : 0)) >> 2];
-        const float d = half_bits_to_float(odd ? (dw >> 16) : dw);
-        Slot<4> s;
-        s.q[0] = (a0 & 0x0F0F0F0Fu) | ((h0 << 4) & 0x30303030u);
-        s.q[1] = (a1 & 0x0F0F0F0Fu) | ((h1 << 4) & 0x30303030u);
-        s.q[2] = (b0 & 0x0F0F0F0Fu) | ((h0 << 2) & 0x30303030u);
-        s.q[3] = (b1 & 0x0F0F0F0Fu) | ((h1 << 2) & 0x30303030u);
-        s.q[4] = ((a0 >> 4) & 0x0F0F0F0Fu) | (h0 & 0x30303030u);
-        s.q[5] = ((a1 >> 4) & 0x0F0F0F0Fu) | (h1 & 0x30303030u);
-        s.q[6] = ((b0 >> 4) & 0x0F0F0F0Fu) | ((h0 >> 2) & 0x30303030u);
-        s.q[7] = ((b1 >> 4) & 0x0F0F0F0Fu) | ((h1 >> 2) & 0x30303030u);
-        // Signed sub-scales through int8_t casts: __builtin_amdgcn_sbfe with a lane-variable
-        // offset was lowered with an unsigned int->float conversion, turning negative
-        // scales into ~4e9.
-        const int is8 = 8 * (qq >> 1);
-        const float sc0 = static_cast<float>(static_cast<int8_t>(s0 >> is8));
-        const float sc1 = static_cast<float>(static_cast<int8_t>(s0 >> (is8 + 16)));
-        const float sc2 = static_cast<float>(static_cast<int8_t>(s1 >> is8));
-        const float sc3 = static_cast<float>(static_cast<int8_t>(s1 >> (is8 + 16)));
-        s.a[0] = d * sc0; s.a[1] = d * sc1; s.a[2] = d * sc2; s.a[3] = d * sc3;
+    __device__ static bool group_valid(int lane, int, int kwin_valid) { return 256 * (lane >> 2) < kwin_valid; }
+    __device__ static Raw load(const uint8_t* win, int lane, int kwin_valid) {
+        const int sb = lane >> 2, n = (lane >> 1) & 1, h = lane & 1;
+        const bool v = 256 * sb < kwin_valid;
+        const uint8_t* p = win + (v ? sb * kBytesQ6_K : 0);
+        Raw r;
+        r.la = ldg16(p + 64 * n + 16 * h);
+        r.lb = ldg16(p + 64 * n + 32 + 16 * h);
+        r.qh = ldg16(p + 128 + 32 * n + 16 * h);
+        uint32_t s[2];
+        __builtin_memcpy(s, p + 192 + 8 * n, 8);
+        r.s0 = s[0];
+        r.s1 = s[1];
+        r.d = ldg_u16(p + 208);
+        return r;
+    }
+    // Chunk cj: group t = cj/2 (q1..q4 of the reference), bytes 8*(cj&1) .. +7 of the slices.
+    __device__ static void chunk_codes(const Raw& r, int cj, const Consts& K, uint32_t out[4]) {
+        const int t = cj >> 1;
+        const bool second = (cj & 1) != 0;
+        const u32x4& ql = (t & 1) ? r.lb : r.la;
+        const uint32_t L[2] = {second ? ql.z : ql.x, second ? ql.w : ql.y};
+        const uint32_t H[2] = {second ? r.qh.z : r.qh.x, second ? r.qh.w : r.qh.y};
 #pragma unroll
-        for (int g = 0; g < 4; ++g) s.b[g] = 32.0f * s.a[g];  // codes enter unsigned (q + 32)
-        return s;
+        for (int i = 0; i < 2; ++i) {
+            // bytes 0,2 then bytes 1,3 of the dword
+#pragma unroll
+            for (int odd = 0; odd < 2; ++odd) {
+                const uint32_t l = odd ? (L[i] >> 8) : L[i];
+                const uint32_t hb = odd ? (H[i] >> 8) : H[i];
+                uint32_t code;
+                if (t < 2) {
+                    // q = (l & 15) | ((qh >> 2t) & 3) << 4, entering as 1024 + q
+                    const uint32_t hs = t == 0 ? (hb << 4) : (hb << 2);
+                    code = and_or((l & 0x000F000Fu) | (hs & ~0x000F000Fu), K.m3f, K.mg);
+                } else {
+                    // q = (l >> 4) | ((qh >> 2t) & 3) << 4, entering as 1024 + 16q
+                    const uint32_t hs = t == 2 ? (hb << 4) : (hb << 2);
+                    code = and_or((l & 0x00F000F0u) | (hs & ~0x00F000F0u), K.m3f0, K.mg);
+                }
+                out[2 * i + odd] = code;
+            }
+        }
+    }
+    __device__ static void group_scales(const Raw& r, int lane, bool valid, float a[kG], float B[kG]) {
+        const int h = lane & 1;
+        const float d = half_bits_to_float(r.d);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            // sc[8n + h + 2t]: byte h + 2t of the half's 8 scale bytes (signed)
+            const uint32_t w = t < 2 ? r.s0 : r.s1;
+            const int sh = 8 * (h + 2 * (t & 1));
+            const float s = d * static_cast<float>(static_cast<int8_t>(w >> sh));
+            // codes q + 32 enter as 1024 + (q+32) (t < 2) or 1024 + 16(q+32) (t >= 2)
+            const float ag = t < 2 ? s : s * 0.0625f;
+            a[t] = valid ? ag : 0.0f;
+            B[t] = valid ? ag * (t < 2 ? 1056.0f : 1536.0f) : 0.0f;
+        }
     }
 };
 
-// ------------------------------------------------------------------------------------
-// Q8_0: 64 blocks (2176 B) per window, lane = block.
-// ------------------------------------------------------------------------------------
-struct FmtQ80 {
+// Q8_0: lane = blocks 2*lane, 2*lane + 1 (64 weights, k = 64*lane + 0..63).  Groups: the blocks.
+struct GQ80 {
     static constexpr int kType = QMM_TYPE_Q8_0;
     static constexpr int kQK = kQK8_0;
     static constexpr int kBlockBytes = kBytesQ8_0;
-    static constexpr int kWindowBytes = 64 * kBytesQ8_0;  // 2176 = 136 x 16
-    static constexpr bool kStaged = true;
-    static constexpr int kGroups = 1;
-    static constexpr int kLoads = (kWindowBytes / 16 + 63) / 64;
-
-    __device__ static void runs(int lane, int off[4]) {
+    static constexpr int kWinBytes = 128 * kBytesQ8_0;  // 4352
+    static constexpr int kG = 2;
+    static constexpr bool kAligned = false;
+    struct Raw {
+        u32x4 q[2][2];
+        uint32_t d[2];
+    };
+    __device__ static int xk(int lane, int cj) { return 64 * lane + 8 * cj; }
+    __device__ static bool group_valid(int lane, int g, int kwin_valid) { return 64 * lane + 32 * g < kwin_valid; }
+    __device__ static Raw load(const uint8_t* win, int lane, int kwin_valid) {
+        Raw r;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) off[r] = 32 * lane + 8 * r;
-    }
-    __device__ static bool lane_valid(int lane, int k0, int K) { return k0 + 32 * lane < K; }
-
-    __device__ static Slot<1> decode(const uint32_t* lds32, int lane) {
-        const int o = 34 * lane;
-        const bool odd = (lane & 1) != 0;
-        const int b = (o - (odd ? 2 : 0)) >> 2;
-        uint32_t dw[9];
-#pragma unroll
-        for (int i = 0; i < 9; ++i) dw[i] = lds32[b + i];
-        const float d = half_bits_to_float(odd ? (dw[0] >> 16) : dw[0]);
-        Slot<1> s;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t v = odd ? dw[i + 1] : __builtin_amdgcn_alignbyte(dw[i + 1], dw[i], 2);
-            s.q[i] = v ^ 0x80808080u;  // signed int8 -> unsigned q + 128
+        for (int b = 0; b < 2; ++b) {
+            const bool v = 64 * lane + 32 * b < kwin_valid;
+            const uint8_t* p = win + (v ? (2 * lane + b) * kBytesQ8_0 : 0);
+            r.q[b][0] = ldg16(p + 2);
+            r.q[b][1] = ldg16(p + 18);
+            r.d[b] = ldg_u16(p);
         }
-        s.a[0] = d;
-        s.b[0] = 128.0f * d;
-        return s;
+        return r;
+    }
+    __device__ static void chunk_codes(const Raw& r, int cj, const Consts& K, uint32_t out[4]) {
+        const u32x4& q = r.q[cj >> 2][(cj >> 1) & 1];
+        const bool second = (cj & 1) != 0;
+        const uint32_t D[2] = {(second ? q.z : q.x) ^ 0x80808080u, (second ? q.w : q.y) ^ 0x80808080u};
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            // [b0, 0x64, b2, 0x64] and [b1, 0x64, b3, 0x64]: 1024 + (q + 128)
+            out[2 * i] = __builtin_amdgcn_perm(K.mg, D[i], 0x07020500u);
+            out[2 * i + 1] = __builtin_amdgcn_perm(K.mg, D[i], 0x07030501u);
+        }
+    }
+    __device__ static void group_scales(const Raw& r, int, bool, float a[kG], float B[kG]) {
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            const float d = half_bits_to_float(r.d[g]);
+            a[g] = d;
+            B[g] = d * 1152.0f;
+        }
     }
 };
 
-// ------------------------------------------------------------------------------------
-// Q4_0: 64 blocks (1152 B) per window, lane = block.
-// ------------------------------------------------------------------------------------
-struct FmtQ40 {
+// Q4_0: lane = blocks 2*lane, 2*lane + 1.  Groups: block b low nibbles (k 32b + 0..15, chunks
+// 4b, 4b+1) and high nibbles (k 32b + 16..31, chunks 4b+2, 4b+3).
+struct GQ40 {
     static constexpr int kType = QMM_TYPE_Q4_0;
     static constexpr int kQK = kQK4_0;
     static constexpr int kBlockBytes = kBytesQ4_0;
-    static constexpr int kWindowBytes = 64 * kBytesQ4_0;  // 1152 = 72 x 16
-    static constexpr bool kStaged = true;
-    static constexpr int kGroups = 2;
-    static constexpr int kLoads = (kWindowBytes / 16 + 63) / 64;
-
-    __device__ static void runs(int lane, int off[4]) {
+    static constexpr int kWinBytes = 128 * kBytesQ4_0;  // 2304
+    static constexpr int kG = 4;
+    static constexpr bool kAligned = false;
+    struct Raw {
+        u32x4 q[2];
+        uint32_t d[2];
+    };
+    __device__ static int xk(int lane, int cj) { return 64 * lane + 8 * cj; }
+    __device__ static bool group_valid(int lane, int g, int kwin_valid) { return 64 * lane + 32 * (g >> 1) < kwin_valid; }
+    __device__ static Raw load(const uint8_t* win, int lane, int kwin_valid) {
+        Raw r;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) off[r] = 32 * lane + 8 * r;
-    }
-    __device__ static bool lane_valid(int lane, int k0, int K) { return k0 + 32 * lane < K; }
-
-    __device__ static Slot<2> decode(const uint32_t* lds32, int lane) {
-        const int o = 18 * lane;
-        const bool odd = (lane & 1) != 0;
-        const int b = (o - (odd ? 2 : 0)) >> 2;
-        uint32_t dw[5];
-#pragma unroll
-        for (int i = 0; i < 5; ++i) dw[i] = lds32[b + i];
-        const float d = half_bits_to_float(odd ? (dw[0] >> 16) : dw[0]);
-        uint32_t qs[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) qs[i] = odd ? dw[i + 1] : __builtin_amdgcn_alignbyte(dw[i + 1], dw[i], 2);
-        Slot<2> s;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            s.q[i] = qs[i] & 0x0F0F0F0Fu;      // weights 0..15
-            s.q[4 + i] = qs[i] & 0xF0F0F0F0u;  // weights 16..31, entering as 16*q
+        for (int b = 0; b < 2; ++b) {
+            const bool v = 64 * lane + 32 * b < kwin_valid;
+            const uint8_t* p = win + (v ? (2 * lane + b) * kBytesQ4_0 : 0);
+            r.q[b] = ldg16(p + 2);
+            r.d[b] = ldg_u16(p);
         }
-        s.a[0] = d;
-        s.a[1] = d * 0.0625f;
-        s.b[0] = 8.0f * d;
-        s.b[1] = 8.0f * d;
-        return s;
+        return r;
+    }
+    __device__ static void chunk_codes(const Raw& r, int cj, const Consts& K, uint32_t out[4]) {
+        const u32x4& q = r.q[cj >> 2];
+        const bool second = (cj & 1) != 0;   // qs bytes 8..15 of the block
+        const uint32_t dlo = second ? q.z : q.x;
+        const uint32_t dhi = second ? q.w : q.y;
+        const uint32_t m = (cj & 2) ? K.mf0 : K.m0f;
+        out[0] = and_or(dlo, m, K.mg);
+        out[1] = and_or(dlo >> 8, m, K.mg);
+        out[2] = and_or(dhi, m, K.mg);
+        out[3] = and_or(dhi >> 8, m, K.mg);
+    }
+    __device__ static void group_scales(const Raw& r, int, bool, float a[kG], float B[kG]) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const float d = half_bits_to_float(r.d[g >> 1]);
+            if (g & 1) {           // high nibbles: 1024 + 16q, w = d (q - 8)
+                a[g] = d * 0.0625f;
+                B[g] = d * 72.0f;  // (1024/16 + 8) d
+            } else {               // low nibbles: 1024 + q
+                a[g] = d;
+                B[g] = d * 1032.0f;
+            }
+        }
     }
 };
 
+// ------------------------------------------------------------------------------------------
+// Activation staging: chunk cj of lane l holds fp16 pairs (x0,x2), (x1,x3), (x4,x6), (x5,x7)
+// of the 8 activations at window k = F::xk(l, cj); xsum[l][q] = sum of the 16 fp16 values of
+// chunks 2q and 2q+1 (fp32, fixed order).
+// ------------------------------------------------------------------------------------------
 template <typename TA>
-__device__ __forceinline__ void load_run8(const TA* __restrict__ p, bool vec, float x[8]);
+__device__ __forceinline__ void load16_act(const TA* p, bool ok, bool vec, uint32_t h[8]);
 
+// The loads are issued whether or not the activations exist (p is always a valid address);
+// missing ones (`ok` false) are replaced by zeros afterwards.
 template <>
-__device__ __forceinline__ void load_run8<float>(const float* __restrict__ p, bool vec, float x[8]) {
+__device__ __forceinline__ void load16_act<float>(const float* p, bool ok, bool vec, uint32_t h[8]) {
+    float x[16];
     if (vec) {
-        const float4 u = reinterpret_cast<const float4*>(p)[0];
-        const float4 v = reinterpret_cast<const float4*>(p)[1];
-        x[0] = u.x; x[1] = u.y; x[2] = u.z; x[3] = u.w;
-        x[4] = v.x; x[5] = v.y; x[6] = v.z; x[7] = v.w;
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] = p[i];
-    }
-}
-
-template <>
-__device__ __forceinline__ void load_run8<__half>(const __half* __restrict__ p, bool vec, float x[8]) {
-    if (vec) {
-        const uint4 u = *reinterpret_cast<const uint4*>(p);
-        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            x[2 * i] = half_bits_to_float(w[i]);
-            x[2 * i + 1] = half_bits_to_float(w[i] >> 16);
+            const float4 v = reinterpret_cast<const float4*>(p)[i];
+            x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] = __half2float(p[i]);
+        for (int i = 0; i < 16; ++i) x[i] = p[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = ok ? x[i] : 0.0f;
+    // pairs (0,2), (1,3), (4,6), (5,7), ... rounded to nearest even (v_cvt_pk_f16_f32)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int b = 8 * c + 4 * (i >> 1) + (i & 1);
+            h16x2 v = {static_cast<_Float16>(x[b]), static_cast<_Float16>(x[b + 2])};
+            __builtin_memcpy(&h[4 * c + i], &v, 4);
+        }
     }
 }
+
+template <>
+__device__ __forceinline__ void load16_act<__half>(const __half* p, bool ok, bool vec, uint32_t h[8]) {
+    uint32_t w[8];
+    if (vec) {
+        const uint4 a = reinterpret_cast<const uint4*>(p)[0];
+        const uint4 b = reinterpret_cast<const uint4*>(p)[1];
+        w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+    } else {
+        const uint16_t* s = reinterpret_cast<const uint16_t*>(p);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = s[2 * i] | (static_cast<uint32_t>(s[2 * i + 1]) << 16);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = ok ? w[i] : 0u;
+    // dwords (x0,x1), (x2,x3) -> (x0,x2), (x1,x3)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        h[2 * c] = __builtin_amdgcn_perm(w[2 * c + 1], w[2 * c], 0x05040100u);
+        h[2 * c + 1] = __builtin_amdgcn_perm(w[2 * c + 1], w[2 * c], 0x07060302u);
+    }
+}
+
+// LDS layout shared by both kernels, in u32x4 entries of the dynamic LDS array:
+//   x  [slot][m][chunk][lane]  (4 fp16 pairs each)   slot = staged window
+//   sx [slot][m][lane]         (float4: the 4 partial sums of the lane's 16-k pieces)
+extern __shared__ u32x4 gemv_lds[];
+
+__device__ __forceinline__ int x_index(int slot, int m, int MR, int cj, int lane) { return ((slot * MR + m) * kChunks + cj) * 64 + lane; }
+__device__ __forceinline__ int sx_index(int nslots, int slot, int m, int MR, int lane) {
+    return nslots * MR * kChunks * 64 + (slot * MR + m) * 64 + lane;
+}
+
+// Stages activation item idx of window w into LDS slot `slot`: item = (m, q, lane) covers the 16
+// activations of chunks 2q, 2q+1 of the lane's slot.
+template <class F, int MR, typename TA>
+struct StageItem {
+    uint32_t h[8];
+    __device__ __forceinline__ void load(const TA* __restrict__ A, int M, int K, int m0, int w, int item, bool vec) {
+        const int m = item >> 8, q = (item >> 6) & 3, lane = item & 63;
+        const int k = w * kGemvWindow + F::xk(lane, 2 * q);
+        const bool ok = m0 + m < M && k < K;
+        const TA* p = A + static_cast<size_t>(ok ? m0 + m : 0) * K + (ok ? k : 0);
+        load16_act<TA>(p, ok, vec, h);
+    }
+    __device__ __forceinline__ void store(int nslots, int slot, int item) const {
+        const int m = item >> 8, q = (item >> 6) & 3, lane = item & 63;
+        gemv_lds[x_index(slot, m, MR, 2 * q, lane)] = u32x4{h[0], h[1], h[2], h[3]};
+        gemv_lds[x_index(slot, m, MR, 2 * q + 1, lane)] = u32x4{h[4], h[5], h[6], h[7]};
+        const uint32_t ones = 0x3C003C00u;  // fp16 (1, 1)
+        float t = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t = dot2(h[j], ones, t);
+        reinterpret_cast<float*>(&gemv_lds[sx_index(nslots, slot, m, MR, lane)])[q] = t;
+    }
+};
 
 template <typename TC>
 __device__ __forceinline__ void store_out(TC* p, float v);
@@ -272,70 +449,164 @@ __device__ __forceinline__ void store_out<__half>(__half* p, float v) {
     *reinterpret_cast<uint16_t*>(p) = float_to_half_bits(v);
 }
 
-// Weight bytes of one window for the YT rows of a wave, as loaded by one lane.
-template <class F, int YT>
-struct WinBuf {
-    static constexpr int kRaw = F::kStaged ? F::kLoads : 2;
-    u32x4 raw[YT][kRaw];
-};
-
-// Activations of one window for one lane: 4 runs of 8 consecutive k per A row.
-template <int MR>
-struct XBuf {
-    float x[MR][32];
-};
-
-// One wave computes YT consecutive output rows over a K-slice; KS waves of a workgroup
-// split the windows of the same rows round-robin (window w goes to wave w % KS) and their
-// partial sums are added through LDS in wave order.  Window w + KS's weight bytes (and, for
-// one A row, its activations) are loaded while window w is being multiplied.
-template <class F, int MR, int YT, int KS, typename TA, typename TC>
-__global__ __launch_bounds__(kWave * kWavesPerBlock)
-void gemv_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W, TC* __restrict__ C,
-                 int M, int N, int K, int a_vec) {
-    constexpr int G = F::kGroups;
-    constexpr int RPG = 4 / G;  // runs per group
-    constexpr int kPieces = F::kWindowBytes / 16;
-    constexpr int kRaw = WinBuf<F, YT>::kRaw;
-    constexpr int kLdsWords = F::kStaged ? ((F::kWindowBytes + 16 + 15) / 16) * 4 : 4;
-    constexpr int kRowGroups = kWavesPerBlock / KS;
-    constexpr bool kPrefetchX = MR == 1;
-    static_assert(kWavesPerBlock % KS == 0, "KS must divide the waves of a block");
-    __shared__ __align__(16) uint32_t lds_all[kWavesPerBlock][kLdsWords];
-    __shared__ float red[KS > 1 ? kWavesPerBlock : 1][MR * YT];
-
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wv = threadIdx.x / kWave;
-    const int rg = wv / KS;
-    const int ks = wv - rg * KS;
-    const int row0 = (blockIdx.x * kRowGroups + rg) * YT;
-    const bool active = row0 < N;  // wave-uniform; idle waves still join the K-split reduction
-    const int m0 = blockIdx.y * MR;
-    const int mrows = min(MR, M - m0);
-    const uint32_t row_bytes = static_cast<uint32_t>(K / F::kQK) * F::kBlockBytes;
-    const bool vec = a_vec != 0;
-    uint32_t* lds32 = lds_all[wv];
-
-    // Rows past N and A rows past M are computed on clamped (valid) addresses and never
-    // stored, so the steady-state loop carries no per-row predicates.  The host guarantees
-    // N * row_bytes < 2^32, so byte offsets fit 32 bits.
-    uint32_t rowoff[YT];
+// acc[m][y] += the window's contribution of row y for activation row m.
+// FULL: every lane slot of the window is inside K (no validity masks).
+template <class F, int MR, int YT, bool FULL>
+__device__ __forceinline__ void mac_window(const typename F::Raw (&cur)[YT], int nslots, int slot, int lane, int kv,
+                                           const Consts& KC, float (&acc)[MR][YT]) {
+    constexpr int G = F::kG;
+    constexpr int CPG = kChunks / G;  // chunks per group
+    float a[YT][G], B[YT][G];
 #pragma unroll
-    for (int y = 0; y < YT; ++y) rowoff[y] = static_cast<uint32_t>(min(row0 + y, N - 1)) * row_bytes;
-    const TA* xrow[MR];
+    for (int y = 0; y < YT; ++y) {
+        F::group_scales(cur[y], lane, true, a[y], B[y]);
+        if constexpr (!FULL) {
 #pragma unroll
-    for (int m = 0; m < MR; ++m) xrow[m] = A + static_cast<size_t>(min(m0 + m, M - 1)) * K;
-
-    int off[4];
-    F::runs(lane, off);
-    uint32_t loff[kRaw];  // per-lane byte offsets of the loads inside a window
-    if constexpr (F::kStaged) {
-#pragma unroll
-        for (int j = 0; j < kRaw; ++j) loff[j] = 16u * static_cast<uint32_t>(min(lane + kWave * j, kPieces - 1));
-    } else {
-        loff[0] = static_cast<uint32_t>(F::kBlockBytes * (lane >> 3));
-        loff[1] = loff[0] + 16u + 16u * static_cast<uint32_t>(lane & 7);
+            for (int g = 0; g < G; ++g) {
+                const bool v = F::group_valid(lane, g, kv);
+                a[y][g] = v ? a[y][g] : 0.0f;
+                B[y][g] = v ? B[y][g] : 0.0f;
+            }
+        }
     }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float S[MR][YT];
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int y = 0; y < YT; ++y) S[m][y] = 0.0f;
+#pragma unroll
+        for (int cc = 0; cc < CPG; ++cc) {
+            const int cj = g * CPG + cc;
+            u32x4 xp[MR];
+#pragma unroll
+            for (int m = 0; m < MR; ++m) xp[m] = gemv_lds[x_index(slot, m, MR, cj, lane)];
+#pragma unroll
+            for (int y = 0; y < YT; ++y) {
+                uint32_t code[4];
+                F::chunk_codes(cur[y], cj, KC, code);
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    float s = S[m][y];
+                    s = dot2(xp[m].x, code[0], s);
+                    s = dot2(xp[m].y, code[1], s);
+                    s = dot2(xp[m].z, code[2], s);
+                    s = dot2(xp[m].w, code[3], s);
+                    S[m][y] = s;
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const u32x4 sv = gemv_lds[sx_index(nslots, slot, m, MR, lane)];
+            float sq[4];
+            __builtin_memcpy(sq, &sv, 16);
+            float sxg;
+            if constexpr (G == 2) sxg = sq[2 * g] + sq[2 * g + 1];
+            else sxg = sq[g];
+#pragma unroll
+            for (int y = 0; y < YT; ++y) {
+                float t = acc[m][y];
+                t = __fmaf_rn(a[y][g], S[m][y], t);
+                t = __fmaf_rn(-B[y][g], sxg, t);
+                acc[m][y] = t;
+            }
+        }
+    }
+}
+
+template <int MR, int YT, typename TC>
+__device__ __forceinline__ void reduce_store(float (&acc)[MR][YT], TC* __restrict__ C, int M, int N, int m0, int row0,
+                                             int lane) {
+    float v[MR][YT];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int y = 0; y < YT; ++y) v[m][y] = wave_sum_to_lane63(acc[m][y]);
+    if (lane == 63) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int y = 0; y < YT; ++y)
+                if (m0 + m < M && row0 + y < N) store_out<TC>(C + static_cast<size_t>(m0 + m) * N + row0 + y, v[m][y]);
+    }
+}
+
+// Resident-activation kernel: the workgroup stages all windows of its MR activation rows once,
+// then every wave streams (row group, window) items (YT rows each) round-robin over the grid.
+// Three register buffers rotate statically: while item i is multiplied, items i+1 and i+2 are
+// in flight.  Row and window arithmetic is wave-uniform (scalar).  No barrier after staging.
+// Dynamic LDS: MR * nwin * 9216 bytes.
+template <class F, int MR, int YT, int NW, typename TA, typename TC>
+__global__ __launch_bounds__(64 * NW, QMM_GEMV_MIN_WAVES)
+void gemv_resident_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W, TC* __restrict__ C,
+                          int M, int N, int K, int a_vec, int nrg) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int m0 = blockIdx.y * MR;
+    const bool vec = a_vec != 0;
+    const size_t row_bytes = static_cast<size_t>(K / F::kQK) * F::kBlockBytes;
+    const int nwin = (K + kGemvWindow - 1) / kGemvWindow;
+    const int stride = gridDim.x * NW;
+    const Consts KC = make_consts();
+
+    typedef typename F::Raw Raw;
+    auto load_item = [&](int g, int w, Raw (&r)[YT]) {
+        g = min(g, nrg - 1);  // a prefetch past the wave's last item re-reads a valid row group
+        const int kv = min(K - w * kGemvWindow, kGemvWindow);
+        const uint8_t* base = W + static_cast<size_t>(w) * F::kWinBytes;
+#pragma unroll
+        for (int y = 0; y < YT; ++y) {
+            const uint8_t* rp = base + static_cast<size_t>(min(g * YT + y, N - 1)) * row_bytes;
+            r[y] = F::load(rp, lane, kv);
+        }
+    };
+    auto next = [&](int& g, int& w) {
+        if (++w == nwin) {
+            w = 0;
+            g += stride;
+        }
+    };
+
+    // Item iterators: (gc, wc) is the next item to multiply, (gl, wl) the next to load.
+    int gc = blockIdx.x * NW + wv, wc = 0;
+    int gl = gc, wl = 0;
+    const bool active = gc < nrg;
+
+    // Staging order: this thread's first activation loads, then three items of weight bytes,
+    // then the LDS writes; the weight loads stay in flight through the barrier.
+    constexpr int kFirst = 2;  // activation items per thread issued before the weight loads
+    const int items = nwin * MR * 256;
+    StageItem<F, MR, TA> st[kFirst];
+#pragma unroll
+    for (int j = 0; j < kFirst; ++j) {
+        const int it = min(tid + 64 * NW * j, items - 1);  // loads always issued (static counts)
+        const int w = it / (MR * 256);
+        st[j].load(A, M, K, m0, w, it - w * (MR * 256), vec);
+    }
+    Raw b0[YT], b1[YT], b2[YT];
+    // issued by every wave (inactive waves re-read a valid row group) to keep counts static
+    load_item(gl, wl, b0); next(gl, wl);
+    load_item(gl, wl, b1); next(gl, wl);
+    load_item(gl, wl, b2); next(gl, wl);
+#pragma unroll
+    for (int j = 0; j < kFirst; ++j) {
+        const int it = tid + 64 * NW * j;
+        if (it < items) {
+            const int w = it / (MR * 256);
+            st[j].store(nwin, w, it - w * (MR * 256));
+        }
+    }
+    for (int it = tid + 64 * NW * kFirst; it < items; it += 64 * NW) {
+        const int w = it / (MR * 256), item = it - w * (MR * 256);
+        StageItem<F, MR, TA> s2;
+        s2.load(A, M, K, m0, w, item, vec);
+        s2.store(nwin, w, item);
+    }
+    __syncthreads();
+    if (!active) return;
 
     float acc[MR][YT];
 #pragma unroll
@@ -343,176 +614,122 @@ void gemv_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W, TC* __
 #pragma unroll
         for (int y = 0; y < YT; ++y) acc[m][y] = 0.0f;
 
-    auto load_x = [&](XBuf<MR>& xb, int w, auto tail_tag) {
-        constexpr bool kTail = decltype(tail_tag)::value;
-        const int k0 = w * kWindow;
-        const bool lv = kTail ? F::lane_valid(lane, k0, K) : true;
-#pragma unroll
-        for (int m = 0; m < MR; ++m) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int o = kTail ? (lv ? off[r] : 0) : off[r];
-                load_run8<TA>(xrow[m] + k0 + o, vec, &xb.x[m][8 * r]);
-                if constexpr (kTail) {
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) xb.x[m][8 * r + i] = lv ? xb.x[m][8 * r + i] : 0.0f;
-                }
-            }
-        }
-    };
-
-    // Issues the loads of window w: the weight bytes of the YT rows, then the activations.
-    auto load = [&](WinBuf<F, YT>& b, XBuf<MR>& xb, int w, auto tail_tag) {
-        constexpr bool kTail = decltype(tail_tag)::value;
-        const int k0 = w * kWindow;
-        const uint32_t wb = static_cast<uint32_t>(w) * F::kWindowBytes;
-        uint32_t lo[kRaw];
-#pragma unroll
-        for (int j = 0; j < kRaw; ++j) lo[j] = loff[j];
-        if constexpr (kTail) {
-            const bool lv = F::lane_valid(lane, k0, K);
-            const int valid_pieces = static_cast<int>((K - k0) / F::kQK) * F::kBlockBytes / 16;
-#pragma unroll
-            for (int j = 0; j < kRaw; ++j) {
-                if constexpr (F::kStaged) lo[j] = 16u * static_cast<uint32_t>(min(lane + kWave * j, valid_pieces - 1));
-                else lo[j] = lv ? loff[j] : (j == 0 ? 0u : 16u);
-            }
-        }
-#pragma unroll
-        for (int y = 0; y < YT; ++y)
-#pragma unroll
-            for (int j = 0; j < kRaw; ++j)
-                b.raw[y][j] = *reinterpret_cast<const u32x4*>(W + (rowoff[y] + wb + lo[j]));
-        if constexpr (kPrefetchX) load_x(xb, w, tail_tag);
-    };
-
-    auto compute = [&](const WinBuf<F, YT>& b, const XBuf<MR>& xpre, int w, auto tail_tag) {
-        constexpr bool kTail = decltype(tail_tag)::value;
-        const bool lv = kTail ? F::lane_valid(lane, w * kWindow, K) : true;
-        XBuf<MR> xl;
-        if constexpr (!kPrefetchX) load_x(xl, w, tail_tag);
-        const XBuf<MR>& xb = kPrefetchX ? xpre : xl;
-        float sx[MR][G];
-#pragma unroll
-        for (int m = 0; m < MR; ++m) {
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float t = xb.x[m][8 * RPG * g];
-#pragma unroll
-                for (int i = 1; i < 8 * RPG; ++i) t += xb.x[m][8 * RPG * g + i];
-                sx[m][g] = t;
-            }
-        }
-#pragma unroll
-        for (int y = 0; y < YT; ++y) {
-            Slot<G> s;
-            if constexpr (F::kStaged) {
-                wave_lds_sync();
-#pragma unroll
-                for (int j = 0; j < kRaw; ++j)
-                    reinterpret_cast<u32x4*>(lds32)[min(lane + kWave * j, kPieces - 1)] = b.raw[y][j];
-                wave_lds_sync();
-                s = F::decode(lds32, lane);
-            } else {
-                s = F::decode(b.raw[y], lane);
-            }
-            if constexpr (kTail) {
-#pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    s.a[g] = lv ? s.a[g] : 0.0f;
-                    s.b[g] = lv ? s.b[g] : 0.0f;
-                }
-            }
-            float c[32];
-#pragma unroll
-            for (int i = 0; i < 32; ++i) c[i] = ubyte_to_float(opaque(s.q[i >> 2]), i & 3);
-#pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                float a = acc[m][y];
-#pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    float t = 0.0f;
-#pragma unroll
-                    for (int i = 0; i < 8 * RPG; ++i) t = __fmaf_rn(xb.x[m][8 * RPG * g + i], c[8 * RPG * g + i], t);
-                    a = __fmaf_rn(s.a[g], t, a);
-                    a = __fmaf_rn(-s.b[g], sx[m][g], a);
-                }
-                acc[m][y] = a;
-            }
-        }
-    };
-
-    const int nfull = K / kWindow;
-    if (active) {
-        int w = ks;
-        if (w < nfull) {
-            WinBuf<F, YT> b0, b1;
-            XBuf<MR> x0, x1;
-            load(b0, x0, w, std::false_type{});
-            while (true) {
-                if (w + KS < nfull) load(b1, x1, w + KS, std::false_type{});
-                compute(b0, x0, w, std::false_type{});
-                w += KS;
-                if (w >= nfull) break;
-                if (w + KS < nfull) load(b0, x0, w + KS, std::false_type{});
-                compute(b1, x1, w, std::false_type{});
-                w += KS;
-                if (w >= nfull) break;
-            }
-        }
-        if (K % kWindow != 0 && nfull % KS == ks) {
-            WinBuf<F, YT> bt;
-            XBuf<MR> xt;
-            load(bt, xt, nfull, std::true_type{});
-            compute(bt, xt, nfull, std::true_type{});
-        }
-    }
-
-    float v[MR][YT];
-#pragma unroll
-    for (int m = 0; m < MR; ++m)
-#pragma unroll
-        for (int y = 0; y < YT; ++y) v[m][y] = wave_sum_to_lane63(acc[m][y]);
-    if constexpr (KS == 1) {
-        if (active && lane == kWave - 1) {
+    auto compute = [&](const Raw (&b)[YT]) {
+        const int kv = min(K - wc * kGemvWindow, kGemvWindow);
+        if (kv == kGemvWindow) mac_window<F, MR, YT, true>(b, nwin, wc, lane, kv, KC, acc);
+        else mac_window<F, MR, YT, false>(b, nwin, wc, lane, kv, KC, acc);
+        if (wc == nwin - 1) {
+            reduce_store<MR, YT, TC>(acc, C, M, N, m0, gc * YT, lane);
 #pragma unroll
             for (int m = 0; m < MR; ++m)
 #pragma unroll
-                for (int y = 0; y < YT; ++y)
-                    if (m < mrows && row0 + y < N) store_out<TC>(C + static_cast<size_t>(m0 + m) * N + row0 + y, v[m][y]);
+                for (int y = 0; y < YT; ++y) acc[m][y] = 0.0f;
         }
-    } else {
-        if (lane == kWave - 1) {
-#pragma unroll
-            for (int m = 0; m < MR; ++m)
-#pragma unroll
-                for (int y = 0; y < YT; ++y) red[wv][m * YT + y] = v[m][y];
-        }
-        __syncthreads();
-        if (active && ks == 0 && lane == kWave - 1) {
-#pragma unroll
-            for (int m = 0; m < MR; ++m) {
-#pragma unroll
-                for (int y = 0; y < YT; ++y) {
-                    float t = red[wv][m * YT + y];
-#pragma unroll
-                    for (int j = 1; j < KS; ++j) t += red[wv + j][m * YT + y];
-                    if (m < mrows && row0 + y < N) store_out<TC>(C + static_cast<size_t>(m0 + m) * N + row0 + y, t);
-                }
-            }
-        }
+        next(gc, wc);
+    };
+
+    // Three items are in flight when an item's multiply starts; its buffer is refilled with the
+    // item three ahead right after (past the wave's last item: a valid row group re-read).
+    const int total = ((nrg - gc + stride - 1) / stride) * nwin;
+    int i = 0;
+    while (true) {
+        compute(b0);
+        if (++i == total) break;
+        load_item(gl, wl, b0); next(gl, wl);
+        compute(b1);
+        if (++i == total) break;
+        load_item(gl, wl, b1); next(gl, wl);
+        compute(b2);
+        if (++i == total) break;
+        load_item(gl, wl, b2); next(gl, wl);
     }
 }
 
+// Windowed kernel (activations too large to keep resident): one workgroup owns NW * YT rows;
+// window w + 1's activations are staged into the other of two LDS slots and its weight bytes
+// loaded while window w is multiplied; one barrier per window.  Dynamic LDS: MR * 2 * 9216.
+template <class F, int MR, int YT, int NW, typename TA, typename TC>
+__global__ __launch_bounds__(64 * NW, QMM_GEMV_MIN_WAVES)
+void gemv_window_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W, TC* __restrict__ C,
+                        int M, int N, int K, int a_vec) {
+    constexpr int kItems = MR * 256;
+    constexpr int kPer = (kItems + 64 * NW - 1) / (64 * NW);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wv = tid >> 6;
+    const int row0 = (blockIdx.x * NW + wv) * YT;
+    const int m0 = blockIdx.y * MR;
+    const bool vec = a_vec != 0;
+    const size_t row_bytes = static_cast<size_t>(K / F::kQK) * F::kBlockBytes;
+    const Consts KC = make_consts();
+
+    // Rows past N are computed on the last valid row and never stored.
+    const uint8_t* rowp[YT];
+#pragma unroll
+    for (int y = 0; y < YT; ++y) rowp[y] = W + static_cast<size_t>(min(row0 + y, N - 1)) * row_bytes;
+
+    const int nwin = (K + kGemvWindow - 1) / kGemvWindow;
+    float acc[MR][YT];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int y = 0; y < YT; ++y) acc[m][y] = 0.0f;
+
+    StageItem<F, MR, TA> st[kPer];
+    typename F::Raw cur[YT], nxt[YT];
+
+    const int kv0 = min(K, kGemvWindow);
+#pragma unroll
+    for (int y = 0; y < YT; ++y) cur[y] = F::load(rowp[y], lane, kv0);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+        if (tid + 64 * NW * i < kItems) st[i].load(A, M, K, m0, 0, tid + 64 * NW * i, vec);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+        if (tid + 64 * NW * i < kItems) st[i].store(2, 0, tid + 64 * NW * i);
+    __syncthreads();
+
+    for (int w = 0; w < nwin; ++w) {
+        const bool more = w + 1 < nwin;
+        {
+            // unconditional weight prefetch (the last one re-reads window w)
+            const int wn = more ? w + 1 : w;
+            const int kv = min(K - wn * kGemvWindow, kGemvWindow);
+            const size_t wo = static_cast<size_t>(wn) * F::kWinBytes;
+#pragma unroll
+            for (int y = 0; y < YT; ++y) nxt[y] = F::load(rowp[y] + wo, lane, kv);
+        }
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < kPer; ++i)
+                if (tid + 64 * NW * i < kItems) st[i].load(A, M, K, m0, w + 1, tid + 64 * NW * i, vec);
+        }
+        {
+            const int kv = min(K - w * kGemvWindow, kGemvWindow);
+            if (kv == kGemvWindow) mac_window<F, MR, YT, true>(cur, 2, w & 1, lane, kv, KC, acc);
+            else mac_window<F, MR, YT, false>(cur, 2, w & 1, lane, kv, KC, acc);
+        }
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < kPer; ++i)
+                if (tid + 64 * NW * i < kItems) st[i].store(2, (w + 1) & 1, tid + 64 * NW * i);
+        }
+#pragma unroll
+        for (int y = 0; y < YT; ++y) cur[y] = nxt[y];
+        __syncthreads();
+    }
+    reduce_store<MR, YT, TC>(acc, C, M, N, m0, row0, lane);
+}
+
 // Alignment-agnostic fallback: one wave per (row n, A row m), lanes over 32-weight groups,
-// byte loads.  Used when a fast-path precondition fails (unaligned W, or K not a multiple of
-// 2048 for Q6_K / of 256 for Q4_0 and Q8_0).
+// byte loads, fp32 FMAs.  Used when W is not 2-byte aligned (16-byte for Q4_K) or A is not
+// 4-byte aligned.
 template <int T, typename TA, typename TC>
-__global__ __launch_bounds__(kWave * kWavesPerBlock)
+__global__ __launch_bounds__(256)
 void gemv_fallback_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W, TC* __restrict__ C,
                           int M, int N, int K) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int n = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+    const int lane = threadIdx.x & 63;
+    const int n = blockIdx.x * 4 + threadIdx.x / 64;
     const int m = blockIdx.y;
     if (n >= N || m >= M) return;
     const int qk = (T == QMM_TYPE_Q4_0 || T == QMM_TYPE_Q8_0) ? 32 : 256;
@@ -522,7 +739,7 @@ void gemv_fallback_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ 
     const TA* x = A + static_cast<size_t>(m) * K;
     const int groups = K / 32;
     float acc = 0.0f;
-    for (int g = lane; g < groups; g += kWave) {
+    for (int g = lane; g < groups; g += 64) {
         float w[32];
         group_weights_bytewise<T>(row, g, w);
 #pragma unroll
@@ -534,84 +751,146 @@ void gemv_fallback_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ 
         }
     }
     acc = wave_sum_to_lane63(acc);
-    if (lane == kWave - 1) store_out<TC>(C + static_cast<size_t>(m) * N + n, acc);
+    if (lane == 63) store_out<TC>(C + static_cast<size_t>(m) * N + n, acc);
 }
 
-template <class F, int MR, int YT, int KS, typename TA, typename TC>
-hipError_t launch_fast(const void* A, const void* W, void* C, int M, int N, int K, bool a_vec,
-                       hipStream_t stream) {
-    constexpr int kRowsPerBlock = (kWavesPerBlock / KS) * YT;
-    const dim3 block(kWave * kWavesPerBlock);
-    const dim3 grid((N + kRowsPerBlock - 1) / kRowsPerBlock, (M + MR - 1) / MR);
-    hipLaunchKernelGGL((gemv_kernel<F, MR, YT, KS, TA, TC>), grid, block, 0, stream,
-                       static_cast<const TA*>(A), static_cast<const uint8_t*>(W), static_cast<TC*>(C),
-                       M, N, K, a_vec ? 1 : 0);
+// Per-device facts and per-(kernel, LDS size) occupancy, cached (queried once; thread-safe).
+struct DevInfo {
+    int cus = 0;
+    size_t max_lds = 0;
+};
+
+std::mutex g_info_mutex;
+
+hipError_t device_info(DevInfo& out) {
+    static std::unordered_map<int, DevInfo> cache;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(g_info_mutex);
+    auto it = cache.find(dev);
+    if (it != cache.end()) {
+        out = it->second;
+        return hipSuccess;
+    }
+    DevInfo d;
+    int v = 0;
+    if ((e = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
+    d.cus = v;
+    if ((e = hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev)) != hipSuccess) return e;
+    d.max_lds = static_cast<size_t>(v);
+    cache[dev] = d;
+    out = d;
+    return hipSuccess;
+}
+
+// Workgroups of `kern` that fit on one CU with `lds` bytes of dynamic LDS (at least 1).
+hipError_t occupancy(const void* kern, int threads, size_t lds, int& blocks) {
+    static std::unordered_map<std::string, int> cache;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const std::string key = std::to_string(dev) + ":" + std::to_string(reinterpret_cast<uintptr_t>(kern)) + ":" +
+                            std::to_string(lds);
+    std::lock_guard<std::mutex> lock(g_info_mutex);
+    auto it = cache.find(key);
+    if (it != cache.end()) {
+        blocks = it->second;
+        return hipSuccess;
+    }
+    if (lds > 65536) {
+        e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (e != hipSuccess) return e;
+    }
+    int n = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, lds);
+    if (e != hipSuccess) return e;
+    blocks = n > 0 ? n : 1;
+    cache[key] = blocks;
+    return hipSuccess;
+}
+
+constexpr size_t kSlotBytes = kChunks * 64 * 16 + 64 * 16;  // x + sx of one window, one A row
+
+template <class F, int MR, int YT, int NW, typename TA, typename TC>
+hipError_t launch_fast(const void* A, const void* W, void* C, int M, int N, int K, bool a_vec, hipStream_t stream) {
+    DevInfo di;
+    hipError_t e = device_info(di);
+    if (e != hipSuccess) return e;
+    const int nwin = (K + kGemvWindow - 1) / kGemvWindow;
+    const int mblocks = (M + MR - 1) / MR;
+    const size_t res_lds = static_cast<size_t>(MR) * nwin * kSlotBytes;
+    const int threads = 64 * NW;
+    if (res_lds <= di.max_lds) {
+        const void* kern = reinterpret_cast<const void*>(&gemv_resident_kernel<F, MR, YT, NW, TA, TC>);
+        int occ = 0;
+        if ((e = occupancy(kern, threads, res_lds, occ)) != hipSuccess) return e;
+        const int nrg = (N + YT - 1) / YT;
+        const int need = (nrg + NW - 1) / NW;
+        const int fill = max(1, occ * di.cus / mblocks);
+        const dim3 grid(min(need, fill), mblocks);
+        hipLaunchKernelGGL((gemv_resident_kernel<F, MR, YT, NW, TA, TC>), grid, dim3(threads), res_lds, stream,
+                           static_cast<const TA*>(A), static_cast<const uint8_t*>(W), static_cast<TC*>(C), M, N, K,
+                           a_vec ? 1 : 0, nrg);
+        return hipGetLastError();
+    }
+    const size_t win_lds = static_cast<size_t>(MR) * 2 * kSlotBytes;
+    const void* kern = reinterpret_cast<const void*>(&gemv_window_kernel<F, MR, YT, NW, TA, TC>);
+    int occ = 0;
+    if ((e = occupancy(kern, threads, win_lds, occ)) != hipSuccess) return e;
+    constexpr int kRows = NW * YT;
+    const dim3 grid((N + kRows - 1) / kRows, mblocks);
+    hipLaunchKernelGGL((gemv_window_kernel<F, MR, YT, NW, TA, TC>), grid, dim3(threads), win_lds, stream,
+                       static_cast<const TA*>(A), static_cast<const uint8_t*>(W), static_cast<TC*>(C), M, N, K,
+                       a_vec ? 1 : 0);
     return hipGetLastError();
-}
-
-// Rows per wave: enough waves to cover the chip several times over.
-inline int pick_yt(int N) {
-    if (N >= 4 * 2048) return 4;
-    if (N >= 2 * 2048) return 2;
-    return 1;
 }
 
 template <class F, typename TA, typename TC>
 hipError_t dispatch_fast(const void* A, const void* W, void* C, int M, int N, int K, bool a_vec,
                          hipStream_t stream) {
-    const int yt = pick_yt(N);
+    // Rows per workgroup: enough workgroups to cover the 256 CUs several times.
+    constexpr int NW = QMM_GEMV_NW;
+    constexpr int YB = QMM_GEMV_YT_BIG;
     if (M == 1) {
-        switch (yt) {
-            case 4: return launch_fast<F, 1, 4, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-            case 2: return launch_fast<F, 1, 2, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-            default: return launch_fast<F, 1, 1, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-        }
+        if (N >= 8192) return launch_fast<F, 1, YB, NW, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+        if (N >= 2048) return launch_fast<F, 1, 2, NW, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+        return launch_fast<F, 1, 1, NW, TA, TC>(A, W, C, M, N, K, a_vec, stream);
     }
     if (M == 2) {
-        switch (yt) {
-            case 4: return launch_fast<F, 2, 4, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-            case 2: return launch_fast<F, 2, 2, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-            default: return launch_fast<F, 2, 1, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-        }
+        if (N >= 8192) return launch_fast<F, 2, YB, NW, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+        if (N >= 2048) return launch_fast<F, 2, 2, NW, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+        return launch_fast<F, 2, 1, NW, TA, TC>(A, W, C, M, N, K, a_vec, stream);
     }
-    switch (yt) {
-        case 4: return launch_fast<F, 4, 4, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-        case 2: return launch_fast<F, 4, 2, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-        default: return launch_fast<F, 4, 1, 1, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-    }
+    if (N >= 4096) return launch_fast<F, 4, 2, NW, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+    return launch_fast<F, 4, 1, NW, TA, TC>(A, W, C, M, N, K, a_vec, stream);
 }
 
 template <int T, typename TA, typename TC>
 hipError_t launch_fallback(const void* A, const void* W, void* C, int M, int N, int K, hipStream_t stream) {
-    const dim3 block(kWave * kWavesPerBlock);
-    const dim3 grid((N + kWavesPerBlock - 1) / kWavesPerBlock, M);
-    hipLaunchKernelGGL((gemv_fallback_kernel<T, TA, TC>), grid, block, 0, stream,
-                       static_cast<const TA*>(A), static_cast<const uint8_t*>(W), static_cast<TC*>(C),
-                       M, N, K);
+    const dim3 grid((N + 3) / 4, M);
+    hipLaunchKernelGGL((gemv_fallback_kernel<T, TA, TC>), grid, dim3(256), 0, stream,
+                       static_cast<const TA*>(A), static_cast<const uint8_t*>(W), static_cast<TC*>(C), M, N, K);
     return hipGetLastError();
 }
 
 template <typename TA, typename TC>
-hipError_t dispatch_types(int t, const void* A, const void* W, void* C, int M, int N, int K,
-                          hipStream_t stream) {
-    // Fast-path preconditions: 16-byte aligned packed rows, and a weight matrix below
-    // 4 GiB so per-lane byte offsets fit 32 bits.
-    const uint64_t total = static_cast<uint64_t>(N) * static_cast<uint64_t>(K / block_elems(t)) *
-                           static_cast<uint64_t>(block_bytes(t));
-    const bool w_aligned = (reinterpret_cast<uintptr_t>(W) & 15u) == 0 && total < (1ull << 32);
+hipError_t dispatch_types(int t, const void* A, const void* W, void* C, int M, int N, int K, hipStream_t stream) {
+    const uintptr_t wa = reinterpret_cast<uintptr_t>(W);
+    const bool a_ok = (reinterpret_cast<uintptr_t>(A) & (sizeof(TA) - 1)) == 0;
     const bool a_vec = (reinterpret_cast<uintptr_t>(A) & 15u) == 0;
     switch (t) {
         case QMM_TYPE_Q4_K:
-            if (w_aligned) return dispatch_fast<FmtQ4K, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+            if ((wa & 15u) == 0 && a_ok) return dispatch_fast<GQ4K, TA, TC>(A, W, C, M, N, K, a_vec, stream);
             return launch_fallback<QMM_TYPE_Q4_K, TA, TC>(A, W, C, M, N, K, stream);
         case QMM_TYPE_Q6_K:
-            if (w_aligned && K % 2048 == 0) return dispatch_fast<FmtQ6K, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+            if ((wa & 1u) == 0 && a_ok) return dispatch_fast<GQ6K, TA, TC>(A, W, C, M, N, K, a_vec, stream);
             return launch_fallback<QMM_TYPE_Q6_K, TA, TC>(A, W, C, M, N, K, stream);
         case QMM_TYPE_Q8_0:
-            if (w_aligned && K % 256 == 0) return dispatch_fast<FmtQ80, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+            if ((wa & 1u) == 0 && a_ok) return dispatch_fast<GQ80, TA, TC>(A, W, C, M, N, K, a_vec, stream);
             return launch_fallback<QMM_TYPE_Q8_0, TA, TC>(A, W, C, M, N, K, stream);
         case QMM_TYPE_Q4_0:
-            if (w_aligned && K % 256 == 0) return dispatch_fast<FmtQ40, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+            if ((wa & 1u) == 0 && a_ok) return dispatch_fast<GQ40, TA, TC>(A, W, C, M, N, K, a_vec, stream);
             return launch_fallback<QMM_TYPE_Q4_0, TA, TC>(A, W, C, M, N, K, stream);
         default:
             return hipErrorInvalidValue;
