@@ -9,13 +9,16 @@ algorithmic bytes (packed weights + fp32 activations read once + fp32 outputs wr
 per second over the timed steps.
 
 The `roofline` object covers the dominant kernel (the Q4_K GEMV serving gate/up,
-28672 x 8192): HIP events recorded around each of its launches inside the timed region give
-its average duration.  `cpu_baseline` times the in-repo NumPy restatement of the reference's
-CPU path (dequantize to fp16, then fp32 matmul) on a bounded sample.  `extra` holds the other
-configurations (8B Q8_0 / Q4_K_M layers, the 8B Q6_K lm_head, 70B at M = 4, the Q4_0
-4096 x 4096 case), each on rotated weight copies larger than the 256 MB MALL.
+28672 x 8192): its 160 launches of one step (gate and up of every layer) are issued back to
+back between two HIP events on their stream, and `achieved` is its algorithmic bytes over the
+average launch duration; `traffic` is the HBM bytes per launch from the committed counter
+summary (profiles/gemv_q4_k_28672x8192_m1_traffic.md, made with `--pmc-workload`).
+`cpu_baseline` times the in-repo NumPy restatement of the reference's CPU path (dequantize to
+fp16, then fp32 matmul) on three full 70B layers.  `extra` holds the other configurations (8B
+Q8_0 / Q4_K_M layers, the 8B Q6_K lm_head, 70B at M = 4, the Q4_0 4096 x 4096 case, prefill
+M = 512), each on rotated weight copies larger than the 256 MB MALL.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-extra] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-extra] [--no-cpu-baseline] [--pmc-workload]
 """
 
 from __future__ import annotations
@@ -163,34 +166,50 @@ class Workload:
         self.descs_py.clear()
 
 
-def run_workload(torch, qmm, hip, wl, steps, warmup, time_dominant=False):
+def run_workload(torch, qmm, hip, wl, steps, warmup):
+    """Average ms per step (one qmm_gemm_batch call over all descriptors) and wall seconds."""
     stream = torch.cuda.current_stream().cuda_stream
     plain = wl.descs()
     for _ in range(warmup):
         qmm.check(qmm.lib().qmm_gemm_batch(plain, len(plain), stream))
     torch.cuda.synchronize()
-    step_arrays, dom_events = [], []
-    for _ in range(steps):
-        events = {}
-        if time_dominant:
-            for i in wl.dominant_idx:
-                events[i] = (hip.event(), hip.event())
-            dom_events.extend(events.values())
-        step_arrays.append(wl.descs(events) if events else plain)
     t_start, t_end = hip.event(), hip.event()
-    torch.cuda.synchronize()
     wall0 = time.perf_counter()
     hip.record(t_start, stream)
-    for arr in step_arrays:
-        qmm.check(qmm.lib().qmm_gemm_batch(arr, len(arr), stream))
+    for _ in range(steps):
+        qmm.check(qmm.lib().qmm_gemm_batch(plain, len(plain), stream))
     hip.record(t_end, stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     total_ms = hip.elapsed_ms(t_start, t_end)
-    dom_ms = [hip.elapsed_ms(a, b) for a, b in dom_events]
-    for e in [t_start, t_end] + [x for pair in dom_events for x in pair]:
-        hip.destroy(e)
-    return total_ms / steps, wall, dom_ms
+    hip.destroy(t_start)
+    hip.destroy(t_end)
+    return total_ms / steps, wall
+
+
+def run_dominant(torch, qmm, hip, wl, reps, warmup=2):
+    """Average duration of the dominant kernel: its launches of one step (the gate and up GEMVs
+    of all layers, distinct weights) issued back to back between two HIP events on the stream
+    they run on, `reps` times; returns (avg_us, launches)."""
+    stream = torch.cuda.current_stream().cuda_stream
+    idx = wl.dominant_idx
+    arr = (wl.qmm.GemmDesc * len(idx))()
+    full = wl.descs()
+    for j, i in enumerate(idx):
+        arr[j] = full[i]
+    for _ in range(warmup):
+        qmm.check(qmm.lib().qmm_gemm_batch(arr, len(arr), stream))
+    torch.cuda.synchronize()
+    a, b = hip.event(), hip.event()
+    hip.record(a, stream)
+    for _ in range(reps):
+        qmm.check(qmm.lib().qmm_gemm_batch(arr, len(arr), stream))
+    hip.record(b, stream)
+    torch.cuda.synchronize()
+    ms = hip.elapsed_ms(a, b)
+    hip.destroy(a)
+    hip.destroy(b)
+    return ms * 1e3 / (reps * len(idx)), reps * len(idx)
 
 
 def run_prefill(torch, qmm, hip, gen, dev, steps, warmup):
@@ -228,9 +247,10 @@ def run_prefill(torch, qmm, hip, gen, dev, steps, warmup):
     return res
 
 
-def cpu_baseline_70b(rows_fraction=0.25, seed=0):
-    """NumPy restatement of the reference CPU path (dequantize -> fp16 -> fp32 matmul) on the
-    first quarter of the rows of each of the 7 matrices of one 70B layer, M = 1."""
+def cpu_baseline_70b(layers=3, seed=0):
+    """NumPy restatement of the reference CPU path (dequantize -> fp16 -> fp32 matmul,
+    src/gguf_parser.py:374-589 and tests/test_gguf_and_q4.py:127-128) over `layers` distinct
+    Llama-3-70B Q4_K_M layers at M = 1 (7 matrices each, 542 MB packed per layer)."""
     import numpy as np
 
     import gguf_oracle as O
@@ -239,29 +259,52 @@ def cpu_baseline_70b(rows_fraction=0.25, seed=0):
     specs = layer_specs(8192, 28672, 1024, Q4_K, Q6_K)
     xs = {"h": rng.standard_normal((1, 8192)).astype(np.float32),
           "f": rng.standard_normal((1, 28672)).astype(np.float32)}
-    mats = []
-    for (_, t, n, k, inp) in specs:
-        rows = max(1, int(n * rows_fraction))
-        mats.append((t, rows, k, O.synth_weights(t, rows, k, rng), inp))
-    t0 = time.perf_counter()
+    t_total = 0.0
     nbytes = 0
-    for (t, rows, k, raw, inp) in mats:
-        W = O.dequantize_f16(t, raw, rows * k).reshape(rows, k).astype(np.float32)
-        _ = xs[inp] @ W.T
-        nbytes += raw.nbytes + 4 * k + 4 * rows
-    dt = time.perf_counter() - t0
+    for _ in range(layers):
+        for (_, t, n, k, inp) in specs:
+            raw = O.synth_weights(t, n, k, rng)  # generation is not timed
+            t0 = time.perf_counter()
+            W = O.dequantize_f16(t, raw, n * k).reshape(n, k).astype(np.float32)
+            _ = xs[inp] @ W.T
+            t_total += time.perf_counter() - t0
+            nbytes += raw.nbytes + 4 * k + 4 * n
+            del W, raw
     threads = os.environ.get("OMP_NUM_THREADS") or os.environ.get("OPENBLAS_NUM_THREADS")
     return {
-        "value": round(nbytes / dt / 1e9, 4),
+        "value": round(nbytes / t_total / 1e9, 4),
         "unit": "GB/s",
         "cores": len(os.sched_getaffinity(0)),
         "kind": "port",
-        "sample": (f"one Llama-3-70B Q4_K_M layer, first {int(rows_fraction * 100)}% of the rows of each of the "
-                   f"7 matrices ({nbytes / 1e6:.0f} MB packed), M=1: NumPy dequantize to fp16 (single thread) "
-                   f"then fp32 matmul (BLAS threads={threads or 'default'}); {dt:.1f} s; "
-                   f"CPU {platform.processor() or platform.machine()}"),
-        "ms_per_token_extrapolated_80_layers": round(dt / rows_fraction * 80 * 1e3, 1),
+        "sample": (f"{layers} distinct Llama-3-70B Q4_K_M layers, all 7 matrices each ({nbytes / 1e9:.2f} GB packed), "
+                   f"M=1: NumPy dequantize to fp16 (single thread) then fp32 matmul (BLAS threads="
+                   f"{threads or 'default'}); {t_total:.1f} s timed; CPU {platform.processor() or platform.machine()}"),
+        "ms_per_token_extrapolated_80_layers": round(t_total / layers * 80 * 1e3, 1),
     }
+
+
+def pmc_workload(torch, qmm, dev, gen, reps=8):
+    """Counter-collection workload: a plain device copy of known size (256 MiB read + 256 MiB
+    written per launch), then the dominant GEMV (Q4_K 28672 x 8192, M = 1) over 16 distinct
+    weight copies.  Run under `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE`: the copy's
+    per-dispatch reading calibrates the counter against known bytes."""
+    stream = torch.cuda.current_stream().cuda_stream
+    src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    n, k = 28672, 8192
+    ws = [make_weight(torch, Q4_K, n, k, gen, dev) for _ in range(16)]
+    x = torch.randn((1, k), device=dev, generator=gen)
+    y = torch.empty((1, n), device=dev)
+    for r in range(reps):
+        for w in ws:
+            qmm.check(qmm.lib().qmm_gemm(Q4_K, x.data_ptr(), qmm.DTYPE_F32, w.data_ptr(), y.data_ptr(),
+                                         qmm.DTYPE_F32, 1, n, k, stream))
+    torch.cuda.synchronize()
+    log(f"pmc workload done: copy 256 MiB x {reps}, Q4_K {n}x{k} GEMV x {16 * reps}")
 
 
 def main():
@@ -272,6 +315,8 @@ def main():
     ap.add_argument("--layers", type=int, default=80)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="run only the counter-collection workload (copy calibration + dominant GEMV)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -289,6 +334,9 @@ def main():
     gen.manual_seed(0)
     props = torch.cuda.get_device_properties(dev)
     log(f"device {props.name} {getattr(props, 'gcnArchName', '')} CUs={props.multi_processor_count}")
+    if args.pmc_workload:
+        pmc_workload(torch, qmm, dev, gen)
+        return
 
     # ---- headline: Llama-3-70B Q4_K_M, M=1, 80 distinct layers -----------------------------
     t0 = time.perf_counter()
@@ -297,21 +345,17 @@ def main():
     wl = Workload(torch, qmm, "70b", [specs70], args.layers, 1, dev, gen, dominant=dominant)
     torch.cuda.synchronize()
     log(f"70B weights ready: {wl.weight_bytes / 1e9:.2f} GB in {time.perf_counter() - t0:.1f} s")
-    ms, wall, dom_ms = run_workload(torch, qmm, hip, wl, args.steps, args.warmup, time_dominant=True)
+    ms, wall = run_workload(torch, qmm, hip, wl, args.steps, args.warmup)
     gbs = wl.algo_bytes / (ms * 1e-3) / 1e9
     log(f"70B M=1: {ms:.3f} ms/token, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM peak), "
         f"wall {wall:.3f} s for {args.steps} steps")
     dom_bytes = weight_bytes(Q4_K, 28672, 8192) + 4 * 8192 + 4 * 28672
-    dom_avg_ms = sum(dom_ms) / len(dom_ms)
-    dom_gbs = dom_bytes / (dom_avg_ms * 1e-3) / 1e9
-    log(f"dominant kernel (Q4_K 28672x8192 GEMV): {dom_avg_ms * 1e3:.2f} us avg over {len(dom_ms)} launches, "
-        f"{dom_gbs:.1f} GB/s")
+    dom_us, dom_launches = run_dominant(torch, qmm, hip, wl, max(2, args.steps // 4))
+    dom_gbs = dom_bytes / (dom_us * 1e-6) / 1e9
+    log(f"dominant kernel (Q4_K 28672x8192 GEMV, M=1): {dom_us:.2f} us avg over {dom_launches} back-to-back "
+        f"launches, {dom_gbs:.1f} GB/s")
 
-    traffic = None
-    tfile = os.path.join(REPO, "profiles", "gemv_q4_k_28672x8192_traffic.json")
-    if os.path.exists(tfile):
-        with open(tfile) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    traffic = read_traffic()
 
     extra = {}
     if not args.no_extra:
@@ -325,7 +369,7 @@ def main():
         remap_out = {id(wl.outputs[k]): wl4.outputs[k] for k in wl.outputs}
         wl4.descs_py = [(t, remap_in[id(a)], w, remap_out[id(c)], n, k) for (t, a, w, c, n, k) in wl.descs_py]
         wl4.algo_bytes = sum(weight_bytes(t, n, k) + 16 * k + 16 * n for (t, _, _, _, n, k) in wl4.descs_py)
-        ms4, _, _ = run_workload(torch, qmm, hip, wl4, max(3, args.steps // 2), 2)
+        ms4, _ = run_workload(torch, qmm, hip, wl4, max(3, args.steps // 2), 2)
         extra["70b_q4_k_m_m4"] = {"GB/s": round(wl4.algo_bytes / (ms4 * 1e-3) / 1e9, 1), "ms_per_token": round(ms4, 3),
                                   "frac_hbm": round(wl4.algo_bytes / (ms4 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         log(f"70B M=4: {ms4:.3f} ms/step, {extra['70b_q4_k_m_m4']['GB/s']} GB/s")
@@ -337,7 +381,7 @@ def main():
         # 8B layers rotated over enough copies to exceed the 256 MB MALL (>= 1.8 GB).
         for key, main_t, down_t, copies in (("8b_q8_0_layer_m1", Q8_0, Q8_0, 8), ("8b_q4_k_m_layer_m1", Q4_K, Q6_K, 14)):
             w8 = Workload(torch, qmm, key, [layer_specs(4096, 14336, 1024, main_t, down_t)], copies, 1, dev, gen)
-            ms8, _, _ = run_workload(torch, qmm, hip, w8, args.steps, args.warmup)
+            ms8, _ = run_workload(torch, qmm, hip, w8, args.steps, args.warmup)
             per_layer_us = ms8 * 1e3 / copies
             g = w8.algo_bytes / (ms8 * 1e-3) / 1e9
             extra[key] = {"GB/s": round(g, 1), "us_per_layer": round(per_layer_us, 2), "frac_hbm": round(g / HBM_PEAK_GBS, 4),
@@ -350,14 +394,14 @@ def main():
         extra["8b_prefill_m512"] = run_prefill(torch, qmm, hip, gen, dev, max(3, args.steps // 2), 2)
         torch.cuda.empty_cache()
         lm = Workload(torch, qmm, "lm_head", [[("lm_head", Q6_K, 128256, 4096, "h")]], 4, 1, dev, gen)
-        msl, _, _ = run_workload(torch, qmm, hip, lm, args.steps, args.warmup)
+        msl, _ = run_workload(torch, qmm, hip, lm, args.steps, args.warmup)
         g = lm.algo_bytes / (msl * 1e-3) / 1e9
         extra["8b_q6_k_lm_head_m1"] = {"GB/s": round(g, 1), "us": round(msl * 1e3 / 4, 2), "frac_hbm": round(g / HBM_PEAK_GBS, 4)}
         log(f"lm_head: {extra['8b_q6_k_lm_head_m1']}")
         lm.free()
         del lm
         q40 = Workload(torch, qmm, "q4_0", [[("w", Q4_0, 4096, 4096, "h")]], 128, 1, dev, gen)
-        msq, _, _ = run_workload(torch, qmm, hip, q40, args.steps, args.warmup)
+        msq, _ = run_workload(torch, qmm, hip, q40, args.steps, args.warmup)
         g = q40.algo_bytes / (msq * 1e-3) / 1e9
         extra["q4_0_4096x4096_m1"] = {"GB/s": round(g, 1), "us": round(msq * 1e3 / 128, 2),
                                       "note": "128 distinct copies (1.2 GB) streamed back to back"}
@@ -392,13 +436,28 @@ def main():
                    "tokens_per_s": round(1e3 / ms, 1)},
         "roofline": {"bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "gemv_kernel<FmtQ4K> (Q4_K 28672x8192, M=1)",
-                     "avg_us": round(dom_avg_ms * 1e3, 3), "launches": len(dom_ms),
+                     "kernel": "gemv_resident_kernel<GQ4K, M=1> (Q4_K 28672x8192)",
+                     "avg_us": round(dom_us, 3), "launches": dom_launches,
                      "algorithmic_bytes_per_launch": dom_bytes},
         "cpu_baseline": cpu,
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
+
+
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "gemv_q4_k_28672x8192_m1_traffic.md")
+
+
+def read_traffic():
+    """HBM bytes per launch of the dominant kernel from its committed counter summary (the
+    `hbm_bytes_per_launch:` line), or None when the summary is absent."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    with open(TRAFFIC_FILE) as f:
+        for line in f:
+            if line.strip().startswith("hbm_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    return None
 
 
 def wl_bytes_gb(layers):

@@ -47,6 +47,10 @@ constexpr int kChunks = 8;          // 8-weight activation chunks per lane slot
 #ifndef QMM_GEMV_NW
 #define QMM_GEMV_NW 8
 #endif
+// Items of weight bytes in flight while one is multiplied (0, 1 or 2).
+#ifndef QMM_GEMV_DEPTH
+#define QMM_GEMV_DEPTH 0
+#endif
 
 // Register-resident constants (v_and_or_b32 on gfx9 takes no literal operands).
 struct Consts {
@@ -586,11 +590,12 @@ void gemv_resident_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ 
         const int w = it / (MR * 256);
         st[j].load(A, M, K, m0, w, it - w * (MR * 256), vec);
     }
+    constexpr int PD = QMM_GEMV_DEPTH;
     Raw b0[YT], b1[YT], b2[YT];
     // issued by every wave (inactive waves re-read a valid row group) to keep counts static
     load_item(gl, wl, b0); next(gl, wl);
-    load_item(gl, wl, b1); next(gl, wl);
-    load_item(gl, wl, b2); next(gl, wl);
+    if constexpr (PD >= 1) { load_item(gl, wl, b1); next(gl, wl); }
+    if constexpr (PD >= 2) { load_item(gl, wl, b2); next(gl, wl); }
 #pragma unroll
     for (int j = 0; j < kFirst; ++j) {
         const int it = tid + 64 * NW * j;
@@ -628,20 +633,37 @@ void gemv_resident_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ 
         next(gc, wc);
     };
 
-    // Three items are in flight when an item's multiply starts; its buffer is refilled with the
-    // item three ahead right after (past the wave's last item: a valid row group re-read).
+    // PD items are in flight while an item is multiplied; its buffer is refilled with the item
+    // PD + 1 ahead right after (past the wave's last item: a valid row group re-read).
     const int total = ((nrg - gc + stride - 1) / stride) * nwin;
     int i = 0;
-    while (true) {
-        compute(b0);
-        if (++i == total) break;
-        load_item(gl, wl, b0); next(gl, wl);
-        compute(b1);
-        if (++i == total) break;
-        load_item(gl, wl, b1); next(gl, wl);
-        compute(b2);
-        if (++i == total) break;
-        load_item(gl, wl, b2); next(gl, wl);
+    if constexpr (PD == 0) {
+        while (true) {
+            compute(b0);
+            if (++i == total) break;
+            load_item(gl, wl, b0); next(gl, wl);
+        }
+    } else if constexpr (PD == 1) {
+        while (true) {
+            compute(b0);
+            if (++i == total) break;
+            load_item(gl, wl, b0); next(gl, wl);
+            compute(b1);
+            if (++i == total) break;
+            load_item(gl, wl, b1); next(gl, wl);
+        }
+    } else {
+        while (true) {
+            compute(b0);
+            if (++i == total) break;
+            load_item(gl, wl, b0); next(gl, wl);
+            compute(b1);
+            if (++i == total) break;
+            load_item(gl, wl, b1); next(gl, wl);
+            compute(b2);
+            if (++i == total) break;
+            load_item(gl, wl, b2); next(gl, wl);
+        }
     }
 }
 

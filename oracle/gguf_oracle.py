@@ -26,7 +26,11 @@ the vectorised restatement of the reference (``dequantize_*``), and a
 "fields" decomposition ``w = a * code - b`` (``fields_*``) written from the
 block-format description, which also yields the exact fp64 weights used as the
 tolerance reference for GEMV/GEMM.  How each route is pinned (known-answer
-blocks, closed forms, brute force) is recorded in ``tests/test_oracle.py``.
+blocks, closed forms, brute force) is recorded in ``tests/test_oracle.py``;
+``tests/test_ref_vectors.py`` additionally pins the dequantizers and the
+test-input quantizers byte-for-byte against outputs of the reference's own
+``src/gguf_parser.py`` functions (``tests/golden/ref_vectors.npz``).  Every
+function here has such a check; none is parity-unpinned.
 """
 
 from __future__ import annotations

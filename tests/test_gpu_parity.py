@@ -98,6 +98,23 @@ def test_dequant_random_bytes_nan_aware(dev, t):
     np.testing.assert_array_equal(got[ok].view(np.uint32), ref[ok].view(np.uint32))
 
 
+REF_VECTORS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ref_vectors.npz")
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("which", ["deq", "quant"])
+def test_dequant_matches_reference_cpu_output(dev, t, which):
+    # fp16 output of the reference's own dequantize_*_cpu (tests/golden/make_ref_vectors.py)
+    import torch
+    import qmm
+    ref = np.load(REF_VECTORS, allow_pickle=False)
+    name = O.TYPE_NAMES[t]
+    raw = ref[f"{name}_deq_in"] if which == "deq" else ref[f"{name}_quant_out"]
+    want = ref[f"{name}_deq_out"] if which == "deq" else ref[f"{name}_quant_deq"]
+    got = qmm.dequantize(t, to_dev(raw, dev), want.size, out_dtype=torch.float16).cpu().numpy()
+    np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
 def test_dequantize_q4_0_reference_case(dev):
     # tests/test_gguf_and_q4.py:94-112: 1M elements, seed 42, x ~ N(0,1) * 0.1; documented exact.
     import matmul_module

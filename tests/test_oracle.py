@@ -233,3 +233,33 @@ def test_mutation_q4_0_swapped_nibbles_detected(kat, monkeypatch):
 
     monkeypatch.setitem(O.DEQUANT_F32, O.GGML_Q4_0, wrong)
     assert _kat_fails(kat, O.GGML_Q4_0)
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_matmul_reference_and_bf16_operands_brute_force(t):
+    # matmul_reference: the reference tests' formula (fp16-rounded dequantized weights, fp32
+    # accumulate); matmul_bf16_operands: both operands rounded to bf16, fp64 accumulate.  Each is
+    # checked against an explicit triple loop on a tiny case, so a transposed operand, a dropped
+    # rounding step or a wrong row stride fails here.
+    rng = np.random.default_rng(314 + t)
+    qk, _ = O.BLOCK_INFO[t]
+    M, N, K = 3, 5, 2 * max(qk, 64)
+    raw = O.synth_weights(t, N, K, rng)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    w16 = O.dequantize_f16(t, raw, N * K).astype(np.float64).reshape(N, K)
+    wb = O.bf16_bits_to_f32(O.f32_to_bf16_bits(O.DEQUANT_F32[t](raw, N * K))).astype(np.float64).reshape(N, K)
+    ab = O.bf16_bits_to_f32(O.f32_to_bf16_bits(A)).astype(np.float64)
+    ref = np.zeros((M, N))
+    refb = np.zeros((M, N))
+    for m in range(M):
+        for n in range(N):
+            s = 0.0
+            sb = 0.0
+            for k in range(K):
+                s += float(A[m, k]) * w16[n, k]
+                sb += ab[m, k] * wb[n, k]
+            ref[m, n] = s
+            refb[m, n] = sb
+    got = O.matmul_reference(t, A, raw, N, K).astype(np.float64)
+    assert np.max(np.abs(got - ref)) <= 1e-5 * np.max(np.abs(ref))
+    np.testing.assert_allclose(O.matmul_bf16_operands(t, A, raw, N, K), refb, rtol=1e-12, atol=1e-12 * np.max(np.abs(refb)))
