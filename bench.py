@@ -38,7 +38,7 @@ for _p in (PKG, os.path.join(REPO, "oracle")):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
-BF16_DENSE_PEAK_TFLOPS = 2500.0
+F16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 / bf16 MFMA
 
 Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
 BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
@@ -213,37 +213,41 @@ def run_dominant(torch, qmm, hip, wl, reps, warmup=2):
 
 
 def run_prefill(torch, qmm, hip, gen, dev, steps, warmup):
-    """Llama-3-8B prefill GEMMs at M = 512 fp32 activations: gate and up (Q4_K 14336 x 4096) and
-    down (Q6_K 4096 x 14336), each on the bf16-MFMA path; TFLOP/s = 2*M*N*K / kernel time."""
+    """Llama-3-8B prefill GEMMs at M = 512: gate and up (Q4_K 14336 x 4096) and down (Q6_K
+    4096 x 14336), each on the f16-MFMA path with fp16 activations (the reference API's dtype) and
+    with fp32 activations (adds the f16 conversion pass); TFLOP/s = 2*M*N*K / time per call."""
     M = 512
     stream = torch.cuda.current_stream().cuda_stream
     res = {}
     for name, t, n, k in (("gate_q4_k_14336x4096", Q4_K, 14336, 4096), ("up_q4_k_14336x4096", Q4_K, 14336, 4096),
                           ("down_q6_k_4096x14336", Q6_K, 4096, 14336)):
         w = make_weight(torch, t, n, k, gen, dev)
-        x = torch.randn((M, k), device=dev, generator=gen)
-        c = torch.empty((M, n), device=dev)
+        x32 = torch.randn((M, k), device=dev, generator=gen)
+        for adt, x in (("f16", x32.half()), ("f32", x32)):
+            c = torch.empty((M, n), device=dev, dtype=x.dtype)
+            dt = qmm.DTYPE_F16 if adt == "f16" else qmm.DTYPE_F32
 
-        def launch():
-            qmm.check(qmm.lib().qmm_gemm(t, x.data_ptr(), qmm.DTYPE_F32, w.data_ptr(), c.data_ptr(), qmm.DTYPE_F32,
-                                         M, n, k, stream))
+            def launch():
+                qmm.check(qmm.lib().qmm_gemm(t, x.data_ptr(), dt, w.data_ptr(), c.data_ptr(), dt, M, n, k, stream))
 
-        for _ in range(warmup):
-            launch()
-        torch.cuda.synchronize()
-        a, b = hip.event(), hip.event()
-        hip.record(a, stream)
-        for _ in range(steps):
-            launch()
-        hip.record(b, stream)
-        torch.cuda.synchronize()
-        us = hip.elapsed_ms(a, b) * 1e3 / steps
-        hip.destroy(a)
-        hip.destroy(b)
-        tf = 2.0 * M * n * k / (us * 1e-6) / 1e12
-        res[name] = {"us": round(us, 2), "TFLOP/s": round(tf, 1), "frac_bf16_peak": round(tf / BF16_DENSE_PEAK_TFLOPS, 4)}
-        log(f"prefill M=512 {name}: {us:.1f} us, {tf:.1f} TFLOP/s ({tf / BF16_DENSE_PEAK_TFLOPS * 100:.1f}% of bf16 peak)")
-        del w, x, c
+            for _ in range(warmup):
+                launch()
+            torch.cuda.synchronize()
+            a, b = hip.event(), hip.event()
+            hip.record(a, stream)
+            for _ in range(steps):
+                launch()
+            hip.record(b, stream)
+            torch.cuda.synchronize()
+            us = hip.elapsed_ms(a, b) * 1e3 / steps
+            hip.destroy(a)
+            hip.destroy(b)
+            tf = 2.0 * M * n * k / (us * 1e-6) / 1e12
+            key = f"{name}_a{adt}"
+            res[key] = {"us": round(us, 2), "TFLOP/s": round(tf, 1), "frac_f16_peak": round(tf / F16_DENSE_PEAK_TFLOPS, 4)}
+            log(f"prefill M=512 {key}: {us:.1f} us, {tf:.1f} TFLOP/s ({tf / F16_DENSE_PEAK_TFLOPS * 100:.1f}% of f16 peak)")
+            del c
+        del w, x32
     return res
 
 

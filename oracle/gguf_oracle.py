@@ -271,16 +271,35 @@ def matmul_f64(ggml_type: int, A: np.ndarray, raw: np.ndarray, N: int, K: int) -
     return np.asarray(A, dtype=np.float64).reshape(-1, K) @ W.T
 
 
-def matmul_bf16_operands(ggml_type: int, A: np.ndarray, raw: np.ndarray, N: int, K: int) -> np.ndarray:
-    """fp64 product of bf16-rounded operands: bf16(A) @ bf16(dequant_f32(W)).T.
+def dequantize_f16_operands(ggml_type: int, raw: np.ndarray, num_elements: int) -> np.ndarray:
+    """Weights as the f16 MFMA operands of the prefill GEMM, returned as exact fp32.
 
-    This is the exact value a bf16-MFMA GEMM with fp32 accumulation approximates (only its
-    accumulation rounds), so it pins the prefill kernel's dequantization and k ordering far more
-    tightly than the fp64 tolerance does.
+    With ``w = a*code - b`` (``fields``): the group scale ``a`` and offset ``-b`` are each rounded
+    to f16 once (RNE), then ``w = f16(code*a16 + (-b)16)`` with a single rounding (a fused f16
+    multiply-add; ``b = 0`` for Q4_0 / Q8_0 / Q6_K, where it is an f16 multiply).  ``a`` is exact
+    in fp32 before its rounding (f16 ``d`` times a 6-bit or int8 sub-scale).  For Q4_0 / Q8_0 the
+    scale is ``d`` itself, so the result equals the reference CPU dequantizer's fp16 output
+    (src/gguf_parser.py:374-384, 408-415); for Q4_K / Q6_K rounding the scale first differs from
+    the reference's fp32 route (src/gguf_parser.py:471-502, 560-589) by at most one f16 ulp of the
+    weight.  ``code*a16 + b16`` is exact in fp64 for every representable field combination whose
+    two terms lie within 2^36 of each other, so the fp64 -> f16 cast is the one rounding.
     """
-    Wb = bf16_bits_to_f32(f32_to_bf16_bits(DEQUANT_F32[ggml_type](raw, N * K))).reshape(N, K)
-    Ab = bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(A, dtype=np.float32).reshape(-1, K)))
-    return Ab.astype(np.float64) @ Wb.astype(np.float64).T
+    a, code, b = fields(ggml_type, raw, num_elements)
+    a16 = a.astype(np.float16).astype(np.float64)
+    nb16 = (-b).astype(np.float16).astype(np.float64)
+    return (code.astype(np.float64) * a16 + nb16).astype(np.float16).astype(np.float32)
+
+
+def matmul_f16_operands(ggml_type: int, A: np.ndarray, raw: np.ndarray, N: int, K: int) -> np.ndarray:
+    """fp64 product of the prefill GEMM's f16 operands: f16(A) @ dequantize_f16_operands(W).T.
+
+    This is the exact value an f16-MFMA GEMM with fp32 accumulation approximates (only its
+    accumulation rounds), so it pins the prefill kernel's dequantization, scale rounding and k
+    ordering far more tightly than the fp64 tolerance does.
+    """
+    W16 = dequantize_f16_operands(ggml_type, raw, N * K).reshape(N, K).astype(np.float64)
+    A16 = np.asarray(A, dtype=np.float32).reshape(-1, K).astype(np.float16).astype(np.float64)
+    return A16 @ W16.T
 
 
 def max_rel_err(y: np.ndarray, y64: np.ndarray) -> float:

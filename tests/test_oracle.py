@@ -236,30 +236,103 @@ def test_mutation_q4_0_swapped_nibbles_detected(kat, monkeypatch):
 
 
 @pytest.mark.parametrize("t", TYPES)
-def test_matmul_reference_and_bf16_operands_brute_force(t):
+def test_matmul_reference_and_f16_operands_brute_force(t):
     # matmul_reference: the reference tests' formula (fp16-rounded dequantized weights, fp32
-    # accumulate); matmul_bf16_operands: both operands rounded to bf16, fp64 accumulate.  Each is
-    # checked against an explicit triple loop on a tiny case, so a transposed operand, a dropped
-    # rounding step or a wrong row stride fails here.
+    # accumulate); matmul_f16_operands: f16 activations times the prefill's f16 weight operands,
+    # fp64 accumulate.  Each is checked against an explicit triple loop on a tiny case, so a
+    # transposed operand, a dropped activation rounding or a wrong row stride fails here.
     rng = np.random.default_rng(314 + t)
     qk, _ = O.BLOCK_INFO[t]
     M, N, K = 3, 5, 2 * max(qk, 64)
     raw = O.synth_weights(t, N, K, rng)
     A = rng.standard_normal((M, K)).astype(np.float32)
     w16 = O.dequantize_f16(t, raw, N * K).astype(np.float64).reshape(N, K)
-    wb = O.bf16_bits_to_f32(O.f32_to_bf16_bits(O.DEQUANT_F32[t](raw, N * K))).astype(np.float64).reshape(N, K)
-    ab = O.bf16_bits_to_f32(O.f32_to_bf16_bits(A)).astype(np.float64)
+    wo = O.dequantize_f16_operands(t, raw, N * K).astype(np.float64).reshape(N, K)
     ref = np.zeros((M, N))
-    refb = np.zeros((M, N))
+    refo = np.zeros((M, N))
     for m in range(M):
         for n in range(N):
             s = 0.0
-            sb = 0.0
+            so = 0.0
             for k in range(K):
                 s += float(A[m, k]) * w16[n, k]
-                sb += ab[m, k] * wb[n, k]
+                so += float(np.float16(A[m, k])) * wo[n, k]
             ref[m, n] = s
-            refb[m, n] = sb
+            refo[m, n] = so
     got = O.matmul_reference(t, A, raw, N, K).astype(np.float64)
     assert np.max(np.abs(got - ref)) <= 1e-5 * np.max(np.abs(ref))
-    np.testing.assert_allclose(O.matmul_bf16_operands(t, A, raw, N, K), refb, rtol=1e-12, atol=1e-12 * np.max(np.abs(refb)))
+    np.testing.assert_allclose(O.matmul_f16_operands(t, A, raw, N, K), refo, rtol=1e-12, atol=1e-12 * np.max(np.abs(refo)))
+
+
+@pytest.mark.parametrize("t", [O.GGML_Q4_0, O.GGML_Q8_0])
+def test_f16_operands_equal_reference_dequant_for_block_scales(t):
+    # Q4_0 / Q8_0: the scale is the block's fp16 d, so code*d rounded once to f16 is exactly the
+    # reference CPU dequantizer's fp16 output (fp32 code*d is exact, then one cast).
+    rng = np.random.default_rng(77 + t)
+    raw = O.synth_weights(t, 64, 1024, rng)
+    np.testing.assert_array_equal(O.dequantize_f16_operands(t, raw, 64 * 1024),
+                                  O.dequantize_f16(t, raw, 64 * 1024).astype(np.float32))
+
+
+@pytest.mark.parametrize("t", [O.GGML_Q4_K, O.GGML_Q6_K])
+def test_f16_operands_error_bound_and_exact_cases(t):
+    # K-quants round the sub-block scale a (and the min b) to f16 before the code multiply, so
+    # |w16 - w| <= |code| * ulp(a16)/2 + ulp(b16)/2 + ulp(w16)/2 against the exact weight; the
+    # result equals the reference's fp32-then-fp16 weight whenever a and b are themselves f16
+    # values (power-of-two d, dmin).
+    rng = np.random.default_rng(91 + t)
+    raw = O.synth_weights(t, 64, 1024, rng)
+    n = 64 * 1024
+    a, code, b = O.fields(t, raw, n)
+    w = O.dequantize_f16_operands(t, raw, n).astype(np.float64)
+    half_ulp = lambda x: np.spacing(np.abs(x).astype(np.float16)).astype(np.float64) / 2
+    bound = np.abs(code) * half_ulp(a) + np.where(b != 0, half_ulp(b), 0.0) + half_ulp(w)
+    assert np.all(np.abs(w - (a * code - b)) <= bound)
+    assert np.any(w != O.dequantize_f16(t, raw, n))  # the two routes do differ on random scales
+    blk = raw.reshape(-1, O.BLOCK_INFO[t][1]).copy()
+    one = np.array([0.0078125], np.float16).view(np.uint8)  # 2^-7: every d*sc, dmin*m is an f16 value
+    if t == O.GGML_Q4_K:
+        blk[:, 0:2] = one
+        blk[:, 2:4] = one
+    else:
+        blk[:, 208:210] = one
+    raw2 = blk.reshape(-1)
+    np.testing.assert_array_equal(O.dequantize_f16_operands(t, raw2, n), O.dequantize_f16(t, raw2, n).astype(np.float32))
+
+
+def test_f16_operands_known_answers():
+    # Hand-worked f16 values (f16 has 10 fraction bits; ulp is 2^-9 on [2, 4), 2^-5 on [32, 64),
+    # 2^-4 on [64, 128)).  d = 1 + 2^-10 is an f16 value.
+    d = np.float16(1.0 + 2.0 ** -10)
+    # Q4_K sub-block 0: sc = 3, codes 15, no min.  d*sc = 3.0029296875 = 3 + 1.5 ulp, a tie that
+    # rounds to the even neighbour 3 + 2 ulp = 3.00390625; 15 * 3.00390625 = 45.05859375 =
+    # 1441.875 ulp -> 45.0625.  (The reference route rounds the exact 45.0439453125 -> 45.03125.)
+    # Sub-block 1: sc = 1 (d = 1 there via a second block), dmin*m = (1 + 2^-10)*3 -> 3.00390625
+    # as above; codes 5: 5 - 3.00390625 = 1.99609375 exactly.  (Reference: 5 - 3.0029296875 =
+    # 1.9970703125, also an f16 value.)
+    sc = np.zeros((2, 8), np.uint8)
+    m = np.zeros((2, 8), np.uint8)
+    q = np.zeros((2, 256), np.uint8)
+    sc[0, 0] = 3
+    q[0, 0:32] = 15
+    sc[1, 1] = 1
+    m[1, 1] = 3
+    q[1, 32:64] = 5
+    raw = O.pack_q4_k(np.array([d, 1.0], np.float16), np.array([0.0, d], np.float16), sc, m, q)
+    w = O.dequantize_f16_operands(O.GGML_Q4_K, raw, 512)
+    r = O.dequantize_f16(O.GGML_Q4_K, raw, 512)
+    assert np.all(w[0:32] == 45.0625) and np.all(r[0:32] == 45.03125)
+    assert np.all(w[256 + 32:256 + 64] == 1.99609375) and np.all(r[256 + 32:256 + 64] == 1.9970703125)
+    # Q6_K group 0 (sub-scale 0 covers weights 0..15): sc = 3, unsigned code 63 (q = 31):
+    # 31 * 3.00390625 = 93.12109375 = 1489.9375 ulp -> 93.125; sc = -3 gives -93.125.
+    # (Reference: 31 * 3.0029296875 = 93.0908203125 -> 93.0625.)
+    sc6 = np.zeros((1, 16), np.int8)
+    sc6[0, 0] = 3
+    sc6[0, 1] = -3
+    u = np.full((1, 256), 32, np.uint8)
+    u[0, 0:32] = 63
+    raw6 = O.pack_q6_k(np.array([d], np.float16), sc6, u)
+    w6 = O.dequantize_f16_operands(O.GGML_Q6_K, raw6, 256)
+    r6 = O.dequantize_f16(O.GGML_Q6_K, raw6, 256)
+    assert np.all(w6[0:16] == 93.125) and np.all(w6[16:32] == -93.125)
+    assert np.all(r6[0:16] == 93.0625)
