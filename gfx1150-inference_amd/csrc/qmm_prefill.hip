@@ -7,17 +7,20 @@
 //   * Operands are f16 (v_mfma_f32_32x32x16_f16, fp32 accumulation).  The reference's API hands
 //     over fp16 activations; f16 keeps three more mantissa bits than bf16 at the same MFMA rate.
 //     fp32 activations are rounded to f16 once by a conversion pass into a workspace.
-//   * A workgroup (4 waves) owns a 128 (m) x 256 (n) output tile and walks its K range in steps of
-//     64; wave w owns weight rows [64w, 64w + 64) of the tile and all 128 activation rows (4 x 2
-//     MFMA tiles of 32 x 32).
+//   * A workgroup (8 waves, two per SIMD, so one wave's memory stalls are covered by the other's
+//     MFMAs) owns a 128 (m) x 256 (n) output tile and walks its K range in steps of 128; wave w
+//     owns weight rows [32w, 32w + 32) of the tile and all 128 activation rows (4 MFMA tiles of
+//     32 x 32, fp32 accumulators in AGPRs).
 //   * Activation tiles are double-buffered in LDS: the next step's tile is loaded into registers
-//     while the current one is multiplied and written to the free slot at the end of the step
-//     (one barrier per step).  Rows are XOR-swizzled so fragment reads are bank-conflict free;
-//     each fragment is read once per step and feeds both of the wave's weight tiles.
+//     during the current step and written to the free slot near its end (one barrier per step).
+//     Rows are XOR-swizzled so fragment reads are bank-conflict free.
 //   * Each wave dequantizes its own weight rows straight into MFMA fragments with packed f16
 //     math: one v_perm makes two (1024 + code) f16 values, v_pk_add_f16 removes the offset
 //     exactly, v_pk_fma_f16 applies the group's scale and min (one rounding to f16).  Raw
 //     bytes are loaded one step ahead.
+//   * A step is software-pipelined in eight sub-steps of one 16-k MFMA block: while a sub-step's
+//     MFMAs run, the wave reads the next sub-step's activation fragments from LDS and
+//     dequantizes its weight fragment.
 //   * Narrow N (few tiles): the K range is split over workgroups; partial tiles land in a
 //     workspace and a second pass adds them in a fixed order (deterministic).
 //   * Tiles sharing a weight slice are placed on the same XCD (L2 reuse of the packed bytes).
@@ -32,10 +35,10 @@ namespace qmm {
 namespace {
 
 constexpr int kBM = 128;        // activation rows per workgroup tile
-constexpr int kBN = 256;        // weight rows per workgroup tile (64 per wave)
-constexpr int kBK = 64;         // k per step
-constexpr int kThreads = 256;
-constexpr int kChunksPerStage = kBM * kBK / 8;  // 16-byte chunks (8 f16) per stage = 1024
+constexpr int kBN = 256;        // weight rows per workgroup tile (32 per wave)
+constexpr int kBK = 128;        // k per step (two halves of 64)
+constexpr int kThreads = 512;   // 8 waves: two per SIMD, so one wave's load stalls are covered
+constexpr int kChunksPerHalf = kBM * 64 / 8;  // 16-byte chunks (8 f16) per 64-k half stage = 1024
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -85,199 +88,235 @@ __device__ __forceinline__ void bytes_to_h2(uint32_t x, h2 sub, h2& lo, h2& hi) 
 __device__ __forceinline__ uint32_t affine(h2 c, h2 a, h2 b) { return as_u32(__builtin_elementwise_fma(c, a, b)); }
 
 // ---------------------------------------------------------------------------------------------
-// Weight producers.  MFMA s (0..3) of a step and lane half h cover step-relative
-// k = 32*(s>>1) + 16*h + 8*(s&1) + (0..7); make() writes the 4 fragments (8 f16 each, natural k
-// order) of one weight row.
+// Weight producers.  A step covers 128 k as two halves U = 0, 1 of 64 and eight sub-steps
+// (U, S), S = 0..3, of one MFMA k-block (16 k) each.  In sub-step (U, S), lane half h covers
+// k = 64U + 32*(S>>1) + 16*h + 8*(S&1) + (0..7) of the step.
+//   load()        one weight row's raw bytes for the whole step (issued a step ahead);
+//   scales<U>()   the f16 scale (and offset) pairs of half U's two 32-weight groups;
+//   frag<U, S>()  the MFMA fragment (8 f16, natural k order) of sub-step (U, S).
+// kv = K - k0 lets the 32-weight formats zero a K tail; the zeroing happens in scales(), so no
+// prefetched value is consumed before its sub-step.
 // ---------------------------------------------------------------------------------------------
 struct PQ4K {
     static constexpr int kQK = kQK_K, kBytes = kBytesQ4_K;
-    struct Raw { u32x4p hd, q; };
-    // step at k0 (multiple of 64): super-block k0/256, qs chunk c = (k0/64)%4; lane half h takes
-    // qs bytes 16h..16h+15 of the chunk (low nibbles: sub-block 2c, high: 2c+1).
+    struct Raw { u32x4p hd, q0, q1; };
+    struct Sc { h2 a0, b0, a1, b1; };
+    // step at k0 (multiple of 128): super-block k0/256, qs chunks c = c0 + U with c0 = (k0/64)%4
+    // (0 or 2); lane half h takes qs bytes 16h..16h+15 of the chunk (low nibbles: sub-block 2c,
+    // high: 2c+1).
     __device__ static Raw load(const uint8_t* row, int k0, int h, int) {
         const uint8_t* sb = row + static_cast<size_t>(k0 >> 8) * kBytes;
+        const int c0 = (k0 >> 6) & 2;
         Raw r;
         r.hd = *reinterpret_cast<const u32x4p*>(sb);
-        r.q = *reinterpret_cast<const u32x4p*>(sb + 16 + 32 * ((k0 >> 6) & 3) + 16 * h);
+        r.q0 = *reinterpret_cast<const u32x4p*>(sb + 16 + 32 * c0 + 16 * h);
+        r.q1 = *reinterpret_cast<const u32x4p*>(sb + 48 + 32 * c0 + 16 * h);
         return r;
     }
-    __device__ static void make(const Raw& r, int k0, int, uint32_t f[4][4]) {
+    template <int U>
+    __device__ static Sc scales(const Raw& r, int k0, int, int) {
         // 6-bit scales/mins of sub-blocks 2c and 2c + 1 (bytes 2(c&1), 2(c&1)+1 of the packed
-        // scale words; sub-blocks 4..7 take their top bits from words 0/1).  c is uniform, so the
-        // choice is a select, not a branch.
-        const int c = (k0 >> 6) & 3;
-        const int sh = 16 * (c & 1);
+        // scale words; sub-blocks 4..7 take their top bits from words 0/1).  c >= 2 is uniform,
+        // so the choice is a select, not a branch.
+        const bool upper = ((k0 >> 6) & 2) != 0;
+        constexpr int sh = 16 * U;
         const uint32_t u0 = r.hd.y >> sh, u1 = r.hd.z >> sh, u2 = r.hd.w >> sh;
         const uint32_t sc_lo = u0 & 0x3F3Fu, m_lo = u1 & 0x3F3Fu;
         const uint32_t sc_hi = (u2 & 0x0F0Fu) | ((u0 >> 2) & 0x3030u);
         const uint32_t m_hi = ((u2 >> 4) & 0x0F0Fu) | ((u1 >> 2) & 0x3030u);
-        const uint32_t scp = c >= 2 ? sc_hi : sc_lo, mp = c >= 2 ? m_hi : m_lo;
-        const uint32_t sc0 = scp & 0xFFu, sc1 = (scp >> 8) & 0xFFu, m0 = mp & 0xFFu, m1 = (mp >> 8) & 0xFFu;
+        const uint32_t scp = upper ? sc_hi : sc_lo, mp = upper ? m_hi : m_lo;
         const float d = half_bits_to_float(r.hd.x), dmin = half_bits_to_float(r.hd.x >> 16);
-        const h2 a0 = splat(d * static_cast<float>(sc0)), b0 = splat(-(dmin * static_cast<float>(m0)));
-        const h2 a1 = splat(d * static_cast<float>(sc1)), b1 = splat(-(dmin * static_cast<float>(m1)));
+        Sc s;
+        s.a0 = splat(d * static_cast<float>(scp & 0xFFu));
+        s.b0 = splat(-(dmin * static_cast<float>(mp & 0xFFu)));
+        s.a1 = splat(d * static_cast<float>((scp >> 8) & 0xFFu));
+        s.b1 = splat(-(dmin * static_cast<float>((mp >> 8) & 0xFFu)));
+        return s;
+    }
+    template <int U, int S>
+    __device__ static void frag(const Raw& r, const Sc& sc, int, uint32_t f[4]) {
+        constexpr bool hi = S >= 2;  // high nibbles: sub-block 2c + 1
+        const u32x4p q = U ? r.q1 : r.q0;
+        const uint32_t w[2] = {(S & 1) ? q.z : q.x, (S & 1) ? q.w : q.y};
         const h2 off = splat(1024.0f);
-        const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const bool hi = s >= 2;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const uint32_t x = w[2 * (s & 1) + j];
-                const uint32_t codes = hi ? ((x >> 4) & 0x0F0F0F0Fu) : (x & 0x0F0F0F0Fu);
-                h2 p, q;
-                bytes_to_h2(codes, off, p, q);
-                f[s][2 * j] = affine(p, hi ? a1 : a0, hi ? b1 : b0);
-                f[s][2 * j + 1] = affine(q, hi ? a1 : a0, hi ? b1 : b0);
-            }
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t codes = hi ? ((w[j] >> 4) & 0x0F0F0F0Fu) : (w[j] & 0x0F0F0F0Fu);
+            h2 p, qq;
+            bytes_to_h2(codes, off, p, qq);
+            f[2 * j] = affine(p, hi ? sc.a1 : sc.a0, hi ? sc.b1 : sc.b0);
+            f[2 * j + 1] = affine(qq, hi ? sc.a1 : sc.a0, hi ? sc.b1 : sc.b0);
         }
     }
 };
 
 struct PQ6K {
     static constexpr int kQK = kQK_K, kBytes = kBytesQ6_K;
-    struct Raw { u32x4p la, lb, qh; uint32_t sc, d; };
-    // step at k0: super-block k0/256, quarter qt = (k0/64)%4 -> half n2 = qt/2, groups t = 2(qt&1) + (s>>1);
-    // lane half h takes l = 16h..16h+15 of ql (groups t even: ql[64n2 + l], odd: ql[64n2 + 32 + l]) and qh.
+    struct Raw { u32x4p la, lb, qh; uint32_t sc0, sc1, d; };
+    struct Sc { h2 a0, a1; };
+    // step at k0 (multiple of 128): super-block k0/256, half n2 = (k0/128)%2, quarter qt = 2n2 + U,
+    // groups t = 2U + (S>>1).  Lane half h takes l = 16h..16h+15 of ql (groups t even:
+    // ql[64n2 + l], odd: ql[64n2 + 32 + l]; both halves U share these bytes, U picks the nibble)
+    // and of qh[32n2 + l].
     __device__ static Raw load(const uint8_t* row, int k0, int h, int) {
         const uint8_t* sb = row + static_cast<size_t>(k0 >> 8) * kBytes;
-        const int qt = (k0 >> 6) & 3, n2 = qt >> 1;
+        const int n2 = (k0 >> 7) & 1;
         Raw r;
         r.la = ld16(sb + 64 * n2 + 16 * h);
         r.lb = ld16(sb + 64 * n2 + 32 + 16 * h);
         r.qh = ld16(sb + 128 + 32 * n2 + 16 * h);
-        r.sc = ld4(sb + 192 + 8 * n2 + 4 * (qt & 1));  // sc[.. + h + {0, 2}]
+        r.sc0 = ld4(sb + 192 + 8 * n2);  // sc[8n2 + 4U + h + {0, 2}]
+        r.sc1 = ld4(sb + 196 + 8 * n2);
         r.d = ld2(sb + 208);
         return r;
     }
-    __device__ static void make(const Raw& r, int k0, int h, uint32_t f[4][4]) {
-        const int qt = (k0 >> 6) & 3;
-        const int nib = 4 * (qt & 1);
+    template <int U>
+    __device__ static Sc scales(const Raw& r, int, int h, int) {
+        const uint32_t sc = U ? r.sc1 : r.sc0;
         const float d = half_bits_to_float(r.d);
-        const h2 a0 = splat(d * static_cast<float>(static_cast<int8_t>(r.sc >> (8 * h))));
-        const h2 a1 = splat(d * static_cast<float>(static_cast<int8_t>(r.sc >> (8 * h + 16))));
+        Sc s;
+        s.a0 = splat(d * static_cast<float>(static_cast<int8_t>(sc >> (8 * h))));
+        s.a1 = splat(d * static_cast<float>(static_cast<int8_t>(sc >> (8 * h + 16))));
+        return s;
+    }
+    template <int U, int S>
+    __device__ static void frag(const Raw& r, const Sc& sc, int, uint32_t f[4]) {
+        constexpr int nib = 4 * U, u = S >> 1;  // group t = 2U + u
+        constexpr int hs = nib + 2 * u;         // qh bit pair of the group
+        const u32x4p l = u ? r.lb : r.la;
+        const uint32_t lw[2] = {(S & 1) ? l.z : l.x, (S & 1) ? l.w : l.y};
+        const uint32_t hw[2] = {(S & 1) ? r.qh.z : r.qh.x, (S & 1) ? r.qh.w : r.qh.y};
         const h2 off = splat(1056.0f);  // 1024 + 32: codes q enter as 1024 + q, weight is a (q - 32)
-        const uint32_t la[4] = {r.la.x, r.la.y, r.la.z, r.la.w};
-        const uint32_t lb[4] = {r.lb.x, r.lb.y, r.lb.z, r.lb.w};
-        const uint32_t qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+        const h2 a = u ? sc.a1 : sc.a0;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int u = s >> 1;  // group t = 2(qt&1) + u
-            const int hs = nib + 2 * u;  // qh bit pair of the group
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int i = 2 * (s & 1) + j;
-                const uint32_t lo4 = ((u ? lb[i] : la[i]) >> nib) & 0x0F0F0F0Fu;
-                const uint32_t hi2 = ((qh[i] >> hs) & 0x03030303u) << 4;
-                h2 p, q;
-                bytes_to_h2(lo4 | hi2, off, p, q);
-                const h2 a = u ? a1 : a0;
-                f[s][2 * j] = as_u32(p * a);
-                f[s][2 * j + 1] = as_u32(q * a);
-            }
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t lo4 = (lw[j] >> nib) & 0x0F0F0F0Fu;
+            const uint32_t hi2 = ((hw[j] >> hs) & 0x03030303u) << 4;
+            h2 p, q;
+            bytes_to_h2(lo4 | hi2, off, p, q);
+            f[2 * j] = as_u32(p * a);
+            f[2 * j + 1] = as_u32(q * a);
         }
     }
 };
 
+// 32-weight block formats: a step covers blocks k0/32 + b, b = 0..3 (block b absent when
+// kv <= 32b: load() clamps its address to block 0 and scales() zeroes its scale).  Half U
+// holds blocks 2U (S = 0, 1) and 2U + 1 (S = 2, 3).
 struct PQ80 {
     static constexpr int kQK = kQK8_0, kBytes = kBytesQ8_0;
-    struct Raw { u32x4p q0, q1; uint32_t d0, d1; };
-    // step at k0: blocks k0/32 (k 0..31) and k0/32 + 1 (k 32..63, absent on a K tail)
+    struct Raw { u32x4p q[4]; uint32_t d[4]; };
+    struct Sc { h2 a0, a1; };
     __device__ static Raw load(const uint8_t* row, int k0, int h, int kv) {
         const uint8_t* b0 = row + static_cast<size_t>(k0 >> 5) * kBytes;
-        const uint8_t* b1 = kv > 32 ? b0 + kBytes : b0;
         Raw r;
-        r.q0 = ld16(b0 + 2 + 16 * h);
-        r.q1 = ld16(b1 + 2 + 16 * h);
-        r.d0 = ld2(b0);
-        const uint32_t d1 = ld2(b1);  // always issued (static load count); zero scale on a K tail
-        r.d1 = kv > 32 ? d1 : 0u;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const uint8_t* bb = kv > 32 * b ? b0 + b * kBytes : b0;
+            r.q[b] = ld16(bb + 2 + 16 * h);
+            r.d[b] = ld2(bb);  // always issued (static load count)
+        }
         return r;
     }
-    __device__ static void make(const Raw& r, int, int, uint32_t f[4][4]) {
-        const h2 a0 = splat(half_bits_to_float(r.d0)), a1 = splat(half_bits_to_float(r.d1));
+    template <int U>
+    __device__ static Sc scales(const Raw& r, int, int, int kv) {
+        Sc s;
+        s.a0 = splat(half_bits_to_float(kv > 64 * U ? r.d[2 * U] : 0u));
+        s.a1 = splat(half_bits_to_float(kv > 64 * U + 32 ? r.d[2 * U + 1] : 0u));
+        return s;
+    }
+    template <int U, int S>
+    __device__ static void frag(const Raw& r, const Sc& sc, int, uint32_t f[4]) {
+        constexpr int u = S >> 1;
+        const u32x4p q = r.q[2 * U + u];
+        const uint32_t w[2] = {(S & 1) ? q.z : q.x, (S & 1) ? q.w : q.y};
         const h2 off = splat(1152.0f);  // signed codes enter as 1024 + (q + 128)
-        const uint32_t q0[4] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w};
-        const uint32_t q1[4] = {r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        const h2 a = u ? sc.a1 : sc.a0;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int u = s >> 1;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int i = 2 * (s & 1) + j;
-                h2 p, q;
-                bytes_to_h2((u ? q1[i] : q0[i]) ^ 0x80808080u, off, p, q);
-                const h2 a = u ? a1 : a0;
-                f[s][2 * j] = as_u32(p * a);
-                f[s][2 * j + 1] = as_u32(q * a);
-            }
+        for (int j = 0; j < 2; ++j) {
+            h2 p, qq;
+            bytes_to_h2(w[j] ^ 0x80808080u, off, p, qq);
+            f[2 * j] = as_u32(p * a);
+            f[2 * j + 1] = as_u32(qq * a);
         }
     }
 };
 
 struct PQ40 {
     static constexpr int kQK = kQK4_0, kBytes = kBytesQ4_0;
-    struct Raw { u32x4p q0, q1; uint32_t d0, d1; };
-    // step at k0: blocks k0/32 and k0/32 + 1; lane half h takes the block's low (h = 0, k 0..15)
-    // or high (h = 1, k 16..31) nibbles.
+    struct Raw { u32x4p q[4]; uint32_t d[4]; };
+    struct Sc { h2 a0, a1; };
+    // lane half h takes the block's low (h = 0, k 0..15) or high (h = 1, k 16..31) nibbles.
     __device__ static Raw load(const uint8_t* row, int k0, int, int kv) {
         const uint8_t* b0 = row + static_cast<size_t>(k0 >> 5) * kBytes;
-        const uint8_t* b1 = kv > 32 ? b0 + kBytes : b0;
         Raw r;
-        r.q0 = ld16(b0 + 2);
-        r.q1 = ld16(b1 + 2);
-        r.d0 = ld2(b0);
-        const uint32_t d1 = ld2(b1);  // always issued (static load count); zero scale on a K tail
-        r.d1 = kv > 32 ? d1 : 0u;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const uint8_t* bb = kv > 32 * b ? b0 + b * kBytes : b0;
+            r.q[b] = ld16(bb + 2);
+            r.d[b] = ld2(bb);  // always issued (static load count)
+        }
         return r;
     }
-    __device__ static void make(const Raw& r, int, int h, uint32_t f[4][4]) {
-        const h2 a0 = splat(half_bits_to_float(r.d0)), a1 = splat(half_bits_to_float(r.d1));
+    template <int U>
+    __device__ static Sc scales(const Raw& r, int, int, int kv) {
+        Sc s;
+        s.a0 = splat(half_bits_to_float(kv > 64 * U ? r.d[2 * U] : 0u));
+        s.a1 = splat(half_bits_to_float(kv > 64 * U + 32 ? r.d[2 * U + 1] : 0u));
+        return s;
+    }
+    template <int U, int S>
+    __device__ static void frag(const Raw& r, const Sc& sc, int h, uint32_t f[4]) {
+        constexpr int u = S >> 1;
+        const u32x4p q = r.q[2 * U + u];
+        const uint32_t w[2] = {(S & 1) ? q.z : q.x, (S & 1) ? q.w : q.y};
         const h2 off = splat(1032.0f);  // codes enter as 1024 + q, weight is d (q - 8)
-        const uint32_t q0[4] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w};
-        const uint32_t q1[4] = {r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        const h2 a = u ? sc.a1 : sc.a0;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int u = s >> 1;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int i = 2 * (s & 1) + j;
-                h2 p, q;
-                bytes_to_h2(((u ? q1[i] : q0[i]) >> (4 * h)) & 0x0F0F0F0Fu, off, p, q);
-                const h2 a = u ? a1 : a0;
-                f[s][2 * j] = as_u32(p * a);
-                f[s][2 * j + 1] = as_u32(q * a);
-            }
+        for (int j = 0; j < 2; ++j) {
+            h2 p, qq;
+            bytes_to_h2((w[j] >> (4 * h)) & 0x0F0F0F0Fu, off, p, qq);
+            f[2 * j] = as_u32(p * a);
+            f[2 * j + 1] = as_u32(qq * a);
         }
     }
 };
 
-template <class P>
-constexpr int raw_loads() {
-    return std::is_same<P, PQ4K>::value ? 2 : std::is_same<P, PQ6K>::value ? 5 : 4;
-}
-
-// Activation chunk (row r, chunk c = 8 f16) position inside a 1024-chunk stage: rows are
+// Activation chunk (row r, chunk c = 8 f16) position inside a 1024-chunk half stage: rows are
 // XOR-swizzled so that 16 consecutive rows read at one chunk hit 16 different bank groups.
 __device__ __forceinline__ int a_slot(int r, int c) { return 8 * r + (c ^ ((r >> 1) & 7)); }
 
-// MFMA s, lane half h -> activation chunk of the step.
+// Sub-step S, lane half h -> activation chunk of the half stage.
 __device__ __forceinline__ int a_chunk(int s, int h) { return 4 * (s >> 1) + 2 * h + (s & 1); }
 
-// Workgroup barrier for LDS traffic only: this wave's LDS writes are complete, then s_barrier.
-// Unlike __syncthreads() it does not wait for outstanding global loads (the prefetches stay in
-// flight); the empty asm statements keep the compiler from moving memory operations across it.
+// Workgroup barrier for LDS traffic only: this wave's LDS operations are complete, then
+// s_barrier.  Unlike __syncthreads() it does not wait for outstanding global loads (the
+// prefetches stay in flight); the empty asm statements keep the compiler from moving memory
+// operations across it.
 __device__ __forceinline__ void lds_barrier() {
     __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     __asm__ volatile("" ::: "memory");
 }
 
+// Instruction interleave of one sub-step for the scheduler: four rounds of one MFMA, one LDS read
+// and a few VALU operations, so the dequantization of the next sub-step runs while the matrix
+// core works on this one.
+template <int V>
+__device__ __forceinline__ void interleave_substep() {
+#define QMM_PF_ROUND                                   \
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); \
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); \
+    __builtin_amdgcn_sched_group_barrier(0x002, V, 0);
+    QMM_PF_ROUND QMM_PF_ROUND QMM_PF_ROUND QMM_PF_ROUND
+#undef QMM_PF_ROUND
+}
+
 template <class P, typename TC>
 __global__ __launch_bounds__(kThreads, 1)
 void prefill_kernel(const _Float16* __restrict__ A16, int lda, const uint8_t* __restrict__ W, TC* __restrict__ C,
                     float* __restrict__ part, int M, int N, int K, int klen, int tiles_m, int tiles_n, int ksplit) {
-    __shared__ __align__(16) u32x4p sA[2][kChunksPerStage];
+    __shared__ __align__(16) u32x4p sA[2][2 * kChunksPerHalf];
 
     // Tile order: m fastest, then n-tile, then k split; blocks sharing a weight slice (same
     // n-tile and k range, different m) are consecutive and dealt to one XCD.
@@ -299,17 +338,16 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, const uint8_t* __
     const int l32 = lane & 31;
 
     const size_t row_bytes = static_cast<size_t>(K / P::kQK) * P::kBytes;
-    const uint8_t* wrow[2];
-#pragma unroll
-    for (int r = 0; r < 2; ++r) wrow[r] = W + static_cast<size_t>(min(n0 + 64 * wv + 32 * r + l32, N - 1)) * row_bytes;
+    const uint8_t* wrow = W + static_cast<size_t>(min(n0 + 32 * wv + l32, N - 1)) * row_bytes;
 
-    // Thread tid copies stage chunks p = tid + 256 j (j = 0..3): row p >> 3, chunk (p & 7) ^ swizzle,
-    // so each thread's 4 global reads are 16-byte aligned f16 runs and its LDS writes are in place.
-    const _Float16* arow[4];
-    int apos[4];
+    // Thread tid copies half-stage chunks p = tid + 512 j (j = 0..1) of both halves: row p >> 3,
+    // chunk (p & 7) ^ swizzle, so each thread's 4 global reads are 16-byte aligned f16 runs and
+    // its LDS writes are in place.
+    const _Float16* arow[2];
+    int apos[2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int p = tid + 256 * j;
+    for (int j = 0; j < 2; ++j) {
+        const int p = tid + 512 * j;
         const int r = p >> 3;
         const int c = (p & 7) ^ ((r >> 1) & 7);
         arow[j] = A16 + static_cast<size_t>(min(m0 + r, M - 1)) * lda + kb + 8 * c;
@@ -318,95 +356,126 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, const uint8_t* __
     auto load_a = [&](int t, u32x4p (&ar)[4]) {
         const int kk = min(t, nsteps - 1) * kBK;  // past the end: re-read the last step
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ar[j] = *reinterpret_cast<const u32x4p*>(arow[j] + kk);
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) ar[2 * u + j] = *reinterpret_cast<const u32x4p*>(arow[j] + kk + 64 * u);
     };
     auto store_a = [&](int slot, const u32x4p (&ar)[4]) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sA[slot][apos[j]] = ar[j];
-    };
-    auto load_raw = [&](int t, typename P::Raw (&raw)[2]) {
-        const int k0 = kb + min(t, nsteps - 1) * kBK;
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int r = 0; r < 2; ++r) raw[r] = P::load(wrow[r], k0, h, kend - k0);
+            for (int j = 0; j < 2; ++j) sA[slot][kChunksPerHalf * u + apos[j]] = ar[2 * u + j];
+    };
+    auto load_raw = [&](int t, typename P::Raw& raw) {
+        const int k0 = kb + min(t, nsteps - 1) * kBK;
+        raw = P::load(wrow, k0, h, kend - k0);
+    };
+    // activation fragments of sub-step (U, S) of the step held in `slot`
+    auto read_a = [&](int slot, int U, int S, f16x8 (&af)[4]) {
+        const u32x4p* sa = sA[slot] + kChunksPerHalf * U;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32x4p av = sa[a_slot(32 * i + l32, a_chunk(S, h))];
+            __builtin_memcpy(&af[i], &av, 16);
+        }
     };
 
-    f32x16 acc[4][2];
+    f32x16 acc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int r = 0; r < 2; ++r)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][r][v] = 0.0f;
+        for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
 
-    // Pipeline: at step t the LDS slot t%2 holds A(t); A(t+1) and the raw weight bytes of step t+1
-    // are in flight in registers while step t is multiplied.  At the end of the step A(t+1) goes
-    // to the other slot and the raw bytes move into `cur`.  One loop body keeps the accumulators
-    // in place (no register renaming across unrolled copies).
+    // Software pipeline.  Step t (k0 = kb + 128t) runs sub-steps q = 0..7 (U = q/4, S = q%4).
+    // While the 4 MFMAs of sub-step q run on wf[q&1] / af[q&1], the wave reads the activation
+    // fragments of q+1 from LDS and dequantizes its weight fragments into the other buffers.
+    //   q = 0: the raw bytes of step t+1 (into `nxt`) and A(t+1) (into `an`) are requested;
+    //   q = 1: scales of half 1 (from `cur`);  q = 5: scales of the next step's half 0 (`nxt`);
+    //   q = 6: after the reads for q = 7, A(t+1) goes to the free LDS slot, then the barrier
+    //          (after it, q = 7 reads the next step's first fragments from that slot);
+    //   q = 7: fragments of the next step's (0, 0) from `nxt`; at the end `cur` takes `nxt`.
+    // The LDS slot (t+1)%2 last served step t-1, whose reads all precede step t-1's barrier, so
+    // one barrier per step covers both the write-after-read and the read-after-write order.
+    using Raw = typename P::Raw;
+    using Sc = typename P::Sc;
     u32x4p an[4];
-    typename P::Raw cur[2], nxt[2];
-    load_a(0, an);
+    Raw cur, nxt;
+    Sc sc[2];          // [half]
+    uint32_t wf[2][4]; // [buffer][dword]
+    f16x8 af[2][4];    // [buffer][i]
+
     load_raw(0, cur);
+    load_a(0, an);
     store_a(0, an);
     lds_barrier();
+    sc[0] = P::template scales<0>(cur, kb, h, kend - kb);
+    P::template frag<0, 0>(cur, sc[0], h, wf[0]);
+    read_a(0, 0, 0, af[0]);
 
     for (int t = 0; t < nsteps; ++t) {
-        load_a(t + 1, an);
-        load_raw(t + 1, nxt);
-        // Keep the prefetches at the top of the step: left alone, the scheduler sinks them next
-        // to their uses at the end of the step and their latency is no longer hidden.
-        __builtin_amdgcn_sched_barrier(0);
         const int k0 = kb + t * kBK;
-        uint32_t wf[2][4][4];
-#pragma unroll
-        for (int r = 0; r < 2; ++r) P::make(cur[r], k0, h, wf[r]);
-        const u32x4p* sa = sA[t & 1];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            f16x8 af[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const u32x4p av = sa[a_slot(32 * i + l32, a_chunk(s, h))];
-                __builtin_memcpy(&af[i], &av, 16);
+        const int slot = t & 1;
+        // raw bytes first: they are consumed (q = 5) before A(t+1) is (q = 6)
+        load_raw(t + 1, nxt);
+        load_a(t + 1, an);
+        __builtin_amdgcn_sched_barrier(0);
+
+        auto sub = [&](auto qc) {
+            constexpr int q = decltype(qc)::value;
+            constexpr int U = q >> 2, S = q & 3, B = q & 1;
+            constexpr int qn = q + 1, Un = (qn >> 2) & 1, Sn = qn & 3;
+            if constexpr (qn < 8) read_a(slot, Un, Sn, af[B ^ 1]);
+            if constexpr (q == 6) {
+                // free slot <- A(t+1).  The barrier comes after the last reads of this step's slot
+                // (those of q = 7, just issued), so the next step may overwrite it.
+                store_a(slot ^ 1, an);
+                lds_barrier();
             }
+            if constexpr (qn == 8) read_a(slot ^ 1, 0, 0, af[B ^ 1]);
+            if constexpr (q == 1) sc[1] = P::template scales<1>(cur, k0, h, kend - k0);
+            if constexpr (q == 5) sc[0] = P::template scales<0>(nxt, k0 + kBK, h, kend - k0 - kBK);
+            if constexpr (qn < 8) P::template frag<Un, Sn>(cur, sc[Un], h, wf[B ^ 1]);
+            else P::template frag<0, 0>(nxt, sc[0], h, wf[B ^ 1]);
+            f16x8 bw;
+            __builtin_memcpy(&bw, wf[B], 16);
 #pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                f16x8 bw;
-                __builtin_memcpy(&bw, wf[r][s], 16);
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    acc[i][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bw, af[i], acc[i][r], 0, 0, 0);
-            }
-        }
-        store_a((t + 1) & 1, an);
-        lds_barrier();
-#pragma unroll
-        for (int r = 0; r < 2; ++r) cur[r] = nxt[r];
+            for (int i = 0; i < 4; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bw, af[B][i], acc[i], 0, 0, 0);
+            interleave_substep<5>();
+            __builtin_amdgcn_sched_barrier(0);
+            (void)U; (void)S;
+        };
+        sub(std::integral_constant<int, 0>{});
+        sub(std::integral_constant<int, 1>{});
+        sub(std::integral_constant<int, 2>{});
+        sub(std::integral_constant<int, 3>{});
+        sub(std::integral_constant<int, 4>{});
+        sub(std::integral_constant<int, 5>{});
+        sub(std::integral_constant<int, 6>{});
+        sub(std::integral_constant<int, 7>{});
+        cur = nxt;
     }
 
-    // D element v of tile (i, r): weight row n = n0 + 64wv + 32r + 8(v/4) + 4h + v%4,
-    // activation row m = m0 + 32i + l32.
+    // D element v of tile i: weight row n = n0 + 32wv + 8(v/4) + 4h + v%4, activation row
+    // m = m0 + 32i + l32.
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int m = m0 + 32 * i + l32;
         if (m >= M) continue;
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int g = 0; g < 4; ++g) {
+            const int n = n0 + 32 * wv + 8 * g + 4 * h;
+            const float vs[4] = {acc[i][4 * g], acc[i][4 * g + 1], acc[i][4 * g + 2], acc[i][4 * g + 3]};
+            if (ksplit > 1) {
+                float* dst = part + (static_cast<size_t>(kz) * M + m) * N;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int n = n0 + 64 * wv + 32 * r + 8 * g + 4 * h;
-                const float vs[4] = {acc[i][r][4 * g], acc[i][r][4 * g + 1], acc[i][r][4 * g + 2], acc[i][r][4 * g + 3]};
-                if (ksplit > 1) {
-                    float* dst = part + (static_cast<size_t>(kz) * M + m) * N;
+                for (int e = 0; e < 4; ++e)
+                    if (n + e < N) dst[n + e] = vs[e];
+            } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (n + e < N) dst[n + e] = vs[e];
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        if (n + e < N) {
-                            if constexpr (sizeof(TC) == 4) reinterpret_cast<float*>(C)[static_cast<size_t>(m) * N + n + e] = vs[e];
-                            else reinterpret_cast<uint16_t*>(C)[static_cast<size_t>(m) * N + n + e] = float_to_half_bits(vs[e]);
-                        }
+                for (int e = 0; e < 4; ++e) {
+                    if (n + e < N) {
+                        if constexpr (sizeof(TC) == 4) reinterpret_cast<float*>(C)[static_cast<size_t>(m) * N + n + e] = vs[e];
+                        else reinterpret_cast<uint16_t*>(C)[static_cast<size_t>(m) * N + n + e] = float_to_half_bits(vs[e]);
                     }
                 }
             }
@@ -504,9 +573,9 @@ hipError_t launch_p(const void* A, const void* W, void* C, int M, int N, int K, 
     const int tiles_n = (N + kBN - 1) / kBN;
     const int steps = (K + kBK - 1) / kBK;
     // split K while the grid would still cover at most half the CUs (the partial-sum pass costs
-    // 4 * (ksplit + 1) * M * N bytes), keeping at least 16 steps per split
+    // 4 * (ksplit + 1) * M * N bytes), keeping at least 8 steps per split
     int ksplit = 1;
-    while (tiles_m * tiles_n * ksplit * 2 <= cus && steps / (ksplit * 2) >= 16) ksplit *= 2;
+    while (tiles_m * tiles_n * ksplit * 2 <= cus && steps / (ksplit * 2) >= 8) ksplit *= 2;
     const int klen = ((steps + ksplit - 1) / ksplit) * kBK;
     ksplit = (steps * kBK + klen - 1) / klen;
 
