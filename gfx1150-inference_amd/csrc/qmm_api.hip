@@ -112,6 +112,44 @@ hipError_t ws_ensure(Workspace& ws, const size_t need[3]) {
     return hipSuccess;
 }
 
+// Byte ranges for the fusion checks of qmm_gemm_batch.
+struct Span {
+    uintptr_t lo, hi;
+    bool overlaps(const Span& o) const { return lo < o.hi && o.lo < hi; }
+};
+Span span_of(const void* p, size_t bytes) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    return Span{a, a + bytes};
+}
+size_t dtype_bytes(int dt) { return dt == QMM_DTYPE_F32 ? 4 : 2; }
+Span a_span(const qmm_gemm_desc& d) { return span_of(d.A, static_cast<size_t>(d.M) * d.K * dtype_bytes(d.a_dtype)); }
+Span w_span(const qmm_gemm_desc& d) {
+    return span_of(d.W, static_cast<size_t>(d.N) * (d.K / qmm::block_elems(d.ggml_type)) * qmm::block_bytes(d.ggml_type));
+}
+Span c_span(const qmm_gemm_desc& d) { return span_of(d.C, static_cast<size_t>(d.M) * d.N * dtype_bytes(d.c_dtype)); }
+
+// Descriptors [i, j) may run as one GEMV launch: same activations, dtypes, type, M and K; GEMV
+// sizes; no events between them; and no output overlapping another output or any input, so the
+// fused launch computes exactly what the sequential launches would.
+bool fusable(const qmm_gemm_desc* d, int i, int j) {
+    const qmm_gemm_desc& h = d[i];
+    if (h.M <= 0 || h.M >= qmm::kGemvMaxM) return false;
+    for (int x = i; x < j; ++x) {
+        const qmm_gemm_desc& e = d[x];
+        if (e.N <= 0 || e.A != h.A || e.a_dtype != h.a_dtype || e.ggml_type != h.ggml_type ||
+            e.c_dtype != h.c_dtype || e.M != h.M || e.K != h.K)
+            return false;
+        if ((x > i && e.ev_before) || (x + 1 < j && e.ev_after)) return false;
+        const Span c = c_span(e);
+        if (c.overlaps(a_span(h))) return false;
+        for (int y = i; y < j; ++y) {
+            if (y != x && c.overlaps(c_span(d[y]))) return false;
+            if (c.overlaps(w_span(d[y]))) return false;
+        }
+    }
+    return true;
+}
+
 int matmul_host(int t, const void* hA, const void* hB, void* hC, int M, int N, int K) {
     int rc = check_gemm_args(t, hA, QMM_DTYPE_F16, hB, hC, QMM_DTYPE_F16, M, N, K);
     if (rc != QMM_OK) return rc;
@@ -185,15 +223,48 @@ int qmm_gemm_batch(const qmm_gemm_desc* descs, int count, void* stream) {
         if (rc != QMM_OK) return fail(rc, "descriptor " + std::to_string(i) + ": " + g_last_error);
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
-    for (int i = 0; i < count; ++i) {
-        const qmm_gemm_desc& d = descs[i];
+    auto record = [&](void* ev) -> int {
         hipError_t e;
-        if (d.ev_before && (e = hipEventRecord(static_cast<hipEvent_t>(d.ev_before), s)) != hipSuccess)
-            return hip_fail(e, "hipEventRecord");
-        int rc = gemm_impl(d.ggml_type, d.A, d.a_dtype, d.W, d.C, d.c_dtype, d.M, d.N, d.K, s);
+        if (ev && (e = hipEventRecord(static_cast<hipEvent_t>(ev), s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
+        return QMM_OK;
+    };
+    const int max_fused = qmm::gemv_max_fused();
+    int i = 0;
+    while (i < count) {
+        // longest run starting at i that one GEMV launch can serve
+        int j = i + 1;
+        while (j < count && j - i < max_fused && fusable(descs, i, j + 1)) ++j;
+        if (j - i >= 2) {
+            const void* W[8];
+            void* C[8];
+            int N[8];
+            for (int x = i; x < j; ++x) {
+                W[x - i] = descs[x].W;
+                C[x - i] = descs[x].C;
+                N[x - i] = descs[x].N;
+            }
+            const qmm_gemm_desc& h = descs[i];
+            int rc = record(h.ev_before);
+            if (rc != QMM_OK) return rc;
+            hipError_t e = qmm::launch_gemv_fused(h.ggml_type, h.A, h.a_dtype, h.c_dtype, h.M, h.K, W, C, N, j - i, s);
+            if (e == hipSuccess) {
+                if ((rc = record(descs[j - 1].ev_after)) != QMM_OK) return rc;
+                i = j;
+                continue;
+            }
+            if (e != hipErrorNotSupported) return hip_fail(e, "qmm_gemm_batch fused kernel launch");
+            // not fusable after all (e.g. byte-load fallback): run the first one alone
+            if ((rc = gemm_impl(h.ggml_type, h.A, h.a_dtype, h.W, h.C, h.c_dtype, h.M, h.N, h.K, s)) != QMM_OK) return rc;
+            if ((rc = record(h.ev_after)) != QMM_OK) return rc;
+            ++i;
+            continue;
+        }
+        const qmm_gemm_desc& d = descs[i];
+        int rc = record(d.ev_before);
         if (rc != QMM_OK) return rc;
-        if (d.ev_after && (e = hipEventRecord(static_cast<hipEvent_t>(d.ev_after), s)) != hipSuccess)
-            return hip_fail(e, "hipEventRecord");
+        if ((rc = gemm_impl(d.ggml_type, d.A, d.a_dtype, d.W, d.C, d.c_dtype, d.M, d.N, d.K, s)) != QMM_OK) return rc;
+        if ((rc = record(d.ev_after)) != QMM_OK) return rc;
+        ++i;
     }
     return QMM_OK;
 }

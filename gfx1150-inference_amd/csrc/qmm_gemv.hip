@@ -20,6 +20,7 @@
 //     so every M < kGemvMaxM is bit-identical to M = 1 (the reference's prefill-vs-M=1
 //     invariant, tests/test_phase5_scale.py:274-310); the cross-lane reduction is a fixed DPP
 //     sequence (no atomics, deterministic).
+#include <climits>
 #include <mutex>
 #include <string>
 #include <type_traits>
@@ -537,6 +538,35 @@ __device__ __forceinline__ void reduce_store(float (&acc)[MR][YT], TC* __restric
     }
 }
 
+// Weight matrices multiplied by the same activations in one launch (e.g. the q, k and v
+// projections): their row groups are concatenated; segment s owns row groups
+// [gend[s-1], gend[s]).  Unused entries have gend = INT_MAX.
+constexpr int kMaxSegs = 4;
+template <typename TC>
+struct GemvSegs {
+    const uint8_t* W[kMaxSegs];
+    TC* C[kMaxSegs];
+    int N[kMaxSegs];
+    int gend[kMaxSegs];
+};
+
+// Segment of row group g (wave-uniform): its weights, output, rows and first row group.
+template <typename TC>
+struct SegRef {
+    const uint8_t* W;
+    TC* C;
+    int N, g0;
+};
+template <typename TC>
+__device__ __forceinline__ SegRef<TC> seg_of(const GemvSegs<TC>& sg, int g) {
+    SegRef<TC> r{sg.W[0], sg.C[0], sg.N[0], 0};
+#pragma unroll
+    for (int j = 1; j < kMaxSegs; ++j) {
+        if (g >= sg.gend[j - 1]) r = SegRef<TC>{sg.W[j], sg.C[j], sg.N[j], sg.gend[j - 1]};
+    }
+    return r;
+}
+
 // Resident-activation kernel: the workgroup stages all windows of its MR activation rows once,
 // then every wave streams (row group, window) items (YT rows each) round-robin over the grid.
 // Three register buffers rotate statically: while item i is multiplied, items i+1 and i+2 are
@@ -544,8 +574,7 @@ __device__ __forceinline__ void reduce_store(float (&acc)[MR][YT], TC* __restric
 // Dynamic LDS: MR * nwin * 9216 bytes.
 template <class F, int MR, int YT, int NW, typename TA, typename TC>
 __global__ __launch_bounds__(64 * NW, QMM_GEMV_MIN_WAVES)
-void gemv_resident_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W, TC* __restrict__ C,
-                          int M, int N, int K, int a_vec, int nrg) {
+void gemv_resident_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K, int a_vec, int nrg) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -559,11 +588,12 @@ void gemv_resident_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ 
     typedef typename F::Raw Raw;
     auto load_item = [&](int g, int w, Raw (&r)[YT]) {
         g = min(g, nrg - 1);  // a prefetch past the wave's last item re-reads a valid row group
+        const SegRef<TC> sr = seg_of(sg, g);
         const int kv = min(K - w * kGemvWindow, kGemvWindow);
-        const uint8_t* base = W + static_cast<size_t>(w) * F::kWinBytes;
+        const uint8_t* base = sr.W + static_cast<size_t>(w) * F::kWinBytes;
 #pragma unroll
         for (int y = 0; y < YT; ++y) {
-            const uint8_t* rp = base + static_cast<size_t>(min(g * YT + y, N - 1)) * row_bytes;
+            const uint8_t* rp = base + static_cast<size_t>(min((g - sr.g0) * YT + y, sr.N - 1)) * row_bytes;
             r[y] = F::load(rp, lane, kv);
         }
     };
@@ -624,7 +654,8 @@ void gemv_resident_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ 
         if (kv == kGemvWindow) mac_window<F, MR, YT, true>(b, nwin, wc, lane, kv, KC, acc);
         else mac_window<F, MR, YT, false>(b, nwin, wc, lane, kv, KC, acc);
         if (wc == nwin - 1) {
-            reduce_store<MR, YT, TC>(acc, C, M, N, m0, gc * YT, lane);
+            const SegRef<TC> sr = seg_of(sg, gc);
+            reduce_store<MR, YT, TC>(acc, sr.C, M, sr.N, m0, (gc - sr.g0) * YT, lane);
 #pragma unroll
             for (int m = 0; m < MR; ++m)
 #pragma unroll
@@ -834,8 +865,16 @@ hipError_t occupancy(const void* kern, int threads, size_t lds, int& blocks) {
 
 constexpr size_t kSlotBytes = kChunks * 64 * 16 + 64 * 16;  // x + sx of one window, one A row
 
+// One weight matrix, or several sharing the activations (segments, resident kernel only; returns
+// hipErrorNotSupported when the activations do not fit in LDS and nseg > 1).
+struct Seg {
+    const void* W;
+    void* C;
+    int N;
+};
+
 template <class F, int MR, int YT, int NW, typename TA, typename TC>
-hipError_t launch_fast(const void* A, const void* W, void* C, int M, int N, int K, bool a_vec, hipStream_t stream) {
+hipError_t launch_fast(const void* A, const Seg* segs, int nseg, int M, int K, bool a_vec, hipStream_t stream) {
     DevInfo di;
     hipError_t e = device_info(di);
     if (e != hipSuccess) return e;
@@ -847,15 +886,31 @@ hipError_t launch_fast(const void* A, const void* W, void* C, int M, int N, int 
         const void* kern = reinterpret_cast<const void*>(&gemv_resident_kernel<F, MR, YT, NW, TA, TC>);
         int occ = 0;
         if ((e = occupancy(kern, threads, res_lds, occ)) != hipSuccess) return e;
-        const int nrg = (N + YT - 1) / YT;
+        GemvSegs<TC> sg;
+        int nrg = 0;
+        for (int j = 0; j < kMaxSegs; ++j) {
+            if (j < nseg) {
+                sg.W[j] = static_cast<const uint8_t*>(segs[j].W);
+                sg.C[j] = static_cast<TC*>(segs[j].C);
+                sg.N[j] = segs[j].N;
+                nrg += (segs[j].N + YT - 1) / YT;
+                sg.gend[j] = nrg;
+            } else {
+                sg.W[j] = sg.W[0];
+                sg.C[j] = sg.C[0];
+                sg.N[j] = sg.N[0];
+                sg.gend[j] = INT_MAX;
+            }
+        }
         const int need = (nrg + NW - 1) / NW;
         const int fill = max(1, occ * di.cus / mblocks);
         const dim3 grid(min(need, fill), mblocks);
         hipLaunchKernelGGL((gemv_resident_kernel<F, MR, YT, NW, TA, TC>), grid, dim3(threads), res_lds, stream,
-                           static_cast<const TA*>(A), static_cast<const uint8_t*>(W), static_cast<TC*>(C), M, N, K,
-                           a_vec ? 1 : 0, nrg);
+                           static_cast<const TA*>(A), sg, M, K, a_vec ? 1 : 0, nrg);
         return hipGetLastError();
     }
+    if (nseg != 1) return hipErrorNotSupported;
+    const int N = segs[0].N;
     const size_t win_lds = static_cast<size_t>(MR) * 2 * kSlotBytes;
     const void* kern = reinterpret_cast<const void*>(&gemv_window_kernel<F, MR, YT, NW, TA, TC>);
     int occ = 0;
@@ -863,29 +918,30 @@ hipError_t launch_fast(const void* A, const void* W, void* C, int M, int N, int 
     constexpr int kRows = NW * YT;
     const dim3 grid((N + kRows - 1) / kRows, mblocks);
     hipLaunchKernelGGL((gemv_window_kernel<F, MR, YT, NW, TA, TC>), grid, dim3(threads), win_lds, stream,
-                       static_cast<const TA*>(A), static_cast<const uint8_t*>(W), static_cast<TC*>(C), M, N, K,
-                       a_vec ? 1 : 0);
+                       static_cast<const TA*>(A), static_cast<const uint8_t*>(segs[0].W), static_cast<TC*>(segs[0].C),
+                       M, N, K, a_vec ? 1 : 0);
     return hipGetLastError();
 }
 
 template <class F, typename TA, typename TC>
-hipError_t dispatch_fast(const void* A, const void* W, void* C, int M, int N, int K, bool a_vec,
-                         hipStream_t stream) {
-    // Rows per workgroup: enough workgroups to cover the 256 CUs several times.
+hipError_t dispatch_fast(const void* A, const Seg* segs, int nseg, int M, int K, bool a_vec, hipStream_t stream) {
+    // Rows per wave item by the total row count (enough items to cover the 256 CUs several times).
     constexpr int NW = QMM_GEMV_NW;
     constexpr int YB = QMM_GEMV_YT_BIG;
+    int N = 0;
+    for (int j = 0; j < nseg; ++j) N += segs[j].N;
     if (M == 1) {
-        if (N >= 8192) return launch_fast<F, 1, YB, NW, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-        if (N >= 2048) return launch_fast<F, 1, 2, NW, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-        return launch_fast<F, 1, 1, NW, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+        if (N >= 8192) return launch_fast<F, 1, YB, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
+        if (N >= 2048) return launch_fast<F, 1, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
+        return launch_fast<F, 1, 1, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
     }
     if (M == 2) {
-        if (N >= 8192) return launch_fast<F, 2, YB, NW, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-        if (N >= 2048) return launch_fast<F, 2, 2, NW, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-        return launch_fast<F, 2, 1, NW, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+        if (N >= 8192) return launch_fast<F, 2, YB, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
+        if (N >= 2048) return launch_fast<F, 2, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
+        return launch_fast<F, 2, 1, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
     }
-    if (N >= 4096) return launch_fast<F, 4, 2, NW, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-    return launch_fast<F, 4, 1, NW, TA, TC>(A, W, C, M, N, K, a_vec, stream);
+    if (N >= 4096) return launch_fast<F, 4, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
+    return launch_fast<F, 4, 1, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
 }
 
 template <int T, typename TA, typename TC>
@@ -896,39 +952,67 @@ hipError_t launch_fallback(const void* A, const void* W, void* C, int M, int N, 
     return hipGetLastError();
 }
 
-template <typename TA, typename TC>
-hipError_t dispatch_types(int t, const void* A, const void* W, void* C, int M, int N, int K, hipStream_t stream) {
+// Fast-path eligibility of a weight pointer: Q4_K headers are read as 16-byte vectors, the other
+// formats need 2-byte alignment (fp16 scales).
+bool fast_weights(int t, const void* W) {
     const uintptr_t wa = reinterpret_cast<uintptr_t>(W);
+    return t == QMM_TYPE_Q4_K ? (wa & 15u) == 0 : (wa & 1u) == 0;
+}
+
+template <typename TA, typename TC>
+hipError_t dispatch_types(int t, const void* A, const Seg* segs, int nseg, int M, int K, hipStream_t stream) {
     const bool a_ok = (reinterpret_cast<uintptr_t>(A) & (sizeof(TA) - 1)) == 0;
     const bool a_vec = (reinterpret_cast<uintptr_t>(A) & 15u) == 0;
-    switch (t) {
-        case QMM_TYPE_Q4_K:
-            if ((wa & 15u) == 0 && a_ok) return dispatch_fast<GQ4K, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-            return launch_fallback<QMM_TYPE_Q4_K, TA, TC>(A, W, C, M, N, K, stream);
-        case QMM_TYPE_Q6_K:
-            if ((wa & 1u) == 0 && a_ok) return dispatch_fast<GQ6K, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-            return launch_fallback<QMM_TYPE_Q6_K, TA, TC>(A, W, C, M, N, K, stream);
-        case QMM_TYPE_Q8_0:
-            if ((wa & 1u) == 0 && a_ok) return dispatch_fast<GQ80, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-            return launch_fallback<QMM_TYPE_Q8_0, TA, TC>(A, W, C, M, N, K, stream);
-        case QMM_TYPE_Q4_0:
-            if ((wa & 1u) == 0 && a_ok) return dispatch_fast<GQ40, TA, TC>(A, W, C, M, N, K, a_vec, stream);
-            return launch_fallback<QMM_TYPE_Q4_0, TA, TC>(A, W, C, M, N, K, stream);
-        default:
-            return hipErrorInvalidValue;
+    bool fast = a_ok;
+    for (int j = 0; j < nseg; ++j) fast = fast && fast_weights(t, segs[j].W);
+    if (!fast) {
+        if (nseg != 1) return hipErrorNotSupported;
+        const void* W = segs[0].W;
+        void* C = segs[0].C;
+        const int N = segs[0].N;
+        switch (t) {
+            case QMM_TYPE_Q4_K: return launch_fallback<QMM_TYPE_Q4_K, TA, TC>(A, W, C, M, N, K, stream);
+            case QMM_TYPE_Q6_K: return launch_fallback<QMM_TYPE_Q6_K, TA, TC>(A, W, C, M, N, K, stream);
+            case QMM_TYPE_Q8_0: return launch_fallback<QMM_TYPE_Q8_0, TA, TC>(A, W, C, M, N, K, stream);
+            case QMM_TYPE_Q4_0: return launch_fallback<QMM_TYPE_Q4_0, TA, TC>(A, W, C, M, N, K, stream);
+            default: return hipErrorInvalidValue;
+        }
     }
+    switch (t) {
+        case QMM_TYPE_Q4_K: return dispatch_fast<GQ4K, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
+        case QMM_TYPE_Q6_K: return dispatch_fast<GQ6K, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
+        case QMM_TYPE_Q8_0: return dispatch_fast<GQ80, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
+        case QMM_TYPE_Q4_0: return dispatch_fast<GQ40, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t dispatch_dtypes(int t, const void* A, int a_dtype, int c_dtype, const Seg* segs, int nseg, int M, int K,
+                           hipStream_t stream) {
+    if (a_dtype == QMM_DTYPE_F32) {
+        if (c_dtype == QMM_DTYPE_F32) return dispatch_types<float, float>(t, A, segs, nseg, M, K, stream);
+        return dispatch_types<float, __half>(t, A, segs, nseg, M, K, stream);
+    }
+    if (c_dtype == QMM_DTYPE_F32) return dispatch_types<__half, float>(t, A, segs, nseg, M, K, stream);
+    return dispatch_types<__half, __half>(t, A, segs, nseg, M, K, stream);
 }
 
 }  // namespace
 
 hipError_t launch_gemv(int ggml_type, const void* A, int a_dtype, const void* W, void* C,
                        int c_dtype, int M, int N, int K, hipStream_t stream) {
-    if (a_dtype == QMM_DTYPE_F32) {
-        if (c_dtype == QMM_DTYPE_F32) return dispatch_types<float, float>(ggml_type, A, W, C, M, N, K, stream);
-        return dispatch_types<float, __half>(ggml_type, A, W, C, M, N, K, stream);
-    }
-    if (c_dtype == QMM_DTYPE_F32) return dispatch_types<__half, float>(ggml_type, A, W, C, M, N, K, stream);
-    return dispatch_types<__half, __half>(ggml_type, A, W, C, M, N, K, stream);
+    const Seg seg{W, C, N};
+    return dispatch_dtypes(ggml_type, A, a_dtype, c_dtype, &seg, 1, M, K, stream);
 }
+
+hipError_t launch_gemv_fused(int ggml_type, const void* A, int a_dtype, int c_dtype, int M, int K,
+                             const void* const* W, void* const* C, const int* N, int count, hipStream_t stream) {
+    if (count < 2 || count > kMaxSegs) return hipErrorNotSupported;
+    Seg segs[kMaxSegs];
+    for (int j = 0; j < count; ++j) segs[j] = Seg{W[j], C[j], N[j]};
+    return dispatch_dtypes(ggml_type, A, a_dtype, c_dtype, segs, count, M, K, stream);
+}
+
+int gemv_max_fused() { return kMaxSegs; }
 
 }  // namespace qmm

@@ -47,6 +47,11 @@ inline int block_bytes(int t) {
 // Kernel launchers (validated arguments; return a hipError_t from the launch).
 hipError_t launch_gemv(int ggml_type, const void* A, int a_dtype, const void* W, void* C,
                        int c_dtype, int M, int N, int K, hipStream_t stream);
+// Several weight matrices (same type and K) times the same activations in one launch; returns
+// hipErrorNotSupported when the fused path does not apply (the caller then launches each).
+hipError_t launch_gemv_fused(int ggml_type, const void* A, int a_dtype, int c_dtype, int M, int K,
+                             const void* const* W, void* const* C, const int* N, int count, hipStream_t stream);
+int gemv_max_fused();
 hipError_t launch_gemm_prefill(int ggml_type, const void* A, int a_dtype, const void* W, void* C,
                                int c_dtype, int M, int N, int K, hipStream_t stream);
 bool gemm_prefill_supported(int ggml_type, int a_dtype, int c_dtype, int M, int N, int K,
