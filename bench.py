@@ -50,9 +50,12 @@ def log(msg):
 
 
 def layer_specs(hidden, inter, kv, main, down):
-    """(name, type, N, K, input) of the 7 projections of one transformer layer."""
+    """(name, type, N, K, input) of the 7 projections of one transformer layer.  Inputs follow a
+    layer's dataflow: q/k/v read the normed hidden state, o the attention output, gate/up the
+    post-attention normed state, down the SwiGLU output (so only q/k/v and gate/up can share a
+    launch)."""
     return [("q", main, hidden, hidden, "h"), ("k", main, kv, hidden, "h"), ("v", main, kv, hidden, "h"),
-            ("o", main, hidden, hidden, "h"), ("gate", main, inter, hidden, "h"), ("up", main, inter, hidden, "h"),
+            ("o", main, hidden, hidden, "attn"), ("gate", main, inter, hidden, "h2"), ("up", main, inter, hidden, "h2"),
             ("down", down, hidden, inter, "f")]
 
 
@@ -261,8 +264,8 @@ def cpu_baseline_70b(layers=3, seed=0):
 
     rng = np.random.default_rng(seed)
     specs = layer_specs(8192, 28672, 1024, Q4_K, Q6_K)
-    xs = {"h": rng.standard_normal((1, 8192)).astype(np.float32),
-          "f": rng.standard_normal((1, 28672)).astype(np.float32)}
+    xs = {name: rng.standard_normal((1, 8192)).astype(np.float32) for name in ("h", "attn", "h2")}
+    xs["f"] = rng.standard_normal((1, 28672)).astype(np.float32)
     t_total = 0.0
     nbytes = 0
     for _ in range(layers):

@@ -923,13 +923,11 @@ hipError_t launch_fast(const void* A, const Seg* segs, int nseg, int M, int K, b
     return hipGetLastError();
 }
 
-template <class F, typename TA, typename TC>
-hipError_t dispatch_fast(const void* A, const Seg* segs, int nseg, int M, int K, bool a_vec, hipStream_t stream) {
+template <class F, int NW, typename TA, typename TC>
+hipError_t dispatch_rows(const void* A, const Seg* segs, int nseg, int M, int N, int K, bool a_vec,
+                         hipStream_t stream) {
     // Rows per wave item by the total row count (enough items to cover the 256 CUs several times).
-    constexpr int NW = QMM_GEMV_NW;
     constexpr int YB = QMM_GEMV_YT_BIG;
-    int N = 0;
-    for (int j = 0; j < nseg; ++j) N += segs[j].N;
     if (M == 1) {
         if (N >= 8192) return launch_fast<F, 1, YB, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
         if (N >= 2048) return launch_fast<F, 1, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
@@ -942,6 +940,19 @@ hipError_t dispatch_fast(const void* A, const Seg* segs, int nseg, int M, int K,
     }
     if (N >= 4096) return launch_fast<F, 4, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
     return launch_fast<F, 4, 1, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
+}
+
+template <class F, typename TA, typename TC>
+hipError_t dispatch_fast(const void* A, const Seg* segs, int nseg, int M, int K, bool a_vec, hipStream_t stream) {
+    int N = 0;
+    for (int j = 0; j < nseg; ++j) N += segs[j].N;
+    // Resident activations above 40 KB of LDS leave room for at most three workgroups per CU:
+    // 16-wave workgroups then keep more waves (bytes in flight) per CU.  M = 1, 2 only (larger M
+    // tiles use the windowed kernel at such K).
+    const int nwin = (K + kGemvWindow - 1) / kGemvWindow;
+    const size_t res_lds = static_cast<size_t>(min(M, 4)) * nwin * kSlotBytes;
+    if (M <= 2 && res_lds > 40 * 1024) return dispatch_rows<F, 16, TA, TC>(A, segs, nseg, M, N, K, a_vec, stream);
+    return dispatch_rows<F, QMM_GEMV_NW, TA, TC>(A, segs, nseg, M, N, K, a_vec, stream);
 }
 
 template <int T, typename TA, typename TC>
