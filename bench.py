@@ -4,15 +4,16 @@
 Headline workload (the JSON line's `value`): one decode token (M = 1) through all 80 layers
 of a Llama-3-70B Q4_K_M model whose weights are distinct random tensors resident in HBM
 (q/k/v/o/gate/up in Q4_K, down in Q6_K; 43.35 GB).  A step issues the 7 projections of
-every layer (560 GEMVs) back to back on one stream through `qmm_gemm_batch`; `value` is
-algorithmic bytes (packed weights + fp32 activations read once + fp32 outputs written once)
-per second over the timed steps.
+every layer (560 GEMVs) back to back on one stream through `qmm_gemm_batch`, which runs q/k/v
+and gate/up (each set reads the same activations) as one launch each: 4 launches per layer.
+`value` is algorithmic bytes (packed weights + fp32 activations read once per GEMV + fp32
+outputs written once) per second over the timed steps.
 
-The `roofline` object covers the dominant kernel (the Q4_K GEMV serving gate/up,
-28672 x 8192): its 160 launches of one step (gate and up of every layer) are issued back to
+The `roofline` object covers the dominant kernel, the fused gate+up launch (two Q4_K
+28672 x 8192 GEMVs on one activation vector): its 80 launches of one step are issued back to
 back between two HIP events on their stream, and `achieved` is its algorithmic bytes over the
 average launch duration; `traffic` is the HBM bytes per launch from the committed counter
-summary (profiles/gemv_q4_k_28672x8192_m1_traffic.md, made with `--pmc-workload`).
+summary (profiles/gemv_q4_k_gate_up_2x28672x8192_m1_traffic.md, made with `--pmc-workload`).
 `cpu_baseline` times the in-repo NumPy restatement of the reference's CPU path (dequantize to
 fp16, then fp32 matmul) on three full 70B layers.  `extra` holds the other configurations (8B
 Q8_0 / Q4_K_M layers, the 8B Q6_K lm_head, 70B at M = 4, the Q4_0 4096 x 4096 case, prefill
@@ -191,28 +192,36 @@ def run_workload(torch, qmm, hip, wl, steps, warmup):
 
 
 def run_dominant(torch, qmm, hip, wl, reps, warmup=2):
-    """Average duration of the dominant kernel: its launches of one step (the gate and up GEMVs
-    of all layers, distinct weights) issued back to back between two HIP events on the stream
-    they run on, `reps` times; returns (avg_us, launches)."""
+    """Average duration of the dominant kernel, the fused gate+up launch: one qmm_gemm_batch call
+    per layer with that layer's gate and up descriptors (one launch each, distinct weights),
+    all layers back to back between two HIP events on the stream they run on, `reps` times;
+    returns (avg_us, launches)."""
     stream = torch.cuda.current_stream().cuda_stream
     idx = wl.dominant_idx
-    arr = (wl.qmm.GemmDesc * len(idx))()
     full = wl.descs()
-    for j, i in enumerate(idx):
-        arr[j] = full[i]
+    pairs = []
+    for j in range(0, len(idx) - 1, 2):
+        arr = (wl.qmm.GemmDesc * 2)()
+        arr[0], arr[1] = full[idx[j]], full[idx[j + 1]]
+        pairs.append(arr)
+
+    def one_pass():
+        for arr in pairs:
+            qmm.check(qmm.lib().qmm_gemm_batch(arr, 2, stream))
+
     for _ in range(warmup):
-        qmm.check(qmm.lib().qmm_gemm_batch(arr, len(arr), stream))
+        one_pass()
     torch.cuda.synchronize()
     a, b = hip.event(), hip.event()
     hip.record(a, stream)
     for _ in range(reps):
-        qmm.check(qmm.lib().qmm_gemm_batch(arr, len(arr), stream))
+        one_pass()
     hip.record(b, stream)
     torch.cuda.synchronize()
     ms = hip.elapsed_ms(a, b)
     hip.destroy(a)
     hip.destroy(b)
-    return ms * 1e3 / (reps * len(idx)), reps * len(idx)
+    return ms * 1e3 / (reps * len(pairs)), reps * len(pairs)
 
 
 def run_prefill(torch, qmm, hip, gen, dev, steps, warmup):
@@ -292,9 +301,10 @@ def cpu_baseline_70b(layers=3, seed=0):
 
 def pmc_workload(torch, qmm, dev, gen, reps=8):
     """Counter-collection workload: a plain device copy of known size (256 MiB read + 256 MiB
-    written per launch), then the dominant GEMV (Q4_K 28672 x 8192, M = 1) over 16 distinct
-    weight copies.  Run under `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE`: the copy's
-    per-dispatch reading calibrates the counter against known bytes."""
+    written per launch), then the dominant kernel (fused gate+up: two Q4_K 28672 x 8192 GEMVs on
+    one activation vector, M = 1) over 8 distinct weight pairs.  Run under `rocprofv3 --pmc
+    FETCH_SIZE` and `--pmc WRITE_SIZE`: the copy's per-dispatch reading calibrates the counter
+    against known bytes."""
     stream = torch.cuda.current_stream().cuda_stream
     src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
@@ -305,13 +315,21 @@ def pmc_workload(torch, qmm, dev, gen, reps=8):
     n, k = 28672, 8192
     ws = [make_weight(torch, Q4_K, n, k, gen, dev) for _ in range(16)]
     x = torch.randn((1, k), device=dev, generator=gen)
-    y = torch.empty((1, n), device=dev)
+    ys = [torch.empty((1, n), device=dev) for _ in range(2)]
+    pairs = []
+    for j in range(0, 16, 2):
+        arr = (qmm.GemmDesc * 2)()
+        for e in range(2):
+            d = arr[e]
+            d.ggml_type, d.A, d.a_dtype, d.W, d.C, d.c_dtype = (Q4_K, x.data_ptr(), qmm.DTYPE_F32, ws[j + e].data_ptr(),
+                                                                ys[e].data_ptr(), qmm.DTYPE_F32)
+            d.M, d.N, d.K = 1, n, k
+        pairs.append(arr)
     for r in range(reps):
-        for w in ws:
-            qmm.check(qmm.lib().qmm_gemm(Q4_K, x.data_ptr(), qmm.DTYPE_F32, w.data_ptr(), y.data_ptr(),
-                                         qmm.DTYPE_F32, 1, n, k, stream))
+        for arr in pairs:
+            qmm.check(qmm.lib().qmm_gemm_batch(arr, 2, stream))
     torch.cuda.synchronize()
-    log(f"pmc workload done: copy 256 MiB x {reps}, Q4_K {n}x{k} GEMV x {16 * reps}")
+    log(f"pmc workload done: copy 256 MiB x {reps}, fused gate+up (2 x Q4_K {n}x{k}) x {8 * reps}")
 
 
 def main():
@@ -356,11 +374,11 @@ def main():
     gbs = wl.algo_bytes / (ms * 1e-3) / 1e9
     log(f"70B M=1: {ms:.3f} ms/token, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM peak), "
         f"wall {wall:.3f} s for {args.steps} steps")
-    dom_bytes = weight_bytes(Q4_K, 28672, 8192) + 4 * 8192 + 4 * 28672
+    dom_bytes = 2 * weight_bytes(Q4_K, 28672, 8192) + 4 * 8192 + 2 * 4 * 28672
     dom_us, dom_launches = run_dominant(torch, qmm, hip, wl, max(2, args.steps // 4))
     dom_gbs = dom_bytes / (dom_us * 1e-6) / 1e9
-    log(f"dominant kernel (Q4_K 28672x8192 GEMV, M=1): {dom_us:.2f} us avg over {dom_launches} back-to-back "
-        f"launches, {dom_gbs:.1f} GB/s")
+    log(f"dominant kernel (fused gate+up, 2 x Q4_K 28672x8192 GEMV, M=1): {dom_us:.2f} us avg over "
+        f"{dom_launches} back-to-back launches, {dom_gbs:.1f} GB/s")
 
     traffic = read_traffic()
 
@@ -439,11 +457,12 @@ def main():
         "config": {"workload": "llama3-70b-q4_k_m-decode-m1-80-layers", "layers": args.layers, "M": 1,
                    "hidden": 8192, "intermediate": 28672, "kv_dim": 1024,
                    "weights_GB": round(wl_bytes_gb(args.layers), 2), "gemvs_per_step": 7 * args.layers,
+                   "launches_per_step": 4 * args.layers,
                    "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                    "tokens_per_s": round(1e3 / ms, 1)},
         "roofline": {"bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "gemv_resident_kernel<GQ4K, M=1> (Q4_K 28672x8192)",
+                     "kernel": "gemv_resident_kernel<GQ4K, M=1>, fused gate+up (2 x Q4_K 28672x8192)",
                      "avg_us": round(dom_us, 3), "launches": dom_launches,
                      "algorithmic_bytes_per_launch": dom_bytes},
         "cpu_baseline": cpu,
@@ -452,7 +471,7 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-TRAFFIC_FILE = os.path.join(REPO, "profiles", "gemv_q4_k_28672x8192_m1_traffic.md")
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "gemv_q4_k_gate_up_2x28672x8192_m1_traffic.md")
 
 
 def read_traffic():

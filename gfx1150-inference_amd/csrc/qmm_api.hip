@@ -325,6 +325,7 @@ int qmm_release_workspace(void) {
     }
     g_ws.clear();
     if ((e = hipSetDevice(cur)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+    if ((e = qmm::release_prefill_workspaces()) != hipSuccess) return hip_fail(e, "release prefill workspace");
     return QMM_OK;
 }
 

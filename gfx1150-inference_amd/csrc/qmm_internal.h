@@ -56,6 +56,9 @@ hipError_t launch_gemm_prefill(int ggml_type, const void* A, int a_dtype, const 
                                int c_dtype, int M, int N, int K, hipStream_t stream);
 bool gemm_prefill_supported(int ggml_type, int a_dtype, int c_dtype, int M, int N, int K,
                             const void* A, const void* W, const void* C);
+// Frees the prefill workspaces (f16 activations, split-K partials) of every device, after
+// synchronizing each device.
+hipError_t release_prefill_workspaces();
 hipError_t launch_dequantize(int ggml_type, const void* W, void* out, int out_dtype,
                              int64_t num_elements, hipStream_t stream);
 

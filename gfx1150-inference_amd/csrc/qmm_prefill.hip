@@ -549,6 +549,29 @@ hipError_t workspace(hipStream_t stream, size_t bytes, void** out) {
     return hipSuccess;
 }
 
+}  // namespace
+
+hipError_t release_prefill_workspaces() {
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return e;
+    for (auto& kv : g_ws) {
+        if (!kv.second.buf) continue;
+        const int dev = std::stoi(kv.first.substr(0, kv.first.find(':')));
+        // queued kernels on any stream of the device may still read the buffer
+        if ((e = hipSetDevice(dev)) != hipSuccess) return e;
+        if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+        if ((e = hipFree(kv.second.buf)) != hipSuccess) return e;
+        kv.second.buf = nullptr;
+        kv.second.cap = 0;
+    }
+    g_ws.clear();
+    return hipSetDevice(cur);
+}
+
+namespace {
+
 int g_cus = 0;
 
 hipError_t cu_count(int& cus) {

@@ -134,7 +134,9 @@ int qmm_dequantize_q4_k_host(const void* h_q4k, void* h_fp16_out, int num_elemen
 int qmm_dequantize_q6_k_host(const void* h_q6k, void* h_fp16_out, int num_elements);
 
 /* Release the host-API workspace (the reference frees its static Q4Workspace at exit,
- * dequantize.hip:715-719). Safe to call at any time; the next host call re-grows it. */
+ * dequantize.hip:715-719) and the prefill workspaces of qmm_gemm (f16 activations, split-K
+ * partials; grow-only per device and stream).  Synchronizes each device that holds one, so it
+ * is safe to call at any time; the next call that needs a workspace re-grows it. */
 int qmm_release_workspace(void);
 
 #ifdef __cplusplus

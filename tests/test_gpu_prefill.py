@@ -115,3 +115,23 @@ def test_prefill_full_size_m512(dev, name, t, N, K):
     sub = np.concatenate([raw[r * rb:(r + 1) * rb] for r in rows])
     assert O.max_rel_err(y[:, rows], O.matmul_f64(t, x, sub, rows.size, K)) <= TOL_F64
     assert O.max_rel_err(y[:, rows], O.matmul_f16_operands(t, x, sub, rows.size, K)) <= TOL_F16
+
+
+def test_prefill_workspace_release_and_regrow(dev):
+    # fp32 activations and a narrow N use the prefill workspace (f16 copy, split-K partials);
+    # qmm_release_workspace frees it and the next call re-grows it with identical results.
+    import torch
+    import qmm
+    t = O.GGML_Q6_K
+    rng = np.random.default_rng(4300)
+    M, N, K = 64, 256, 4096
+    raw = O.synth_weights(t, N, K, rng)
+    A = to_dev(rng.standard_normal((M, K)).astype(np.float32), dev)
+    W = to_dev(raw, dev)
+    y1 = qmm.gemm(t, A, W, N, K)
+    torch.cuda.synchronize()
+    qmm.check(qmm.lib().qmm_release_workspace())
+    y2 = qmm.gemm(t, A, W, N, K)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    assert O.max_rel_err(y2.cpu().numpy().astype(np.float64), O.matmul_f64(t, A.cpu().numpy(), raw, N, K)) <= TOL_F64
