@@ -16,8 +16,9 @@ average launch duration; `traffic` is the HBM bytes per launch from the committe
 summary (profiles/gemv_q4_k_gate_up_2x28672x8192_m1_traffic.md, made with `--pmc-workload`).
 `cpu_baseline` times the in-repo NumPy restatement of the reference's CPU path (dequantize to
 fp16, then fp32 matmul) on three full 70B layers.  `extra` holds the other configurations (8B
-Q8_0 / Q4_K_M layers, the 8B Q6_K lm_head, 70B at M = 4, the Q4_0 4096 x 4096 case, prefill
-M = 512), each on rotated weight copies larger than the 256 MB MALL.
+Q8_0 / Q4_K_M layers, the 8B Q6_K lm_head and token-embedding gather-dequant, 70B at M = 4, the
+Q4_0 4096 x 4096 case, prefill M = 512 with the vendor f16 GEMM on dense weights beside it), the
+GEMV ones on rotated weight copies larger than the 256 MB MALL.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-extra] [--no-cpu-baseline] [--pmc-workload]
 """
@@ -259,7 +260,27 @@ def run_prefill(torch, qmm, hip, gen, dev, steps, warmup):
             res[key] = {"us": round(us, 2), "TFLOP/s": round(tf, 1), "frac_f16_peak": round(tf / F16_DENSE_PEAK_TFLOPS, 4)}
             log(f"prefill M=512 {key}: {us:.1f} us, {tf:.1f} TFLOP/s ({tf / F16_DENSE_PEAK_TFLOPS * 100:.1f}% of f16 peak)")
             del c
-        del w, x32
+        # context: the vendor f16 GEMM (torch -> hipBLASLt) on dense f16 weights of the same
+        # shape, no dequantization (3.5x more weight bytes than Q4_K)
+        w16 = torch.randn((n, k), device=dev, generator=gen, dtype=torch.float16)
+        x16 = x32.half()
+        for _ in range(warmup):
+            _ = x16 @ w16.t()
+        torch.cuda.synchronize()
+        a, b = hip.event(), hip.event()
+        hip.record(a, stream)
+        for _ in range(steps):
+            _ = x16 @ w16.t()
+        hip.record(b, stream)
+        torch.cuda.synchronize()
+        us = hip.elapsed_ms(a, b) * 1e3 / steps
+        hip.destroy(a)
+        hip.destroy(b)
+        tf = 2.0 * M * n * k / (us * 1e-6) / 1e12
+        key = f"{name}_dense_f16_vendor_gemm"
+        res[key] = {"us": round(us, 2), "TFLOP/s": round(tf, 1), "frac_f16_peak": round(tf / F16_DENSE_PEAK_TFLOPS, 4)}
+        log(f"prefill M=512 {key}: {us:.1f} us, {tf:.1f} TFLOP/s (reference point, dense f16 weights)")
+        del w, x32, w16, x16
     return res
 
 
@@ -423,6 +444,33 @@ def main():
         g = lm.algo_bytes / (msl * 1e-3) / 1e9
         extra["8b_q6_k_lm_head_m1"] = {"GB/s": round(g, 1), "us": round(msl * 1e3 / 4, 2), "frac_hbm": round(g / HBM_PEAK_GBS, 4)}
         log(f"lm_head: {extra['8b_q6_k_lm_head_m1']}")
+        # token embeddings gathered and dequantized from the same Q6_K 128256 x 4096 table
+        # (the reference does this on the CPU, src/tokenizer.py:336-389)
+        table = lm.weights[0]
+        stream = torch.cuda.current_stream().cuda_stream
+        for label, ntok in (("prompt_512", 512), ("decode_1", 1)):
+            ids = torch.randint(0, 128256, (ntok,), device=dev, generator=gen, dtype=torch.int64)
+            out = torch.empty((ntok, 4096), device=dev, dtype=torch.float16)
+
+            def emb():
+                qmm.check(qmm.lib().qmm_embed(Q6_K, table.data_ptr(), 128256, 4096, ids.data_ptr(), ntok,
+                                              out.data_ptr(), qmm.DTYPE_F16, None, stream))
+
+            for _ in range(3):
+                emb()
+            torch.cuda.synchronize()
+            a, b = hip.event(), hip.event()
+            hip.record(a, stream)
+            for _ in range(50):
+                emb()
+            hip.record(b, stream)
+            torch.cuda.synchronize()
+            us = hip.elapsed_ms(a, b) * 1e3 / 50
+            hip.destroy(a)
+            hip.destroy(b)
+            nbytes = ntok * (weight_bytes(Q6_K, 1, 4096) + 8 + 2 * 4096)
+            extra[f"8b_q6_k_embed_{label}"] = {"us": round(us, 2), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1)}
+            log(f"embed {label}: {extra[f'8b_q6_k_embed_{label}']}")
         lm.free()
         del lm
         q40 = Workload(torch, qmm, "q4_0", [[("w", Q4_0, 4096, 4096, "h")]], 128, 1, dev, gen)

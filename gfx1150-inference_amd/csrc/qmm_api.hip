@@ -269,6 +269,34 @@ int qmm_gemm_batch(const qmm_gemm_desc* descs, int count, void* stream) {
     return QMM_OK;
 }
 
+int qmm_embed(int ggml_type, const void* table, int64_t n_rows, int hidden, const int64_t* ids, int64_t n_ids,
+              void* out, int out_dtype, int* bad, void* stream) {
+    const bool dense = ggml_type == QMM_TYPE_F16 || ggml_type == QMM_TYPE_F32;
+    if (!dense && !known_type(ggml_type))
+        return fail(QMM_ERR_INVALID_ARGUMENT, "Unsupported token_embd.weight type: " + std::to_string(ggml_type));
+    if (out_dtype != QMM_DTYPE_F32 && out_dtype != QMM_DTYPE_F16 && out_dtype != QMM_DTYPE_BF16)
+        return fail(QMM_ERR_INVALID_ARGUMENT, "out_dtype must be QMM_DTYPE_F32, QMM_DTYPE_F16 or QMM_DTYPE_BF16.");
+    const int qk = dense ? 32 : qmm::block_elems(ggml_type);
+    if (hidden <= 0 || hidden % qk != 0)
+        return fail(QMM_ERR_INVALID_ARGUMENT, "hidden must be a positive multiple of " + std::to_string(qk) + ".");
+    if (n_ids < 0 || n_rows < 0) return fail(QMM_ERR_INVALID_ARGUMENT, "n_ids and n_rows must be non-negative.");
+    if (n_ids == 0) return QMM_OK;
+    if (n_rows == 0) return fail(QMM_ERR_INVALID_ARGUMENT, "the embedding table has no rows.");
+    if (table == nullptr || ids == nullptr || out == nullptr)
+        return fail(QMM_ERR_INVALID_ARGUMENT, "table, ids and out must be non-null device pointers.");
+    if ((reinterpret_cast<uintptr_t>(out) & 15u) != 0) return fail(QMM_ERR_INVALID_ARGUMENT, "out must be 16-byte aligned.");
+    const uintptr_t ta = reinterpret_cast<uintptr_t>(table);
+    if ((ggml_type == QMM_TYPE_F32 && (ta & 3u)) || (ggml_type == QMM_TYPE_F16 && (ta & 1u)))
+        return fail(QMM_ERR_INVALID_ARGUMENT, "table must be aligned to its element size.");
+    if ((reinterpret_cast<uintptr_t>(ids) & 7u) != 0) return fail(QMM_ERR_INVALID_ARGUMENT, "ids must be 8-byte aligned.");
+    const int64_t row_bytes = dense ? static_cast<int64_t>(hidden) * (ggml_type == QMM_TYPE_F32 ? 4 : 2)
+                                    : static_cast<int64_t>(hidden / qk) * qmm::block_bytes(ggml_type);
+    hipError_t e = qmm::launch_embed(ggml_type, table, n_rows, row_bytes, hidden, ids, n_ids, out, out_dtype, bad,
+                                     static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "qmm_embed kernel launch");
+    return QMM_OK;
+}
+
 int qmm_dequantize(int ggml_type, const void* W, void* out, int out_dtype, int64_t num_elements, void* stream) {
     int rc = check_dequant_args(ggml_type, W, out, out_dtype, num_elements, true);
     if (rc != QMM_OK) return rc;

@@ -59,6 +59,8 @@ bool gemm_prefill_supported(int ggml_type, int a_dtype, int c_dtype, int M, int 
 // Frees the prefill workspaces (f16 activations, split-K partials) of every device, after
 // synchronizing each device.
 hipError_t release_prefill_workspaces();
+hipError_t launch_embed(int ggml_type, const void* table, int64_t n_rows, int64_t row_bytes, int hidden,
+                        const int64_t* ids, int64_t n_ids, void* out, int out_dtype, int* bad, hipStream_t stream);
 hipError_t launch_dequantize(int ggml_type, const void* W, void* out, int out_dtype,
                              int64_t num_elements, hipStream_t stream);
 

@@ -29,6 +29,8 @@ GGML_Q4_0 = 2
 GGML_Q8_0 = 8
 GGML_Q4_K = 12
 GGML_Q6_K = 14
+GGML_F32 = 0   # token-embedding tables only
+GGML_F16 = 1   # token-embedding tables only
 
 # (block_elems, block_bytes) of every supported type (src/kernels/dequantize.h:6-22).
 BLOCK_INFO = {GGML_Q4_0: (32, 18), GGML_Q8_0: (32, 34), GGML_Q4_K: (256, 144), GGML_Q6_K: (256, 210)}
@@ -75,6 +77,7 @@ _SIGNATURES = {
     "qmm_weight_bytes": (ctypes.c_size_t, [_i, _i64, _i64]),
     "qmm_gemm": (_i, [_i, _vp, _i, _vp, _vp, _i, _i, _i, _i, _vp]),
     "qmm_dequantize": (_i, [_i, _vp, _vp, _i, _i64, _vp]),
+    "qmm_embed": (_i, [_i, _vp, _i64, _i, _vp, _i64, _vp, _i, _vp, _vp]),
     "qmm_gemm_batch": (_i, [ctypes.POINTER(GemmDesc), _i, _vp]),
     "qmm_release_workspace": (_i, []),
 }
@@ -173,6 +176,51 @@ def dequantize(ggml_type: int, W, num_elements: int, out=None, out_dtype=None, s
         out = torch.empty((num_elements,), dtype=out_dtype or torch.float16, device=W.device)
     check(_lib.qmm_dequantize(ggml_type, W.data_ptr(), out.data_ptr(), _dtype_code(out.dtype),
                               num_elements, _stream_handle(stream)))
+    return out
+
+
+def _row_bytes(ggml_type: int, hidden: int) -> int:
+    if ggml_type == GGML_F32:
+        return 4 * hidden
+    if ggml_type == GGML_F16:
+        return 2 * hidden
+    qk, bb = BLOCK_INFO[ggml_type]
+    return (hidden // qk) * bb
+
+
+def embed_tokens(token_ids, ggml_type: int, table, hidden_size: int, out_dtype=None, stream=None):
+    """Token embeddings ``(len(token_ids), hidden_size)`` (fp16 by default) from the token table,
+    gathered and dequantized on the GPU.
+
+    Mirrors the reference's ``embed_tokens(token_ids, embd_info, embd_view, hidden_size)``
+    (src/tokenizer.py:336-389): the same result dtype and values (bit-exact with its CPU
+    dequantizers), an empty ``(0, hidden_size)`` result for no ids, and the same ``ValueError``
+    for an unsupported table type or an id outside the table (checked on the host before any GPU
+    work, like the reference).  ``table`` is the packed ``token_embd.weight`` as a device tensor:
+    uint8 bytes for Q4_0 / Q8_0 / Q4_K / Q6_K, or float16 / float32 values for F16 / F32.
+    """
+    import numpy as np
+    torch = _torch()
+    ids = np.asarray(token_ids, dtype=np.int64).reshape(-1)
+    dt = out_dtype or torch.float16
+    if ids.size == 0:
+        return torch.empty((0, hidden_size), dtype=dt, device=table.device)
+    if ggml_type not in (GGML_F32, GGML_F16) and ggml_type not in BLOCK_INFO:
+        raise ValueError(f"Unsupported token_embd.weight type: {ggml_type}")
+    row_bytes = _row_bytes(ggml_type, hidden_size)
+    n_rows = (table.numel() * table.element_size()) // row_bytes
+    bad = (ids < 0) | (ids >= n_rows)
+    if bad.any():
+        raise ValueError(f"Token ID {int(ids[bad][0])} is out of range for embedding table with {n_rows} rows")
+    dev_ids = torch.from_numpy(ids).to(table.device)  # copied on the current stream
+    out = torch.empty((ids.size, hidden_size), dtype=dt, device=table.device)
+    if stream is not None:
+        # the kernel on `stream` must see the copied ids, and the ids must outlive it there
+        stream.wait_stream(torch.cuda.current_stream(table.device))
+        dev_ids.record_stream(stream)
+        out.record_stream(stream)
+    check(_lib.qmm_embed(ggml_type, table.data_ptr(), n_rows, hidden_size, dev_ids.data_ptr(), ids.size,
+                         out.data_ptr(), _dtype_code(dt), None, _stream_handle(stream)))
     return out
 
 

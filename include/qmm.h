@@ -32,7 +32,8 @@ enum qmm_status {
 };
 
 enum qmm_ggml_type {
-    QMM_TYPE_F16 = 1,
+    QMM_TYPE_F32 = 0,   /* token-embedding tables only (qmm_embed) */
+    QMM_TYPE_F16 = 1,   /* token-embedding tables only (qmm_embed) */
     QMM_TYPE_Q4_0 = 2,
     QMM_TYPE_Q8_0 = 8,
     QMM_TYPE_Q4_K = 12,
@@ -92,6 +93,20 @@ int qmm_gemm_batch(const qmm_gemm_desc* descs, int count, void* stream);
  * (reference src/kernels/dequantize.hip:68-88, 213-229, 335-371, 508-544). */
 int qmm_dequantize(int ggml_type, const void* W, void* out, int out_dtype,
                    int64_t num_elements, void* stream);
+
+/* Token-embedding lookup: out[i, :] = dequant(table row ids[i]) for i < n_ids, `hidden` elements
+ * per row, in out_dtype (F16 as the reference, BF16 or F32), bit-exact with the reference's CPU
+ * dequantizers.  Replaces embed_tokens (reference src/tokenizer.py:336-389), which gathers the
+ * packed rows of token_embd.weight and dequantizes them on the CPU.
+ * table: n_rows rows of GGUF blocks (Q4_0, Q8_0, Q4_K, Q6_K) or of F16 / F32 values (ggml_type
+ * QMM_TYPE_F16 / QMM_TYPE_F32), device memory; ids: n_ids int64 device values; out: 16-byte
+ * aligned device buffer.  hidden must be a positive multiple of 32 (256 for Q4_K / Q6_K).
+ * The reference raises ValueError for an id outside [0, n_rows) before any work; ids here live
+ * on the device, so such an id reads nothing out of bounds: its output row is zero-filled and
+ * *bad (a device int the caller zeroes first; may be NULL) is set to 1.  The Python wrapper
+ * qmm.embed_tokens validates host ids exactly like the reference. */
+int qmm_embed(int ggml_type, const void* table, int64_t n_rows, int hidden, const int64_t* ids,
+              int64_t n_ids, void* out, int out_dtype, int* bad, void* stream);
 
 /* Largest M served by the GEMV family (exclusive bound), and the prefill threshold. */
 int qmm_gemv_max_m(void);
