@@ -8,17 +8,19 @@
 //     over fp16 activations; f16 keeps three more mantissa bits than bf16 at the same MFMA rate.
 //     fp32 activations are rounded to f16 once by a conversion pass into a workspace.
 //   * A workgroup (8 waves, two per SIMD, so one wave's memory stalls are covered by the other's
-//     MFMAs) owns a 128 (m) x 256 (n) output tile and walks its K range in steps of 128; wave w
+//     MFMAs) owns a 128 (m) x 256 (n) output tile and walks its K range in steps of 256 (one
+//     Q4_K / Q6_K super-block per weight row, so each row's bytes arrive in one batch); wave w
 //     owns weight rows [32w, 32w + 32) of the tile and all 128 activation rows (4 MFMA tiles of
-//     32 x 32, fp32 accumulators in AGPRs).
-//   * Activation tiles are double-buffered in LDS: the next step's tile is loaded into registers
-//     during the current step and written to the free slot near its end (one barrier per step).
+//     32 x 32, fp32 accumulators).
+//   * Activation tiles (128 x 256 f16, 64 KiB) are double-buffered in LDS: the next step's tile
+//     is loaded into registers during the current step and written to the free slot near its end
+//     (one barrier per step).
 //     Rows are XOR-swizzled so fragment reads are bank-conflict free.
 //   * Each wave dequantizes its own weight rows straight into MFMA fragments with packed f16
 //     math: one v_perm makes two (1024 + code) f16 values, v_pk_add_f16 removes the offset
 //     exactly, v_pk_fma_f16 applies the group's scale and min (one rounding to f16).  Raw
 //     bytes are loaded one step ahead.
-//   * A step is software-pipelined in eight sub-steps of one 16-k MFMA block: while a sub-step's
+//   * A step is software-pipelined in sixteen sub-steps of one 16-k MFMA block: while a sub-step's
 //     MFMAs run, the wave reads the next sub-step's activation fragments from LDS and
 //     dequantizes its weight fragment.
 //   * Narrow N (few tiles): the K range is split over workgroups; partial tiles land in a
@@ -27,6 +29,7 @@
 #include <mutex>
 #include <string>
 #include <type_traits>
+#include <utility>
 #include <unordered_map>
 
 #include "qmm_device.h"
@@ -36,7 +39,8 @@ namespace {
 
 constexpr int kBM = 128;        // activation rows per workgroup tile
 constexpr int kBN = 256;        // weight rows per workgroup tile (32 per wave)
-constexpr int kBK = 128;        // k per step (two halves of 64)
+constexpr int kHalves = 4;      // 64-k halves per step
+constexpr int kBK = 64 * kHalves;  // k per step (one Q4_K / Q6_K super-block)
 constexpr int kThreads = 512;   // 8 waves: two per SIMD, so one wave's load stalls are covered
 constexpr int kChunksPerHalf = kBM * 64 / 8;  // 16-byte chunks (8 f16) per 64-k half stage = 1024
 
@@ -88,8 +92,9 @@ __device__ __forceinline__ void bytes_to_h2(uint32_t x, h2 sub, h2& lo, h2& hi) 
 __device__ __forceinline__ uint32_t affine(h2 c, h2 a, h2 b) { return as_u32(__builtin_elementwise_fma(c, a, b)); }
 
 // ---------------------------------------------------------------------------------------------
-// Weight producers.  A step covers 128 k as two halves U = 0, 1 of 64 and eight sub-steps
-// (U, S), S = 0..3, of one MFMA k-block (16 k) each.  In sub-step (U, S), lane half h covers
+// Weight producers.  A step covers 256 k (one Q4_K / Q6_K super-block per row, eight Q4_0 /
+// Q8_0 blocks) as four halves U = 0..3 of 64 and sixteen sub-steps (U, S), S = 0..3, of one MFMA
+// k-block (16 k) each.  In sub-step (U, S), lane half h covers
 // k = 64U + 32*(S>>1) + 16*h + 8*(S&1) + (0..7) of the step.
 //   load()        one weight row's raw bytes for the whole step (issued a step ahead);
 //   scales<U>()   the f16 scale (and offset) pairs of half U's two 32-weight groups;
@@ -99,32 +104,32 @@ __device__ __forceinline__ uint32_t affine(h2 c, h2 a, h2 b) { return as_u32(__b
 // ---------------------------------------------------------------------------------------------
 struct PQ4K {
     static constexpr int kQK = kQK_K, kBytes = kBytesQ4_K;
-    struct Raw { u32x4p hd, q0, q1; };
+    struct Raw { u32x4p hd, q[4]; };
     struct Sc { h2 a0, b0, a1, b1; };
-    // step at k0 (multiple of 128): super-block k0/256, qs chunks c = c0 + U with c0 = (k0/64)%4
-    // (0 or 2); lane half h takes qs bytes 16h..16h+15 of the chunk (low nibbles: sub-block 2c,
-    // high: 2c+1).
+    // step at k0 (multiple of 256): super-block k0/256; half U is qs chunk c = U (low nibbles:
+    // sub-block 2c, high: 2c+1); lane half h takes qs bytes 16h..16h+15 of each chunk.
     __device__ static Raw load(const uint8_t* row, int k0, int h, int) {
         const uint8_t* sb = row + static_cast<size_t>(k0 >> 8) * kBytes;
-        const int c0 = (k0 >> 6) & 2;
         Raw r;
         r.hd = *reinterpret_cast<const u32x4p*>(sb);
-        r.q0 = *reinterpret_cast<const u32x4p*>(sb + 16 + 32 * c0 + 16 * h);
-        r.q1 = *reinterpret_cast<const u32x4p*>(sb + 48 + 32 * c0 + 16 * h);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) r.q[c] = *reinterpret_cast<const u32x4p*>(sb + 16 + 32 * c + 16 * h);
         return r;
     }
     template <int U>
-    __device__ static Sc scales(const Raw& r, int k0, int, int) {
-        // 6-bit scales/mins of sub-blocks 2c and 2c + 1 (bytes 2(c&1), 2(c&1)+1 of the packed
-        // scale words; sub-blocks 4..7 take their top bits from words 0/1).  c >= 2 is uniform,
-        // so the choice is a select, not a branch.
-        const bool upper = ((k0 >> 6) & 2) != 0;
-        constexpr int sh = 16 * U;
+    __device__ static Sc scales(const Raw& r, int, int, int) {
+        // 6-bit scales/mins of sub-blocks 2U and 2U + 1: bytes 2(U&1), 2(U&1)+1 of the packed
+        // scale words; sub-blocks 4..7 (U >= 2) take their top bits from words 0/1.
+        constexpr int sh = 16 * (U & 1);
         const uint32_t u0 = r.hd.y >> sh, u1 = r.hd.z >> sh, u2 = r.hd.w >> sh;
-        const uint32_t sc_lo = u0 & 0x3F3Fu, m_lo = u1 & 0x3F3Fu;
-        const uint32_t sc_hi = (u2 & 0x0F0Fu) | ((u0 >> 2) & 0x3030u);
-        const uint32_t m_hi = ((u2 >> 4) & 0x0F0Fu) | ((u1 >> 2) & 0x3030u);
-        const uint32_t scp = upper ? sc_hi : sc_lo, mp = upper ? m_hi : m_lo;
+        uint32_t scp, mp;
+        if constexpr (U < 2) {
+            scp = u0 & 0x3F3Fu;
+            mp = u1 & 0x3F3Fu;
+        } else {
+            scp = (u2 & 0x0F0Fu) | ((u0 >> 2) & 0x3030u);
+            mp = ((u2 >> 4) & 0x0F0Fu) | ((u1 >> 2) & 0x3030u);
+        }
         const float d = half_bits_to_float(r.hd.x), dmin = half_bits_to_float(r.hd.x >> 16);
         Sc s;
         s.a0 = splat(d * static_cast<float>(scp & 0xFFu));
@@ -135,8 +140,8 @@ struct PQ4K {
     }
     template <int U, int S>
     __device__ static void frag(const Raw& r, const Sc& sc, int, uint32_t f[4]) {
-        constexpr bool hi = S >= 2;  // high nibbles: sub-block 2c + 1
-        const u32x4p q = U ? r.q1 : r.q0;
+        constexpr bool hi = S >= 2;  // high nibbles: sub-block 2U + 1
+        const u32x4p q = r.q[U];
         const uint32_t w[2] = {(S & 1) ? q.z : q.x, (S & 1) ? q.w : q.y};
         const h2 off = splat(1024.0f);
 #pragma unroll
@@ -152,27 +157,29 @@ struct PQ4K {
 
 struct PQ6K {
     static constexpr int kQK = kQK_K, kBytes = kBytesQ6_K;
-    struct Raw { u32x4p la, lb, qh; uint32_t sc0, sc1, d; };
+    struct Raw { u32x4p la[2], lb[2], qh[2], sc; uint32_t d; };
     struct Sc { h2 a0, a1; };
-    // step at k0 (multiple of 128): super-block k0/256, half n2 = (k0/128)%2, quarter qt = 2n2 + U,
-    // groups t = 2U + (S>>1).  Lane half h takes l = 16h..16h+15 of ql (groups t even:
-    // ql[64n2 + l], odd: ql[64n2 + 32 + l]; both halves U share these bytes, U picks the nibble)
-    // and of qh[32n2 + l].
+    // step at k0 (multiple of 256): super-block k0/256; half U is quarter qt = U of the block:
+    // half n2 = U>>1 of 128 weights, groups t = 2(U&1) + (S>>1).  Lane half h takes l = 16h..16h+15
+    // of ql (groups t even: ql[64n2 + l], odd: ql[64n2 + 32 + l]; U&1 picks the nibble) and of
+    // qh[32n2 + l]; the sixteen int8 sub-scales arrive as one 16-byte load.
     __device__ static Raw load(const uint8_t* row, int k0, int h, int) {
         const uint8_t* sb = row + static_cast<size_t>(k0 >> 8) * kBytes;
-        const int n2 = (k0 >> 7) & 1;
         Raw r;
-        r.la = ld16(sb + 64 * n2 + 16 * h);
-        r.lb = ld16(sb + 64 * n2 + 32 + 16 * h);
-        r.qh = ld16(sb + 128 + 32 * n2 + 16 * h);
-        r.sc0 = ld4(sb + 192 + 8 * n2);  // sc[8n2 + 4U + h + {0, 2}]
-        r.sc1 = ld4(sb + 196 + 8 * n2);
+#pragma unroll
+        for (int n2 = 0; n2 < 2; ++n2) {
+            r.la[n2] = ld16(sb + 64 * n2 + 16 * h);
+            r.lb[n2] = ld16(sb + 64 * n2 + 32 + 16 * h);
+            r.qh[n2] = ld16(sb + 128 + 32 * n2 + 16 * h);
+        }
+        r.sc = ld16(sb + 192);
         r.d = ld2(sb + 208);
         return r;
     }
     template <int U>
     __device__ static Sc scales(const Raw& r, int, int h, int) {
-        const uint32_t sc = U ? r.sc1 : r.sc0;
+        // sub-scales sc[4U + h + {0, 2}]
+        const uint32_t sc = U == 0 ? r.sc.x : U == 1 ? r.sc.y : U == 2 ? r.sc.z : r.sc.w;
         const float d = half_bits_to_float(r.d);
         Sc s;
         s.a0 = splat(d * static_cast<float>(static_cast<int8_t>(sc >> (8 * h))));
@@ -181,11 +188,12 @@ struct PQ6K {
     }
     template <int U, int S>
     __device__ static void frag(const Raw& r, const Sc& sc, int, uint32_t f[4]) {
-        constexpr int nib = 4 * U, u = S >> 1;  // group t = 2U + u
-        constexpr int hs = nib + 2 * u;         // qh bit pair of the group
-        const u32x4p l = u ? r.lb : r.la;
+        constexpr int n2 = U >> 1, nib = 4 * (U & 1), u = S >> 1;  // group t = 2(U&1) + u
+        constexpr int hs = nib + 2 * u;                              // qh bit pair of the group
+        const u32x4p l = u ? r.lb[n2] : r.la[n2];
+        const u32x4p qh = r.qh[n2];
         const uint32_t lw[2] = {(S & 1) ? l.z : l.x, (S & 1) ? l.w : l.y};
-        const uint32_t hw[2] = {(S & 1) ? r.qh.z : r.qh.x, (S & 1) ? r.qh.w : r.qh.y};
+        const uint32_t hw[2] = {(S & 1) ? qh.z : qh.x, (S & 1) ? qh.w : qh.y};
         const h2 off = splat(1056.0f);  // 1024 + 32: codes q enter as 1024 + q, weight is a (q - 32)
         const h2 a = u ? sc.a1 : sc.a0;
 #pragma unroll
@@ -200,18 +208,18 @@ struct PQ6K {
     }
 };
 
-// 32-weight block formats: a step covers blocks k0/32 + b, b = 0..3 (block b absent when
+// 32-weight block formats: a step covers blocks k0/32 + b, b = 0..7 (block b absent when
 // kv <= 32b: load() clamps its address to block 0 and scales() zeroes its scale).  Half U
 // holds blocks 2U (S = 0, 1) and 2U + 1 (S = 2, 3).
 struct PQ80 {
     static constexpr int kQK = kQK8_0, kBytes = kBytesQ8_0;
-    struct Raw { u32x4p q[4]; uint32_t d[4]; };
+    struct Raw { u32x4p q[8]; uint32_t d[8]; };
     struct Sc { h2 a0, a1; };
     __device__ static Raw load(const uint8_t* row, int k0, int h, int kv) {
         const uint8_t* b0 = row + static_cast<size_t>(k0 >> 5) * kBytes;
         Raw r;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
+        for (int b = 0; b < 8; ++b) {
             const uint8_t* bb = kv > 32 * b ? b0 + b * kBytes : b0;
             r.q[b] = ld16(bb + 2 + 16 * h);
             r.d[b] = ld2(bb);  // always issued (static load count)
@@ -244,14 +252,14 @@ struct PQ80 {
 
 struct PQ40 {
     static constexpr int kQK = kQK4_0, kBytes = kBytesQ4_0;
-    struct Raw { u32x4p q[4]; uint32_t d[4]; };
+    struct Raw { u32x4p q[8]; uint32_t d[8]; };
     struct Sc { h2 a0, a1; };
     // lane half h takes the block's low (h = 0, k 0..15) or high (h = 1, k 16..31) nibbles.
     __device__ static Raw load(const uint8_t* row, int k0, int, int kv) {
         const uint8_t* b0 = row + static_cast<size_t>(k0 >> 5) * kBytes;
         Raw r;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
+        for (int b = 0; b < 8; ++b) {
             const uint8_t* bb = kv > 32 * b ? b0 + b * kBytes : b0;
             r.q[b] = ld16(bb + 2);
             r.d[b] = ld2(bb);  // always issued (static load count)
@@ -312,11 +320,17 @@ __device__ __forceinline__ void interleave_substep() {
 #undef QMM_PF_ROUND
 }
 
+// f(integral_constant<int, Q>) for Q = 0, 1, ... in order (compile-time sub-step indices).
+template <class F, int... Q>
+__device__ __forceinline__ void for_each_index(F& f, std::integer_sequence<int, Q...>) {
+    (f(std::integral_constant<int, Q>{}), ...);
+}
+
 template <class P, typename TC>
 __global__ __launch_bounds__(kThreads, 1)
 void prefill_kernel(const _Float16* __restrict__ A16, int lda, const uint8_t* __restrict__ W, TC* __restrict__ C,
                     float* __restrict__ part, int M, int N, int K, int klen, int tiles_m, int tiles_n, int ksplit) {
-    __shared__ __align__(16) u32x4p sA[2][2 * kChunksPerHalf];
+    __shared__ __align__(16) u32x4p sA[2][kHalves * kChunksPerHalf];
 
     // Tile order: m fastest, then n-tile, then k split; blocks sharing a weight slice (same
     // n-tile and k range, different m) are consecutive and dealt to one XCD.
@@ -353,16 +367,16 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, const uint8_t* __
         arow[j] = A16 + static_cast<size_t>(min(m0 + r, M - 1)) * lda + kb + 8 * c;
         apos[j] = p;
     }
-    auto load_a = [&](int t, u32x4p (&ar)[4]) {
+    auto load_a = [&](int t, u32x4p (&ar)[2 * kHalves]) {
         const int kk = min(t, nsteps - 1) * kBK;  // past the end: re-read the last step
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < kHalves; ++u)
 #pragma unroll
             for (int j = 0; j < 2; ++j) ar[2 * u + j] = *reinterpret_cast<const u32x4p*>(arow[j] + kk + 64 * u);
     };
-    auto store_a = [&](int slot, const u32x4p (&ar)[4]) {
+    auto store_a = [&](int slot, const u32x4p (&ar)[2 * kHalves]) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < kHalves; ++u)
 #pragma unroll
             for (int j = 0; j < 2; ++j) sA[slot][kChunksPerHalf * u + apos[j]] = ar[2 * u + j];
     };
@@ -386,19 +400,20 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, const uint8_t* __
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
 
-    // Software pipeline.  Step t (k0 = kb + 128t) runs sub-steps q = 0..7 (U = q/4, S = q%4).
+    // Software pipeline.  Step t (k0 = kb + 256t) runs sub-steps q = 0..15 (U = q/4, S = q%4).
     // While the 4 MFMAs of sub-step q run on wf[q&1] / af[q&1], the wave reads the activation
-    // fragments of q+1 from LDS and dequantizes its weight fragments into the other buffers.
+    // fragments of q+1 from LDS and dequantizes its weight fragment into the other buffers.
     //   q = 0: the raw bytes of step t+1 (into `nxt`) and A(t+1) (into `an`) are requested;
-    //   q = 1: scales of half 1 (from `cur`);  q = 5: scales of the next step's half 0 (`nxt`);
-    //   q = 6: after the reads for q = 7, A(t+1) goes to the free LDS slot, then the barrier
-    //          (after it, q = 7 reads the next step's first fragments from that slot);
-    //   q = 7: fragments of the next step's (0, 0) from `nxt`; at the end `cur` takes `nxt`.
+    //   q = 4U+1 (U < 3): scales of half U+1 (from `cur`) into sc[(U+1)&1];
+    //   q = 13: scales of the next step's half 0 (from `nxt`) into sc[0];
+    //   q = 14: after the reads for q = 15, A(t+1) goes to the free LDS slot, then the barrier
+    //           (after it, q = 15 reads the next step's first fragments from that slot);
+    //   q = 15: fragment of the next step's (0, 0) from `nxt`; at the end `cur` takes `nxt`.
     // The LDS slot (t+1)%2 last served step t-1, whose reads all precede step t-1's barrier, so
     // one barrier per step covers both the write-after-read and the read-after-write order.
     using Raw = typename P::Raw;
     using Sc = typename P::Sc;
-    u32x4p an[4];
+    u32x4p an[2 * kHalves];
     Raw cur, nxt;
     Sc sc[2];          // [half]
     uint32_t wf[2][4]; // [buffer][dword]
@@ -415,26 +430,28 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, const uint8_t* __
     for (int t = 0; t < nsteps; ++t) {
         const int k0 = kb + t * kBK;
         const int slot = t & 1;
-        // raw bytes first: they are consumed (q = 5) before A(t+1) is (q = 6)
+        // raw bytes first: they are consumed (q = 13) before A(t+1) is (q = 14)
         load_raw(t + 1, nxt);
         load_a(t + 1, an);
         __builtin_amdgcn_sched_barrier(0);
 
+        constexpr int kQ = 4 * kHalves;  // sub-steps per step
         auto sub = [&](auto qc) {
             constexpr int q = decltype(qc)::value;
-            constexpr int U = q >> 2, S = q & 3, B = q & 1;
-            constexpr int qn = q + 1, Un = (qn >> 2) & 1, Sn = qn & 3;
-            if constexpr (qn < 8) read_a(slot, Un, Sn, af[B ^ 1]);
-            if constexpr (q == 6) {
+            constexpr int U = q >> 2, B = q & 1;
+            constexpr int qn = q + 1, Un = qn >> 2, Sn = qn & 3;
+            if constexpr (qn < kQ) read_a(slot, Un, Sn, af[B ^ 1]);
+            if constexpr (q == kQ - 2) {
                 // free slot <- A(t+1).  The barrier comes after the last reads of this step's slot
-                // (those of q = 7, just issued), so the next step may overwrite it.
+                // (those of the last sub-step, just issued), so the next step may overwrite it.
                 store_a(slot ^ 1, an);
                 lds_barrier();
             }
-            if constexpr (qn == 8) read_a(slot ^ 1, 0, 0, af[B ^ 1]);
-            if constexpr (q == 1) sc[1] = P::template scales<1>(cur, k0, h, kend - k0);
-            if constexpr (q == 5) sc[0] = P::template scales<0>(nxt, k0 + kBK, h, kend - k0 - kBK);
-            if constexpr (qn < 8) P::template frag<Un, Sn>(cur, sc[Un], h, wf[B ^ 1]);
+            if constexpr (qn == kQ) read_a(slot ^ 1, 0, 0, af[B ^ 1]);
+            if constexpr ((q & 3) == 1 && U + 1 < kHalves)
+                sc[(U + 1) & 1] = P::template scales<(U + 1) % kHalves>(cur, k0, h, kend - k0);
+            if constexpr (q == kQ - 3) sc[0] = P::template scales<0>(nxt, k0 + kBK, h, kend - k0 - kBK);
+            if constexpr (qn < kQ) P::template frag<Un % kHalves, Sn>(cur, sc[Un & 1], h, wf[B ^ 1]);
             else P::template frag<0, 0>(nxt, sc[0], h, wf[B ^ 1]);
             f16x8 bw;
             __builtin_memcpy(&bw, wf[B], 16);
@@ -442,16 +459,8 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, const uint8_t* __
             for (int i = 0; i < 4; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bw, af[B][i], acc[i], 0, 0, 0);
             interleave_substep<5>();
             __builtin_amdgcn_sched_barrier(0);
-            (void)U; (void)S;
         };
-        sub(std::integral_constant<int, 0>{});
-        sub(std::integral_constant<int, 1>{});
-        sub(std::integral_constant<int, 2>{});
-        sub(std::integral_constant<int, 3>{});
-        sub(std::integral_constant<int, 4>{});
-        sub(std::integral_constant<int, 5>{});
-        sub(std::integral_constant<int, 6>{});
-        sub(std::integral_constant<int, 7>{});
+        for_each_index(sub, std::make_integer_sequence<int, kQ>{});
         cur = nxt;
     }
 
@@ -596,9 +605,9 @@ hipError_t launch_p(const void* A, const void* W, void* C, int M, int N, int K, 
     const int tiles_n = (N + kBN - 1) / kBN;
     const int steps = (K + kBK - 1) / kBK;
     // split K while the grid would still cover at most half the CUs (the partial-sum pass costs
-    // 4 * (ksplit + 1) * M * N bytes), keeping at least 8 steps per split
+    // 4 * (ksplit + 1) * M * N bytes), keeping at least 4 steps (1024 k) per split
     int ksplit = 1;
-    while (tiles_m * tiles_n * ksplit * 2 <= cus && steps / (ksplit * 2) >= 8) ksplit *= 2;
+    while (tiles_m * tiles_n * ksplit * 2 <= cus && steps / (ksplit * 2) >= 4) ksplit *= 2;
     const int klen = ((steps + ksplit - 1) / ksplit) * kBK;
     ksplit = (steps * kBK + klen - 1) / klen;
 
