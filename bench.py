@@ -21,6 +21,7 @@ Q4_0 4096 x 4096 case, prefill M = 512 with the vendor f16 GEMM on dense weights
 GEMV ones on rotated weight copies larger than the 256 MB MALL.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-extra] [--no-cpu-baseline] [--pmc-workload]
+       [--prefill-only]
 """
 
 from __future__ import annotations
@@ -171,24 +172,28 @@ class Workload:
         self.descs_py.clear()
 
 
-def run_workload(torch, qmm, hip, wl, steps, warmup):
-    """Average ms per step (one qmm_gemm_batch call over all descriptors) and wall seconds."""
+def run_workload(torch, qmm, hip, wl, steps, warmup, per_step=None):
+    """Average ms per step (one qmm_gemm_batch call over all descriptors) and wall seconds.
+    With `per_step` (a list), a HIP event is also recorded between steps and each step's duration
+    in ms is appended to it (for the median / p95)."""
     stream = torch.cuda.current_stream().cuda_stream
     plain = wl.descs()
     for _ in range(warmup):
         qmm.check(qmm.lib().qmm_gemm_batch(plain, len(plain), stream))
     torch.cuda.synchronize()
-    t_start, t_end = hip.event(), hip.event()
+    evs = [hip.event() for _ in range(steps + 1)]
     wall0 = time.perf_counter()
-    hip.record(t_start, stream)
-    for _ in range(steps):
+    hip.record(evs[0], stream)
+    for i in range(steps):
         qmm.check(qmm.lib().qmm_gemm_batch(plain, len(plain), stream))
-    hip.record(t_end, stream)
+        hip.record(evs[i + 1], stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
-    total_ms = hip.elapsed_ms(t_start, t_end)
-    hip.destroy(t_start)
-    hip.destroy(t_end)
+    total_ms = hip.elapsed_ms(evs[0], evs[-1])
+    if per_step is not None:
+        per_step.extend(hip.elapsed_ms(evs[i], evs[i + 1]) for i in range(steps))
+    for e in evs:
+        hip.destroy(e)
     return total_ms / steps, wall
 
 
@@ -361,6 +366,8 @@ def main():
     ap.add_argument("--layers", type=int, default=80)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="run only the prefill section (8B M=512 shapes) and print its results as JSON")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run only the counter-collection workload (copy calibration + dominant GEMV)")
     args = ap.parse_args()
@@ -383,6 +390,10 @@ def main():
     if args.pmc_workload:
         pmc_workload(torch, qmm, dev, gen)
         return
+    if args.prefill_only:
+        print(json.dumps({"prefill_8b_m512": run_prefill(torch, qmm, hip, gen, dev, max(3, args.steps // 2), 2)}),
+              flush=True)
+        return
 
     # ---- headline: Llama-3-70B Q4_K_M, M=1, 80 distinct layers -----------------------------
     t0 = time.perf_counter()
@@ -391,10 +402,14 @@ def main():
     wl = Workload(torch, qmm, "70b", [specs70], args.layers, 1, dev, gen, dominant=dominant)
     torch.cuda.synchronize()
     log(f"70B weights ready: {wl.weight_bytes / 1e9:.2f} GB in {time.perf_counter() - t0:.1f} s")
-    ms, wall = run_workload(torch, qmm, hip, wl, args.steps, args.warmup)
+    step_ms = []
+    ms, wall = run_workload(torch, qmm, hip, wl, args.steps, args.warmup, per_step=step_ms)
+    step_ms.sort()
+    p50 = step_ms[len(step_ms) // 2]
+    p95 = step_ms[min(len(step_ms) - 1, int(round(0.95 * (len(step_ms) - 1))))]
     gbs = wl.algo_bytes / (ms * 1e-3) / 1e9
-    log(f"70B M=1: {ms:.3f} ms/token, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM peak), "
-        f"wall {wall:.3f} s for {args.steps} steps")
+    log(f"70B M=1: {ms:.3f} ms/token (median {p50:.3f}, p95 {p95:.3f}), {gbs:.1f} GB/s "
+        f"({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM peak), wall {wall:.3f} s for {args.steps} steps")
     dom_bytes = 2 * weight_bytes(Q4_K, 28672, 8192) + 4 * 8192 + 2 * 4 * 28672
     dom_us, dom_launches = run_dominant(torch, qmm, hip, wl, max(2, args.steps // 4))
     dom_gbs = dom_bytes / (dom_us * 1e-6) / 1e9
@@ -507,7 +522,8 @@ def main():
                    "weights_GB": round(wl_bytes_gb(args.layers), 2), "gemvs_per_step": 7 * args.layers,
                    "launches_per_step": 4 * args.layers,
                    "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
-                   "tokens_per_s": round(1e3 / ms, 1)},
+                   "tokens_per_s": round(1e3 / ms, 1),
+                   "ms_per_token_p50": round(p50, 4), "ms_per_token_p95": round(p95, 4)},
         "roofline": {"bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "gemv_resident_kernel<GQ4K, M=1>, fused gate+up (2 x Q4_K 28672x8192)",
