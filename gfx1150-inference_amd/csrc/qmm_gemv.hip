@@ -209,6 +209,9 @@ struct GQ6K {
         return r;
     }
     // Chunk cj: group t = cj/2 (q1..q4 of the reference), bytes 8*(cj&1) .. +7 of the slices.
+    // Per dword of 4 codes: the 6-bit unsigned codes u = q + 32 are assembled byte-wise (low 4
+    // bits from ql, the qh bit pair of group t masked in place), then v_perm makes the fp16
+    // pairs (1024 + u) of bytes (0, 2) and (1, 3).
     __device__ static void chunk_codes(const Raw& r, int cj, const Consts& K, uint32_t out[4]) {
         const int t = cj >> 1;
         const bool second = (cj & 1) != 0;
@@ -217,23 +220,12 @@ struct GQ6K {
         const uint32_t H[2] = {second ? r.qh.z : r.qh.x, second ? r.qh.w : r.qh.y};
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            // bytes 0,2 then bytes 1,3 of the dword
-#pragma unroll
-            for (int odd = 0; odd < 2; ++odd) {
-                const uint32_t l = odd ? (L[i] >> 8) : L[i];
-                const uint32_t hb = odd ? (H[i] >> 8) : H[i];
-                uint32_t code;
-                if (t < 2) {
-                    // q = (l & 15) | ((qh >> 2t) & 3) << 4, entering as 1024 + q
-                    const uint32_t hs = t == 0 ? (hb << 4) : (hb << 2);
-                    code = and_or((l & 0x000F000Fu) | (hs & ~0x000F000Fu), K.m3f, K.mg);
-                } else {
-                    // q = (l >> 4) | ((qh >> 2t) & 3) << 4, entering as 1024 + 16q
-                    const uint32_t hs = t == 2 ? (hb << 4) : (hb << 2);
-                    code = and_or((l & 0x00F000F0u) | (hs & ~0x00F000F0u), K.m3f0, K.mg);
-                }
-                out[2 * i + odd] = code;
-            }
+            const uint32_t lo4 = (t < 2 ? L[i] : L[i] >> 4) & 0x0F0F0F0Fu;
+            // bits 2t, 2t+1 of each qh byte -> bits 4, 5
+            const uint32_t hs = t == 0 ? H[i] << 4 : t == 1 ? H[i] << 2 : t == 2 ? H[i] : H[i] >> 2;
+            const uint32_t u = and_or(hs, 0x30303030u, lo4);
+            out[2 * i] = __builtin_amdgcn_perm(K.mg, u, 0x07020500u);
+            out[2 * i + 1] = __builtin_amdgcn_perm(K.mg, u, 0x07030501u);
         }
     }
     __device__ static void group_scales(const Raw& r, int lane, bool valid, float a[kG], float B[kG]) {
@@ -245,10 +237,9 @@ struct GQ6K {
             const uint32_t w = t < 2 ? r.s0 : r.s1;
             const int sh = 8 * (h + 2 * (t & 1));
             const float s = d * static_cast<float>(static_cast<int8_t>(w >> sh));
-            // codes q + 32 enter as 1024 + (q+32) (t < 2) or 1024 + 16(q+32) (t >= 2)
-            const float ag = t < 2 ? s : s * 0.0625f;
-            a[t] = valid ? ag : 0.0f;
-            B[t] = valid ? ag * (t < 2 ? 1056.0f : 1536.0f) : 0.0f;
+            // codes q + 32 enter as 1024 + (q + 32)
+            a[t] = valid ? s : 0.0f;
+            B[t] = valid ? s * 1056.0f : 0.0f;
         }
     }
 };
