@@ -34,6 +34,13 @@
 
 #include "qmm_device.h"
 
+#ifndef QMM_PF_WIDE
+#define QMM_PF_WIDE 1
+#endif
+#ifndef QMM_PF_WIDE_VALU
+#define QMM_PF_WIDE_VALU 3
+#endif
+
 namespace qmm {
 namespace {
 
@@ -92,9 +99,9 @@ __device__ __forceinline__ void bytes_to_h2(uint32_t x, h2 sub, h2& lo, h2& hi) 
 __device__ __forceinline__ uint32_t affine(h2 c, h2 a, h2 b) { return as_u32(__builtin_elementwise_fma(c, a, b)); }
 
 // ---------------------------------------------------------------------------------------------
-// Weight producers.  A step covers 256 k (one Q4_K / Q6_K super-block per row, eight Q4_0 /
-// Q8_0 blocks) as four halves U = 0..3 of 64 and sixteen sub-steps (U, S), S = 0..3, of one MFMA
-// k-block (16 k) each.  In sub-step (U, S), lane half h covers
+// Weight producers, for steps of H halves of 64 k (H = 4: one Q4_K / Q6_K super-block or eight
+// Q4_0 / Q8_0 blocks per step; H = 2: half of that).  A step runs 4H sub-steps (U, S), U < H,
+// S = 0..3, of one MFMA k-block (16 k) each; in sub-step (U, S), lane half h covers
 // k = 64U + 32*(S>>1) + 16*h + 8*(S&1) + (0..7) of the step.
 //   load()        one weight row's raw bytes for the whole step (issued a step ahead);
 //   scales<U>()   the f16 scale (and offset) pairs of half U's two 32-weight groups;
@@ -102,33 +109,42 @@ __device__ __forceinline__ uint32_t affine(h2 c, h2 a, h2 b) { return as_u32(__b
 // kv = K - k0 lets the 32-weight formats zero a K tail; the zeroing happens in scales(), so no
 // prefetched value is consumed before its sub-step.
 // ---------------------------------------------------------------------------------------------
+template <int H>
 struct PQ4K {
+    static_assert(H == 2 || H == 4, "steps of 128 or 256 k");
     static constexpr int kQK = kQK_K, kBytes = kBytesQ4_K;
-    struct Raw { u32x4p hd, q[4]; };
+    struct Raw { u32x4p hd, q[H]; };
     struct Sc { h2 a0, b0, a1, b1; };
-    // step at k0 (multiple of 256): super-block k0/256; half U is qs chunk c = U (low nibbles:
-    // sub-block 2c, high: 2c+1); lane half h takes qs bytes 16h..16h+15 of each chunk.
+    // step at k0 (multiple of 64H): super-block k0/256, qs chunks c = c0 + U with c0 = (k0/64)%4
+    // (always 0 when H = 4); lane half h takes qs bytes 16h..16h+15 of chunk c (low nibbles:
+    // sub-block 2c, high: 2c+1).
     __device__ static Raw load(const uint8_t* row, int k0, int h, int) {
         const uint8_t* sb = row + static_cast<size_t>(k0 >> 8) * kBytes;
+        const int c0 = H == 4 ? 0 : ((k0 >> 6) & 2);
         Raw r;
         r.hd = *reinterpret_cast<const u32x4p*>(sb);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) r.q[c] = *reinterpret_cast<const u32x4p*>(sb + 16 + 32 * c + 16 * h);
+        for (int c = 0; c < H; ++c) r.q[c] = *reinterpret_cast<const u32x4p*>(sb + 16 + 32 * (c0 + c) + 16 * h);
         return r;
     }
     template <int U>
-    __device__ static Sc scales(const Raw& r, int, int, int) {
-        // 6-bit scales/mins of sub-blocks 2U and 2U + 1: bytes 2(U&1), 2(U&1)+1 of the packed
-        // scale words; sub-blocks 4..7 (U >= 2) take their top bits from words 0/1.
+    __device__ static Sc scales(const Raw& r, int k0, int, int) {
+        // 6-bit scales/mins of sub-blocks 2c and 2c + 1: bytes 2(c&1), 2(c&1)+1 of the packed
+        // scale words; sub-blocks 4..7 (c >= 2) take their top bits from words 0/1.  With H = 2
+        // the choice is uniform over the step, so it is a select, not a branch.
         constexpr int sh = 16 * (U & 1);
         const uint32_t u0 = r.hd.y >> sh, u1 = r.hd.z >> sh, u2 = r.hd.w >> sh;
+        const uint32_t sc_lo = u0 & 0x3F3Fu, m_lo = u1 & 0x3F3Fu;
+        const uint32_t sc_hi = (u2 & 0x0F0Fu) | ((u0 >> 2) & 0x3030u);
+        const uint32_t m_hi = ((u2 >> 4) & 0x0F0Fu) | ((u1 >> 2) & 0x3030u);
         uint32_t scp, mp;
-        if constexpr (U < 2) {
-            scp = u0 & 0x3F3Fu;
-            mp = u1 & 0x3F3Fu;
+        if constexpr (H == 4) {
+            scp = U < 2 ? sc_lo : sc_hi;
+            mp = U < 2 ? m_lo : m_hi;
         } else {
-            scp = (u2 & 0x0F0Fu) | ((u0 >> 2) & 0x3030u);
-            mp = ((u2 >> 4) & 0x0F0Fu) | ((u1 >> 2) & 0x3030u);
+            const bool upper = ((k0 >> 6) & 2) != 0;
+            scp = upper ? sc_hi : sc_lo;
+            mp = upper ? m_hi : m_lo;
         }
         const float d = half_bits_to_float(r.hd.x), dmin = half_bits_to_float(r.hd.x >> 16);
         Sc s;
@@ -140,7 +156,7 @@ struct PQ4K {
     }
     template <int U, int S>
     __device__ static void frag(const Raw& r, const Sc& sc, int, uint32_t f[4]) {
-        constexpr bool hi = S >= 2;  // high nibbles: sub-block 2U + 1
+        constexpr bool hi = S >= 2;  // high nibbles: sub-block 2c + 1
         const u32x4p q = r.q[U];
         const uint32_t w[2] = {(S & 1) ? q.z : q.x, (S & 1) ? q.w : q.y};
         const h2 off = splat(1024.0f);
@@ -155,31 +171,42 @@ struct PQ4K {
     }
 };
 
+template <int H>
 struct PQ6K {
+    static_assert(H == 2 || H == 4, "steps of 128 or 256 k");
     static constexpr int kQK = kQK_K, kBytes = kBytesQ6_K;
-    struct Raw { u32x4p la[2], lb[2], qh[2], sc; uint32_t d; };
+    struct Raw { u32x4p la[H / 2], lb[H / 2], qh[H / 2]; uint32_t sc[H], d; };
     struct Sc { h2 a0, a1; };
-    // step at k0 (multiple of 256): super-block k0/256; half U is quarter qt = U of the block:
-    // half n2 = U>>1 of 128 weights, groups t = 2(U&1) + (S>>1).  Lane half h takes l = 16h..16h+15
-    // of ql (groups t even: ql[64n2 + l], odd: ql[64n2 + 32 + l]; U&1 picks the nibble) and of
-    // qh[32n2 + l]; the sixteen int8 sub-scales arrive as one 16-byte load.
+    // step at k0 (multiple of 64H): super-block k0/256.  Half U covers the block's 64-weight
+    // quarter 2*n2 + (U&1) of 128-weight half n2 = U>>1 (H = 4) or (k0/128)%2 (H = 2), groups
+    // t = 2(U&1) + (S>>1).  Lane half h takes l = 16h..16h+15 of ql (groups t even: ql[64n2 + l],
+    // odd: ql[64n2 + 32 + l]; U&1 picks the nibble) and of qh[32n2 + l]; sub-scale word U holds
+    // sc[8n2 + 4(U&1) + (0..3)].
     __device__ static Raw load(const uint8_t* row, int k0, int h, int) {
         const uint8_t* sb = row + static_cast<size_t>(k0 >> 8) * kBytes;
+        const int nb = H == 4 ? 0 : ((k0 >> 7) & 1);
         Raw r;
 #pragma unroll
-        for (int n2 = 0; n2 < 2; ++n2) {
-            r.la[n2] = ld16(sb + 64 * n2 + 16 * h);
-            r.lb[n2] = ld16(sb + 64 * n2 + 32 + 16 * h);
-            r.qh[n2] = ld16(sb + 128 + 32 * n2 + 16 * h);
+        for (int j = 0; j < H / 2; ++j) {
+            const int n2 = nb + j;
+            r.la[j] = ld16(sb + 64 * n2 + 16 * h);
+            r.lb[j] = ld16(sb + 64 * n2 + 32 + 16 * h);
+            r.qh[j] = ld16(sb + 128 + 32 * n2 + 16 * h);
         }
-        r.sc = ld16(sb + 192);
+        if constexpr (H == 4) {
+            const u32x4p s = ld16(sb + 192);
+            r.sc[0] = s.x, r.sc[1] = s.y, r.sc[2] = s.z, r.sc[3] = s.w;
+        } else {
+            r.sc[0] = ld4(sb + 192 + 8 * nb);
+            r.sc[1] = ld4(sb + 196 + 8 * nb);
+        }
         r.d = ld2(sb + 208);
         return r;
     }
     template <int U>
     __device__ static Sc scales(const Raw& r, int, int h, int) {
-        // sub-scales sc[4U + h + {0, 2}]
-        const uint32_t sc = U == 0 ? r.sc.x : U == 1 ? r.sc.y : U == 2 ? r.sc.z : r.sc.w;
+        // sub-scales of word U, bytes h and h + 2
+        const uint32_t sc = r.sc[U];
         const float d = half_bits_to_float(r.d);
         Sc s;
         s.a0 = splat(d * static_cast<float>(static_cast<int8_t>(sc >> (8 * h))));
@@ -188,38 +215,39 @@ struct PQ6K {
     }
     template <int U, int S>
     __device__ static void frag(const Raw& r, const Sc& sc, int, uint32_t f[4]) {
-        constexpr int n2 = U >> 1, nib = 4 * (U & 1), u = S >> 1;  // group t = 2(U&1) + u
-        constexpr int hs = nib + 2 * u;                              // qh bit pair of the group
-        const u32x4p l = u ? r.lb[n2] : r.la[n2];
-        const u32x4p qh = r.qh[n2];
+        constexpr int j = U >> 1, nib = 4 * (U & 1), u = S >> 1;  // group t = 2(U&1) + u
+        constexpr int hs = nib + 2 * u;                             // qh bit pair of the group
+        const u32x4p l = u ? r.lb[j] : r.la[j];
+        const u32x4p qh = r.qh[j];
         const uint32_t lw[2] = {(S & 1) ? l.z : l.x, (S & 1) ? l.w : l.y};
         const uint32_t hw[2] = {(S & 1) ? qh.z : qh.x, (S & 1) ? qh.w : qh.y};
         const h2 off = splat(1056.0f);  // 1024 + 32: codes q enter as 1024 + q, weight is a (q - 32)
         const h2 a = u ? sc.a1 : sc.a0;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint32_t lo4 = (lw[j] >> nib) & 0x0F0F0F0Fu;
-            const uint32_t hi2 = ((hw[j] >> hs) & 0x03030303u) << 4;
+        for (int jj = 0; jj < 2; ++jj) {
+            const uint32_t lo4 = (lw[jj] >> nib) & 0x0F0F0F0Fu;
+            const uint32_t hi2 = ((hw[jj] >> hs) & 0x03030303u) << 4;
             h2 p, q;
             bytes_to_h2(lo4 | hi2, off, p, q);
-            f[2 * j] = as_u32(p * a);
-            f[2 * j + 1] = as_u32(q * a);
+            f[2 * jj] = as_u32(p * a);
+            f[2 * jj + 1] = as_u32(q * a);
         }
     }
 };
 
-// 32-weight block formats: a step covers blocks k0/32 + b, b = 0..7 (block b absent when
+// 32-weight block formats: a step covers blocks k0/32 + b, b < 2H (block b absent when
 // kv <= 32b: load() clamps its address to block 0 and scales() zeroes its scale).  Half U
 // holds blocks 2U (S = 0, 1) and 2U + 1 (S = 2, 3).
+template <int H>
 struct PQ80 {
     static constexpr int kQK = kQK8_0, kBytes = kBytesQ8_0;
-    struct Raw { u32x4p q[8]; uint32_t d[8]; };
+    struct Raw { u32x4p q[2 * H]; uint32_t d[2 * H]; };
     struct Sc { h2 a0, a1; };
     __device__ static Raw load(const uint8_t* row, int k0, int h, int kv) {
         const uint8_t* b0 = row + static_cast<size_t>(k0 >> 5) * kBytes;
         Raw r;
 #pragma unroll
-        for (int b = 0; b < 8; ++b) {
+        for (int b = 0; b < 2 * H; ++b) {
             const uint8_t* bb = kv > 32 * b ? b0 + b * kBytes : b0;
             r.q[b] = ld16(bb + 2 + 16 * h);
             r.d[b] = ld2(bb);  // always issued (static load count)
@@ -250,16 +278,17 @@ struct PQ80 {
     }
 };
 
+template <int H>
 struct PQ40 {
     static constexpr int kQK = kQK4_0, kBytes = kBytesQ4_0;
-    struct Raw { u32x4p q[8]; uint32_t d[8]; };
+    struct Raw { u32x4p q[2 * H]; uint32_t d[2 * H]; };
     struct Sc { h2 a0, a1; };
     // lane half h takes the block's low (h = 0, k 0..15) or high (h = 1, k 16..31) nibbles.
     __device__ static Raw load(const uint8_t* row, int k0, int, int kv) {
         const uint8_t* b0 = row + static_cast<size_t>(k0 >> 5) * kBytes;
         Raw r;
 #pragma unroll
-        for (int b = 0; b < 8; ++b) {
+        for (int b = 0; b < 2 * H; ++b) {
             const uint8_t* bb = kv > 32 * b ? b0 + b * kBytes : b0;
             r.q[b] = ld16(bb + 2);
             r.d[b] = ld2(bb);  // always issued (static load count)
@@ -492,6 +521,235 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, const uint8_t* __
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Wide tile for M >= 256: one wave per SIMD, each wave owns 64 weight rows x 256 activation rows
+// (16 MFMA tiles of 32 x 32, 256 fp32 accumulators in the AGPR file).  Every dequantized weight
+// fragment feeds 8 MFMAs and every activation fragment read from LDS feeds 2, so a sub-step
+// issues 16 MFMAs (512 matrix-core cycles) against ~40 VALU and 8 LDS reads: the dequantization
+// and the LDS traffic hide under the matrix core within one wave instead of depending on two
+// waves interleaving.
+//   * Workgroup: 4 waves, tile 256 (m) x 256 (n); steps of 128 k (H = 2 producer halves).
+//   * Activation tile of a step: 256 x 128 f16 = 64 KiB, double-buffered in LDS (128 KiB).  The
+//     next step's tile is requested at the start of the current step with direct global -> LDS
+//     loads (no staging registers, no LDS write instructions); one barrier per step.
+//   * Raw weight bytes of the next step (two rows per lane) are loaded at the start of a step.
+// ---------------------------------------------------------------------------------------------
+constexpr int kWBM = 256;       // activation rows per workgroup tile
+constexpr int kWBN = 256;       // weight rows per workgroup tile (64 per wave)
+constexpr int kWH = 2;          // 64-k halves per step
+constexpr int kWBK = 64 * kWH;  // k per step
+constexpr int kWThreads = 256;  // 4 waves, one per SIMD
+constexpr int kWChunksPerHalf = kWBM * 64 / 8;  // 16-byte chunks per 64-k half stage = 2048
+
+// Direct global -> LDS load of 16 bytes per lane (global_load_lds_dwordx4): lane l's bytes land
+// at the wave-uniform LDS address of `lds` plus 16 l.  Issued as inline assembly, so the
+// compiler's wait counting covers only the ordinary loads and LDS reads; the caller waits for
+// these with an explicit vmcnt(0) before the barrier that publishes the stage.  (Memory operations
+// unknown to the compiler can only make its own vmcnt / lgkmcnt waits wait longer.)
+__device__ __forceinline__ void lds_direct_load16(const void* g, const u32x4p* lds) {
+    const uint32_t la = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));  // LDS offset
+    __asm__ volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(la) : "memory", "m0");
+}
+
+// Instruction interleave of one wide sub-step: sixteen rounds of one MFMA, one LDS read (eight
+// exist) and V VALU operations.
+template <int V>
+__device__ __forceinline__ void interleave_wide() {
+#define QMM_PF_ROUND                                   \
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); \
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); \
+    __builtin_amdgcn_sched_group_barrier(0x002, V, 0);
+    QMM_PF_ROUND QMM_PF_ROUND QMM_PF_ROUND QMM_PF_ROUND QMM_PF_ROUND QMM_PF_ROUND QMM_PF_ROUND QMM_PF_ROUND
+    QMM_PF_ROUND QMM_PF_ROUND QMM_PF_ROUND QMM_PF_ROUND QMM_PF_ROUND QMM_PF_ROUND QMM_PF_ROUND QMM_PF_ROUND
+#undef QMM_PF_ROUND
+}
+
+template <class P, typename TC>
+__global__ __launch_bounds__(kWThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void prefill_wide_kernel(const _Float16* __restrict__ A16, int lda, const uint8_t* __restrict__ W, TC* __restrict__ C,
+                         float* __restrict__ part, int M, int N, int K, int klen, int tiles_m, int tiles_n, int ksplit) {
+    // two separate arrays (not one [2][...] array) so that the compiler's tracking of the direct
+    // loads into one of them adds no waits to the reads of the other
+    __shared__ __align__(16) u32x4p sA0[kWH * kWChunksPerHalf];
+    __shared__ __align__(16) u32x4p sA1[kWH * kWChunksPerHalf];
+
+    // Tile order as in prefill_kernel: m fastest, then n-tile, then k split, dealt to XCDs in runs.
+    const int tiles = tiles_m * tiles_n * ksplit;
+    int b = blockIdx.x;
+    if (tiles % 8 == 0) b = (b % 8) * (tiles / 8) + b / 8;
+    const int tm = b % tiles_m;
+    const int tn = (b / tiles_m) % tiles_n;
+    const int kz = b / (tiles_m * tiles_n);
+    const int m0 = tm * kWBM, n0 = tn * kWBN;
+    const int kb = kz * klen;
+    const int kend = min(K, kb + klen);
+    const int nsteps = (kend - kb + kWBK - 1) / kWBK;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5;
+    const int l32 = lane & 31;
+
+    const size_t row_bytes = static_cast<size_t>(K / P::kQK) * P::kBytes;
+    const uint8_t* wrow[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+        wrow[nb] = W + static_cast<size_t>(min(n0 + 64 * wv + 32 * nb + l32, N - 1)) * row_bytes;
+
+    // Thread tid copies chunks p = tid + 256j (j = 0..7) of each half stage: row (tid >> 3) + 32j,
+    // stored in place at p, holding logical chunk c = (tid & 7) ^ swizzle(row) (the swizzle of
+    // a_slot() is the same for all eight rows).  aoff[j]: element offset of the row's chunk c.
+    // The copy is a direct global -> LDS load (global_load_lds_dwordx4): lane l of wave wv
+    // writes 16 bytes at the wave-uniform base chunk 2048u + 256j + 64wv plus l, i.e. at p.
+    const int ac = (tid & 7) ^ ((tid >> 4) & 7);
+    uint32_t aoff[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        aoff[j] = static_cast<uint32_t>(min(m0 + (tid >> 3) + 32 * j, M - 1)) * static_cast<uint32_t>(lda) +
+                  static_cast<uint32_t>(kb + 8 * ac);
+    auto copy_a = [&](int t, u32x4p* dst) {
+        const int kk = min(t, nsteps - 1) * kWBK;  // past the end: re-read the last step
+#pragma unroll
+        for (int u = 0; u < kWH; ++u)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                lds_direct_load16(A16 + aoff[j] + kk + 64 * u, dst + kWChunksPerHalf * u + 256 * j + 64 * wv);
+    };
+    using Raw = typename P::Raw;
+    using Sc = typename P::Sc;
+    auto load_raw = [&](int t, Raw (&raw)[2]) {
+        const int k0 = kb + min(t, nsteps - 1) * kWBK;
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) raw[nb] = P::load(wrow[nb], k0, h, kend - k0);
+    };
+    auto read_a = [&](const u32x4p* stage, int U, int S, f16x8 (&af)[8]) {
+        const u32x4p* sa = stage + kWChunksPerHalf * U;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const u32x4p av = sa[a_slot(32 * i + l32, a_chunk(S, h))];
+            __builtin_memcpy(&af[i], &av, 16);
+        }
+    };
+
+    f32x16 acc[2][8];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[nb][i][v] = 0.0f;
+
+    // Software pipeline.  Step t (k0 = kb + 128t) runs sub-steps q = 0..7 (U = q/4, S = q%4) on
+    // the stage held in sA0 (t even) or sA1 (t odd).  While the 16 MFMAs of sub-step q run on
+    // wf[q&1] / af[q&1], the wave reads the activation fragments of q+1 from LDS and dequantizes
+    // its two weight fragments into the other buffers.
+    //   q = 0: the direct loads of A(t+1) into the other stage, then the raw bytes of step t+1
+    //          (into `nxt`), are issued;
+    //   q = 1: scales of half 1 (from `cur`);
+    //   q = 5: scales of the next step's half 0 (from `nxt`);
+    //   q = 7: first this wave's loads (A(t+1), `nxt`) and LDS reads (issued a sub-step earlier)
+    //          complete, then the barrier; then the fragments of the next step's (0, 0):
+    //          activations from the other stage, weights from `nxt`; at the end `cur` takes `nxt`.
+    // The other stage last served step t-1, whose reads all precede step t-1's barrier, so one
+    // barrier per step covers both the write-after-read and the read-after-write order.
+    Raw cur[2], nxt[2];
+    Sc sc[2][2];          // [weight block][half]
+    uint32_t wf[2][2][4]; // [buffer][weight block][dword]
+    f16x8 af[2][8];       // [buffer][activation block]
+
+    load_raw(0, cur);
+    copy_a(0, sA0);
+    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+    lds_barrier();
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        sc[nb][0] = P::template scales<0>(cur[nb], kb, h, kend - kb);
+        P::template frag<0, 0>(cur[nb], sc[nb][0], h, wf[0][nb]);
+    }
+    read_a(sA0, 0, 0, af[0]);
+
+    auto step = [&](auto stage_c, int t) {
+        constexpr bool odd = decltype(stage_c)::value != 0;
+        const u32x4p* const s_cur = odd ? sA1 : sA0;
+        u32x4p* const s_nxt = odd ? sA0 : sA1;
+        const int k0 = kb + t * kWBK;
+        copy_a(t + 1, s_nxt);
+        load_raw(t + 1, nxt);
+        __builtin_amdgcn_sched_barrier(0);
+
+        constexpr int kQ = 4 * kWH;  // sub-steps per step
+        auto sub = [&](auto qc) {
+            constexpr int q = decltype(qc)::value;
+            constexpr int B = q & 1;
+            constexpr int qn = q + 1, Un = qn >> 2, Sn = qn & 3;
+            if constexpr (qn == kQ) {
+                __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): A(t+1) is in LDS
+                lds_barrier();
+                read_a(s_nxt, 0, 0, af[B ^ 1]);
+            } else {
+                read_a(s_cur, Un, Sn, af[B ^ 1]);
+            }
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                if constexpr (q == 1) sc[nb][1] = P::template scales<1>(cur[nb], k0, h, kend - k0);
+                if constexpr (q == kQ - 3) sc[nb][0] = P::template scales<0>(nxt[nb], k0 + kWBK, h, kend - k0 - kWBK);
+                if constexpr (qn < kQ) P::template frag<Un, Sn>(cur[nb], sc[nb][Un], h, wf[B ^ 1][nb]);
+                else P::template frag<0, 0>(nxt[nb], sc[nb][0], h, wf[B ^ 1][nb]);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) {
+                    f16x8 bw;
+                    __builtin_memcpy(&bw, wf[B][nb], 16);
+                    acc[nb][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bw, af[B][i], acc[nb][i], 0, 0, 0);
+                }
+            interleave_wide<QMM_PF_WIDE_VALU>();
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        for_each_index(sub, std::make_integer_sequence<int, kQ>{});
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) cur[nb] = nxt[nb];
+    };
+    int t = 0;
+    for (; t + 1 < nsteps; t += 2) {
+        step(std::integral_constant<int, 0>{}, t);
+        step(std::integral_constant<int, 1>{}, t + 1);
+    }
+    if (t < nsteps) step(std::integral_constant<int, 0>{}, t);
+
+    // D element v of tile (nb, i): weight row n = n0 + 64wv + 32nb + 8(v/4) + 4h + v%4,
+    // activation row m = m0 + 32i + l32.
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int m = m0 + 32 * i + l32;
+        if (m >= M) continue;
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int n = n0 + 64 * wv + 32 * nb + 8 * g + 4 * h;
+                const float vs[4] = {acc[nb][i][4 * g], acc[nb][i][4 * g + 1], acc[nb][i][4 * g + 2],
+                                     acc[nb][i][4 * g + 3]};
+                if (ksplit > 1) {
+                    float* dst = part + (static_cast<size_t>(kz) * M + m) * N;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (n + e < N) dst[n + e] = vs[e];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if (n + e < N) {
+                            if constexpr (sizeof(TC) == 4) reinterpret_cast<float*>(C)[static_cast<size_t>(m) * N + n + e] = vs[e];
+                            else reinterpret_cast<uint16_t*>(C)[static_cast<size_t>(m) * N + n + e] = float_to_half_bits(vs[e]);
+                        }
+                    }
+                }
+            }
+    }
+}
+
 // fp32 / fp16 activations [M, K] -> f16 [M, lda] (round to nearest even; columns K..lda-1 zero).
 template <typename TA>
 __global__ __launch_bounds__(256) void to_f16_kernel(const TA* __restrict__ A, _Float16* __restrict__ out, int M, int K,
@@ -596,23 +854,42 @@ hipError_t cu_count(int& cus) {
     return hipSuccess;
 }
 
-template <class P, typename TA, typename TC>
+// The wide tile pays off once a 256-row activation tile is mostly filled (M >= 256, and padding M
+// to 256 costs at most 64 rows more than padding it to 128) and its tiles cover at least half the
+// CUs without splitting K (one workgroup per CU; a split costs a partial-sum pass).  Its element
+// offsets are 32-bit.
+bool use_wide(int M, int N, int K, int cus) {
+#if QMM_PF_WIDE
+    const int64_t pad256 = (static_cast<int64_t>(M) + kWBM - 1) / kWBM * kWBM;
+    const int64_t pad128 = (static_cast<int64_t>(M) + kBM - 1) / kBM * kBM;
+    const int64_t lda = (static_cast<int64_t>(K) + kWBK - 1) / kWBK * kWBK;
+    const int64_t tiles = (pad256 / kWBM) * ((static_cast<int64_t>(N) + kWBN - 1) / kWBN);
+    return M >= kWBM && pad256 <= pad128 + 64 && 2 * tiles >= cus && static_cast<int64_t>(M) * lda < (int64_t{1} << 31);
+#else
+    (void)M, (void)N, (void)K, (void)cus;
+    return false;
+#endif
+}
+
+template <class P, typename TA, typename TC, bool Wide>
 hipError_t launch_p(const void* A, const void* W, void* C, int M, int N, int K, hipStream_t stream) {
+    constexpr int BM = Wide ? kWBM : kBM, BN = Wide ? kWBN : kBN, BK = Wide ? kWBK : kBK;
+    constexpr int threads = Wide ? kWThreads : kThreads;
     int cus = 0;
     hipError_t e = cu_count(cus);
     if (e != hipSuccess) return e;
-    const int tiles_m = (M + kBM - 1) / kBM;
-    const int tiles_n = (N + kBN - 1) / kBN;
-    const int steps = (K + kBK - 1) / kBK;
+    const int tiles_m = (M + BM - 1) / BM;
+    const int tiles_n = (N + BN - 1) / BN;
+    const int steps = (K + BK - 1) / BK;
     // split K while the grid would still cover at most half the CUs (the partial-sum pass costs
-    // 4 * (ksplit + 1) * M * N bytes), keeping at least 4 steps (1024 k) per split
+    // 4 * (ksplit + 1) * M * N bytes), keeping at least 1024 k per split
     int ksplit = 1;
-    while (tiles_m * tiles_n * ksplit * 2 <= cus && steps / (ksplit * 2) >= 4) ksplit *= 2;
-    const int klen = ((steps + ksplit - 1) / ksplit) * kBK;
-    ksplit = (steps * kBK + klen - 1) / klen;
+    while (tiles_m * tiles_n * ksplit * 2 <= cus && steps / (ksplit * 2) >= 1024 / BK) ksplit *= 2;
+    const int klen = ((steps + ksplit - 1) / ksplit) * BK;
+    ksplit = (steps * BK + klen - 1) / klen;
 
-    const bool direct = sizeof(TA) == 2 && K % kBK == 0 && (reinterpret_cast<uintptr_t>(A) & 15u) == 0;
-    const int lda = direct ? K : steps * kBK;
+    const bool direct = sizeof(TA) == 2 && K % BK == 0 && (reinterpret_cast<uintptr_t>(A) & 15u) == 0;
+    const int lda = direct ? K : steps * BK;
     const size_t a_bytes = direct ? 0 : static_cast<size_t>(M) * lda * 2;
     const size_t p_bytes = ksplit > 1 ? static_cast<size_t>(ksplit) * M * N * 4 : 0;
     void* ws = nullptr;
@@ -628,8 +905,14 @@ hipError_t launch_p(const void* A, const void* W, void* C, int M, int N, int K, 
     }
     float* part = ksplit > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + ((a_bytes + 255) / 256) * 256) : nullptr;
     const int tiles = tiles_m * tiles_n * ksplit;
-    hipLaunchKernelGGL((prefill_kernel<P, TC>), dim3(tiles), dim3(kThreads), 0, stream, a16, lda,
-                       static_cast<const uint8_t*>(W), static_cast<TC*>(C), part, M, N, K, klen, tiles_m, tiles_n, ksplit);
+    if constexpr (Wide)
+        hipLaunchKernelGGL((prefill_wide_kernel<P, TC>), dim3(tiles), dim3(threads), 0, stream, a16, lda,
+                           static_cast<const uint8_t*>(W), static_cast<TC*>(C), part, M, N, K, klen, tiles_m, tiles_n,
+                           ksplit);
+    else
+        hipLaunchKernelGGL((prefill_kernel<P, TC>), dim3(tiles), dim3(threads), 0, stream, a16, lda,
+                           static_cast<const uint8_t*>(W), static_cast<TC*>(C), part, M, N, K, klen, tiles_m, tiles_n,
+                           ksplit);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (ksplit > 1) {
         const int64_t mn = static_cast<int64_t>(M) * N;
@@ -640,13 +923,22 @@ hipError_t launch_p(const void* A, const void* W, void* C, int M, int N, int K, 
     return hipSuccess;
 }
 
+template <template <int> class PF, typename TA, typename TC>
+hipError_t launch_family(const void* A, const void* W, void* C, int M, int N, int K, hipStream_t stream) {
+    int cus = 0;
+    hipError_t e = cu_count(cus);
+    if (e != hipSuccess) return e;
+    if (use_wide(M, N, K, cus)) return launch_p<PF<kWH>, TA, TC, true>(A, W, C, M, N, K, stream);
+    return launch_p<PF<kHalves>, TA, TC, false>(A, W, C, M, N, K, stream);
+}
+
 template <typename TA, typename TC>
 hipError_t dispatch_p(int t, const void* A, const void* W, void* C, int M, int N, int K, hipStream_t stream) {
     switch (t) {
-        case QMM_TYPE_Q4_K: return launch_p<PQ4K, TA, TC>(A, W, C, M, N, K, stream);
-        case QMM_TYPE_Q6_K: return launch_p<PQ6K, TA, TC>(A, W, C, M, N, K, stream);
-        case QMM_TYPE_Q8_0: return launch_p<PQ80, TA, TC>(A, W, C, M, N, K, stream);
-        case QMM_TYPE_Q4_0: return launch_p<PQ40, TA, TC>(A, W, C, M, N, K, stream);
+        case QMM_TYPE_Q4_K: return launch_family<PQ4K, TA, TC>(A, W, C, M, N, K, stream);
+        case QMM_TYPE_Q6_K: return launch_family<PQ6K, TA, TC>(A, W, C, M, N, K, stream);
+        case QMM_TYPE_Q8_0: return launch_family<PQ80, TA, TC>(A, W, C, M, N, K, stream);
+        case QMM_TYPE_Q4_0: return launch_family<PQ40, TA, TC>(A, W, C, M, N, K, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -5,8 +5,9 @@ Bars (written into each check):
 * max_i|y_i - yo_i| / max_i|yo_i| <= 1e-5 against the fp64 product of the kernel's f16 operands
   (activations rounded to f16, weights from gguf_oracle.dequantize_f16_operands; only the fp32
   accumulation differs), which pins dequantization, scale rounding and the k ordering;
-* edge shapes: M, N not multiples of the 128 x 256 tile, K tails of 32 for Q4_0 / Q8_0,
-  fp16 and fp32 activations and outputs; the Llama-3-8B prefill shapes (M = 512) on sampled rows.
+* edge shapes: M, N not multiples of the 128 x 256 tile (M < 256) or of the 256 x 256 wide tile
+  (M >= 256), K tails of 32 for Q4_0 / Q8_0, split K, fp16 and fp32 activations and outputs; the
+  Llama-3-8B prefill shapes (M = 512) on sampled rows.
 """
 
 import zlib
@@ -49,6 +50,21 @@ def shapes(t):
     return [(32, 256, 512), (128, 512, 2048), (200, 300, 544), (129, 257, 96), (40, 64, 32)]
 
 
+def wide_shapes(t):
+    # The 256 x 256 tile serves M >= 256 when its tiles cover at least half the CUs (>= 128 tiles):
+    # exact tiles, ragged M / N with a K tail, and a K long enough to split over workgroups.
+    if t in (O.GGML_Q4_K, O.GGML_Q6_K):
+        return [(256, 32768, 256), (400, 16428, 1280), (256, 32768, 4096)]
+    return [(256, 32768, 128), (448, 16420, 544), (256, 32768, 4096)]
+
+
+def sampled_cols(rng, N):
+    # output columns (weight rows) checked against the oracle: random ones plus the first and
+    # the last tile's
+    cols = set(rng.choice(N, size=40, replace=False).tolist()) | {0, 1, N - 2, N - 1, (N // 256) * 256}
+    return np.array(sorted(c for c in cols if c < N))
+
+
 def test_prefill_threshold(dev):
     import qmm
     assert qmm.gemv_max_m() == 32
@@ -63,6 +79,25 @@ def test_prefill_vs_fp64_and_f16_operands(dev, t):
         y = run(t, x, raw, N, K, dev)
         assert O.max_rel_err(y, O.matmul_f64(t, x, raw, N, K)) <= TOL_F64, (O.TYPE_NAMES[t], M, N, K)
         assert O.max_rel_err(y, O.matmul_f16_operands(t, x, raw, N, K)) <= TOL_F16, (O.TYPE_NAMES[t], M, N, K)
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_prefill_wide_tile_vs_fp64_and_f16_operands(dev, t):
+    rng = np.random.default_rng(4100 + t)
+    for i, (M, N, K) in enumerate(wide_shapes(t)):
+        raw = O.synth_weights(t, N, K, rng)
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        y = run(t, x, raw, N, K, dev, a16=i == 1, c16=i == 2)
+        assert np.all(np.isfinite(y))
+        if i == 1:
+            x = x.astype(np.float16).astype(np.float32)  # the activations the kernel was given
+        cols = sampled_cols(rng, N)
+        rb = O.weight_bytes(t, 1, K)
+        sub = np.concatenate([raw[r * rb:(r + 1) * rb] for r in cols])
+        ys = y[:, cols]
+        assert O.max_rel_err(ys, O.matmul_f64(t, x, sub, cols.size, K)) <= TOL_F64, (O.TYPE_NAMES[t], M, N, K)
+        tol = 1e-3 if i == 2 else TOL_F16  # fp16 output: one more rounding of each result
+        assert O.max_rel_err(ys, O.matmul_f16_operands(t, x, sub, cols.size, K)) <= tol, (O.TYPE_NAMES[t], M, N, K)
 
 
 @pytest.mark.parametrize("t", TYPES)
