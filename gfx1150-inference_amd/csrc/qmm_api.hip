@@ -128,16 +128,19 @@ Span w_span(const qmm_gemm_desc& d) {
 }
 Span c_span(const qmm_gemm_desc& d) { return span_of(d.C, static_cast<size_t>(d.M) * d.N * dtype_bytes(d.c_dtype)); }
 
-// Descriptors [i, j) may run as one GEMV launch: same activations, dtypes, type, M and K; GEMV
-// sizes; no events between them; and no output overlapping another output or any input, so the
-// fused launch computes exactly what the sequential launches would.
+// Descriptors [i, j) may run as one launch: same activations, dtypes, type, M and K; no events
+// between them; no output overlapping another output or any input, so the fused launch computes
+// what the sequential launches would; and, for prefill sizes, weights the prefill kernel takes.
 bool fusable(const qmm_gemm_desc* d, int i, int j) {
     const qmm_gemm_desc& h = d[i];
-    if (h.M <= 0 || h.M >= qmm::kGemvMaxM) return false;
+    if (h.M <= 0) return false;
+    const bool prefill = h.M >= qmm::kGemvMaxM;
     for (int x = i; x < j; ++x) {
         const qmm_gemm_desc& e = d[x];
         if (e.N <= 0 || e.A != h.A || e.a_dtype != h.a_dtype || e.ggml_type != h.ggml_type ||
             e.c_dtype != h.c_dtype || e.M != h.M || e.K != h.K)
+            return false;
+        if (prefill && !qmm::gemm_prefill_supported(e.ggml_type, e.a_dtype, e.c_dtype, e.M, e.N, e.K, e.A, e.W, e.C))
             return false;
         if ((x > i && e.ev_before) || (x + 1 < j && e.ev_after)) return false;
         const Span c = c_span(e);
@@ -228,10 +231,10 @@ int qmm_gemm_batch(const qmm_gemm_desc* descs, int count, void* stream) {
         if (ev && (e = hipEventRecord(static_cast<hipEvent_t>(ev), s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
         return QMM_OK;
     };
-    const int max_fused = qmm::gemv_max_fused();
     int i = 0;
     while (i < count) {
-        // longest run starting at i that one GEMV launch can serve
+        // longest run starting at i that one launch can serve
+        const int max_fused = descs[i].M >= qmm::kGemvMaxM ? qmm::prefill_max_fused() : qmm::gemv_max_fused();
         int j = i + 1;
         while (j < count && j - i < max_fused && fusable(descs, i, j + 1)) ++j;
         if (j - i >= 2) {
@@ -246,7 +249,10 @@ int qmm_gemm_batch(const qmm_gemm_desc* descs, int count, void* stream) {
             const qmm_gemm_desc& h = descs[i];
             int rc = record(h.ev_before);
             if (rc != QMM_OK) return rc;
-            hipError_t e = qmm::launch_gemv_fused(h.ggml_type, h.A, h.a_dtype, h.c_dtype, h.M, h.K, W, C, N, j - i, s);
+            hipError_t e = h.M >= qmm::kGemvMaxM
+                               ? qmm::launch_gemm_prefill_fused(h.ggml_type, h.A, h.a_dtype, h.c_dtype, h.M, h.K, W, C, N,
+                                                                j - i, s)
+                               : qmm::launch_gemv_fused(h.ggml_type, h.A, h.a_dtype, h.c_dtype, h.M, h.K, W, C, N, j - i, s);
             if (e == hipSuccess) {
                 if ((rc = record(descs[j - 1].ev_after)) != QMM_OK) return rc;
                 i = j;

@@ -56,6 +56,11 @@ hipError_t launch_gemm_prefill(int ggml_type, const void* A, int a_dtype, const 
                                int c_dtype, int M, int N, int K, hipStream_t stream);
 bool gemm_prefill_supported(int ggml_type, int a_dtype, int c_dtype, int M, int N, int K,
                             const void* A, const void* W, const void* C);
+// Prefill of several weight matrices (same type and K, each passing gemm_prefill_supported) times
+// the same activations in one launch: their output tiles share one grid.
+hipError_t launch_gemm_prefill_fused(int ggml_type, const void* A, int a_dtype, int c_dtype, int M, int K,
+                                     const void* const* W, void* const* C, const int* N, int count, hipStream_t stream);
+int prefill_max_fused();
 // Frees the prefill workspaces (f16 activations, split-K partials) of every device, after
 // synchronizing each device.
 hipError_t release_prefill_workspaces();

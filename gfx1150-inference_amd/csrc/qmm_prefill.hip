@@ -26,6 +26,7 @@
 //   * Narrow N (few tiles): the K range is split over workgroups; partial tiles land in a
 //     workspace and a second pass adds them in a fixed order (deterministic).
 //   * Tiles sharing a weight slice are placed on the same XCD (L2 reuse of the packed bytes).
+#include <climits>
 #include <mutex>
 #include <string>
 #include <type_traits>
@@ -319,6 +320,30 @@ struct PQ40 {
     }
 };
 
+// Output segments of one launch: consecutive weight matrices that multiply the same activations
+// (q/k/v, gate/up).  Their n-tiles are concatenated; tile_end[s] is the cumulative n-tile count
+// through segment s (INT_MAX for unused entries), part_off[s] the offset of segment s's split-K
+// partial block ([ksplit][M][N_s] fp32) in the partial workspace.
+constexpr int kPfMaxSegs = 4;
+template <typename TC>
+struct PfSegs {
+    const uint8_t* W[kPfMaxSegs];
+    TC* C[kPfMaxSegs];
+    int N[kPfMaxSegs];
+    int tile_end[kPfMaxSegs];
+    size_t part_off[kPfMaxSegs];
+};
+
+// Segment of the workgroup's n-tile tn (uniform), and tn's index inside that segment.
+template <typename TC>
+__device__ __forceinline__ int pf_seg_of(const PfSegs<TC>& sg, int& tn) {
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < kPfMaxSegs - 1; ++i) s += tn >= sg.tile_end[i] ? 1 : 0;
+    if (s > 0) tn -= sg.tile_end[s - 1];
+    return s;
+}
+
 // Activation chunk (row r, chunk c = 8 f16) position inside a 1024-chunk half stage: rows are
 // XOR-swizzled so that 16 consecutive rows read at one chunk hit 16 different bank groups.
 __device__ __forceinline__ int a_slot(int r, int c) { return 8 * r + (c ^ ((r >> 1) & 7)); }
@@ -357,8 +382,8 @@ __device__ __forceinline__ void for_each_index(F& f, std::integer_sequence<int, 
 
 template <class P, typename TC>
 __global__ __launch_bounds__(kThreads, 1)
-void prefill_kernel(const _Float16* __restrict__ A16, int lda, const uint8_t* __restrict__ W, TC* __restrict__ C,
-                    float* __restrict__ part, int M, int N, int K, int klen, int tiles_m, int tiles_n, int ksplit) {
+void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, float* __restrict__ part_base, int M, int K,
+                    int klen, int tiles_m, int tiles_n, int ksplit) {
     __shared__ __align__(16) u32x4p sA[2][kHalves * kChunksPerHalf];
 
     // Tile order: m fastest, then n-tile, then k split; blocks sharing a weight slice (same
@@ -367,8 +392,13 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, const uint8_t* __
     int b = blockIdx.x;
     if (tiles % 8 == 0) b = (b % 8) * (tiles / 8) + b / 8;
     const int tm = b % tiles_m;
-    const int tn = (b / tiles_m) % tiles_n;
+    int tn = (b / tiles_m) % tiles_n;
     const int kz = b / (tiles_m * tiles_n);
+    const int sgi = pf_seg_of(sg, tn);
+    const uint8_t* __restrict__ W = sg.W[sgi];
+    TC* __restrict__ C = sg.C[sgi];
+    const int N = sg.N[sgi];
+    float* __restrict__ part = part_base + sg.part_off[sgi];
     const int m0 = tm * kBM, n0 = tn * kBN;
     const int kb = kz * klen;
     const int kend = min(K, kb + klen);
@@ -566,8 +596,8 @@ __device__ __forceinline__ void interleave_wide() {
 
 template <class P, typename TC>
 __global__ __launch_bounds__(kWThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void prefill_wide_kernel(const _Float16* __restrict__ A16, int lda, const uint8_t* __restrict__ W, TC* __restrict__ C,
-                         float* __restrict__ part, int M, int N, int K, int klen, int tiles_m, int tiles_n, int ksplit) {
+void prefill_wide_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, float* __restrict__ part_base, int M,
+                         int K, int klen, int tiles_m, int tiles_n, int ksplit) {
     // two separate arrays (not one [2][...] array) so that the compiler's tracking of the direct
     // loads into one of them adds no waits to the reads of the other
     __shared__ __align__(16) u32x4p sA0[kWH * kWChunksPerHalf];
@@ -578,8 +608,13 @@ void prefill_wide_kernel(const _Float16* __restrict__ A16, int lda, const uint8_
     int b = blockIdx.x;
     if (tiles % 8 == 0) b = (b % 8) * (tiles / 8) + b / 8;
     const int tm = b % tiles_m;
-    const int tn = (b / tiles_m) % tiles_n;
+    int tn = (b / tiles_m) % tiles_n;
     const int kz = b / (tiles_m * tiles_n);
+    const int sgi = pf_seg_of(sg, tn);
+    const uint8_t* __restrict__ W = sg.W[sgi];
+    TC* __restrict__ C = sg.C[sgi];
+    const int N = sg.N[sgi];
+    float* __restrict__ part = part_base + sg.part_off[sgi];
     const int m0 = tm * kWBM, n0 = tn * kWBN;
     const int kb = kz * klen;
     const int kend = min(K, kb + klen);
@@ -858,28 +893,39 @@ hipError_t cu_count(int& cus) {
 // to 256 costs at most 64 rows more than padding it to 128) and its tiles cover at least half the
 // CUs without splitting K (one workgroup per CU; a split costs a partial-sum pass).  Its element
 // offsets are 32-bit.
-bool use_wide(int M, int N, int K, int cus) {
+bool use_wide(int M, int64_t wide_tiles_n, int K, int cus) {
 #if QMM_PF_WIDE
     const int64_t pad256 = (static_cast<int64_t>(M) + kWBM - 1) / kWBM * kWBM;
     const int64_t pad128 = (static_cast<int64_t>(M) + kBM - 1) / kBM * kBM;
     const int64_t lda = (static_cast<int64_t>(K) + kWBK - 1) / kWBK * kWBK;
-    const int64_t tiles = (pad256 / kWBM) * ((static_cast<int64_t>(N) + kWBN - 1) / kWBN);
+    const int64_t tiles = (pad256 / kWBM) * wide_tiles_n;
     return M >= kWBM && pad256 <= pad128 + 64 && 2 * tiles >= cus && static_cast<int64_t>(M) * lda < (int64_t{1} << 31);
 #else
-    (void)M, (void)N, (void)K, (void)cus;
+    (void)M, (void)wide_tiles_n, (void)K, (void)cus;
     return false;
 #endif
 }
 
+struct PfSeg {
+    const void* W;
+    void* C;
+    int N;
+};
+
 template <class P, typename TA, typename TC, bool Wide>
-hipError_t launch_p(const void* A, const void* W, void* C, int M, int N, int K, hipStream_t stream) {
+hipError_t launch_p(const void* A, const PfSeg* segs, int nseg, int M, int K, hipStream_t stream) {
     constexpr int BM = Wide ? kWBM : kBM, BN = Wide ? kWBN : kBN, BK = Wide ? kWBK : kBK;
     constexpr int threads = Wide ? kWThreads : kThreads;
     int cus = 0;
     hipError_t e = cu_count(cus);
     if (e != hipSuccess) return e;
     const int tiles_m = (M + BM - 1) / BM;
-    const int tiles_n = (N + BN - 1) / BN;
+    int tiles_n = 0;
+    int64_t n_total = 0;
+    for (int i = 0; i < nseg; ++i) {
+        tiles_n += (segs[i].N + BN - 1) / BN;
+        n_total += segs[i].N;
+    }
     const int steps = (K + BK - 1) / BK;
     // split K while the grid would still cover at most half the CUs (the partial-sum pass costs
     // 4 * (ksplit + 1) * M * N bytes), keeping at least 1024 k per split
@@ -891,7 +937,7 @@ hipError_t launch_p(const void* A, const void* W, void* C, int M, int N, int K, 
     const bool direct = sizeof(TA) == 2 && K % BK == 0 && (reinterpret_cast<uintptr_t>(A) & 15u) == 0;
     const int lda = direct ? K : steps * BK;
     const size_t a_bytes = direct ? 0 : static_cast<size_t>(M) * lda * 2;
-    const size_t p_bytes = ksplit > 1 ? static_cast<size_t>(ksplit) * M * N * 4 : 0;
+    const size_t p_bytes = ksplit > 1 ? static_cast<size_t>(ksplit) * M * n_total * 4 : 0;
     void* ws = nullptr;
     if (a_bytes + p_bytes > 0 && (e = workspace(stream, a_bytes + p_bytes + 256, &ws)) != hipSuccess) return e;
     const _Float16* a16 = static_cast<const _Float16*>(A);
@@ -904,43 +950,68 @@ hipError_t launch_p(const void* A, const void* W, void* C, int M, int N, int K, 
         a16 = dst;
     }
     float* part = ksplit > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + ((a_bytes + 255) / 256) * 256) : nullptr;
+    PfSegs<TC> sg;
+    size_t off = 0;
+    int tiles_acc = 0;
+    for (int i = 0; i < kPfMaxSegs; ++i) {
+        const bool used = i < nseg;
+        sg.W[i] = used ? static_cast<const uint8_t*>(segs[i].W) : nullptr;
+        sg.C[i] = used ? static_cast<TC*>(segs[i].C) : nullptr;
+        sg.N[i] = used ? segs[i].N : 0;
+        if (used) tiles_acc += (segs[i].N + BN - 1) / BN;
+        sg.tile_end[i] = used ? tiles_acc : INT_MAX;
+        sg.part_off[i] = off;
+        if (used && ksplit > 1) off += static_cast<size_t>(ksplit) * M * segs[i].N;
+    }
     const int tiles = tiles_m * tiles_n * ksplit;
     if constexpr (Wide)
-        hipLaunchKernelGGL((prefill_wide_kernel<P, TC>), dim3(tiles), dim3(threads), 0, stream, a16, lda,
-                           static_cast<const uint8_t*>(W), static_cast<TC*>(C), part, M, N, K, klen, tiles_m, tiles_n,
-                           ksplit);
+        hipLaunchKernelGGL((prefill_wide_kernel<P, TC>), dim3(tiles), dim3(threads), 0, stream, a16, lda, sg, part, M, K,
+                           klen, tiles_m, tiles_n, ksplit);
     else
-        hipLaunchKernelGGL((prefill_kernel<P, TC>), dim3(tiles), dim3(threads), 0, stream, a16, lda,
-                           static_cast<const uint8_t*>(W), static_cast<TC*>(C), part, M, N, K, klen, tiles_m, tiles_n,
-                           ksplit);
+        hipLaunchKernelGGL((prefill_kernel<P, TC>), dim3(tiles), dim3(threads), 0, stream, a16, lda, sg, part, M, K, klen,
+                           tiles_m, tiles_n, ksplit);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (ksplit > 1) {
-        const int64_t mn = static_cast<int64_t>(M) * N;
-        hipLaunchKernelGGL((reduce_kernel<TC>), dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, stream, part,
-                           static_cast<TC*>(C), mn, ksplit);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
+        for (int i = 0; i < nseg; ++i) {
+            const int64_t mn = static_cast<int64_t>(M) * segs[i].N;
+            hipLaunchKernelGGL((reduce_kernel<TC>), dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, stream,
+                               part + sg.part_off[i], sg.C[i], mn, ksplit);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
     }
     return hipSuccess;
 }
 
 template <template <int> class PF, typename TA, typename TC>
-hipError_t launch_family(const void* A, const void* W, void* C, int M, int N, int K, hipStream_t stream) {
+hipError_t launch_family(const void* A, const PfSeg* segs, int nseg, int M, int K, hipStream_t stream) {
     int cus = 0;
     hipError_t e = cu_count(cus);
     if (e != hipSuccess) return e;
-    if (use_wide(M, N, K, cus)) return launch_p<PF<kWH>, TA, TC, true>(A, W, C, M, N, K, stream);
-    return launch_p<PF<kHalves>, TA, TC, false>(A, W, C, M, N, K, stream);
+    int64_t wide_tiles_n = 0;
+    for (int i = 0; i < nseg; ++i) wide_tiles_n += (segs[i].N + kWBN - 1) / kWBN;
+    if (use_wide(M, wide_tiles_n, K, cus)) return launch_p<PF<kWH>, TA, TC, true>(A, segs, nseg, M, K, stream);
+    return launch_p<PF<kHalves>, TA, TC, false>(A, segs, nseg, M, K, stream);
 }
 
 template <typename TA, typename TC>
-hipError_t dispatch_p(int t, const void* A, const void* W, void* C, int M, int N, int K, hipStream_t stream) {
+hipError_t dispatch_p(int t, const void* A, const PfSeg* segs, int nseg, int M, int K, hipStream_t stream) {
     switch (t) {
-        case QMM_TYPE_Q4_K: return launch_family<PQ4K, TA, TC>(A, W, C, M, N, K, stream);
-        case QMM_TYPE_Q6_K: return launch_family<PQ6K, TA, TC>(A, W, C, M, N, K, stream);
-        case QMM_TYPE_Q8_0: return launch_family<PQ80, TA, TC>(A, W, C, M, N, K, stream);
-        case QMM_TYPE_Q4_0: return launch_family<PQ40, TA, TC>(A, W, C, M, N, K, stream);
+        case QMM_TYPE_Q4_K: return launch_family<PQ4K, TA, TC>(A, segs, nseg, M, K, stream);
+        case QMM_TYPE_Q6_K: return launch_family<PQ6K, TA, TC>(A, segs, nseg, M, K, stream);
+        case QMM_TYPE_Q8_0: return launch_family<PQ80, TA, TC>(A, segs, nseg, M, K, stream);
+        case QMM_TYPE_Q4_0: return launch_family<PQ40, TA, TC>(A, segs, nseg, M, K, stream);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t dispatch_dtypes(int t, const void* A, int a_dtype, int c_dtype, const PfSeg* segs, int nseg, int M, int K,
+                           hipStream_t stream) {
+    if (a_dtype == QMM_DTYPE_F32) {
+        if (c_dtype == QMM_DTYPE_F32) return dispatch_p<float, float>(t, A, segs, nseg, M, K, stream);
+        return dispatch_p<float, __half>(t, A, segs, nseg, M, K, stream);
+    }
+    if (c_dtype == QMM_DTYPE_F32) return dispatch_p<__half, float>(t, A, segs, nseg, M, K, stream);
+    return dispatch_p<__half, __half>(t, A, segs, nseg, M, K, stream);
 }
 
 }  // namespace
@@ -958,12 +1029,18 @@ bool gemm_prefill_supported(int ggml_type, int a_dtype, int c_dtype, int M, int 
 
 hipError_t launch_gemm_prefill(int ggml_type, const void* A, int a_dtype, const void* W, void* C, int c_dtype, int M,
                                int N, int K, hipStream_t stream) {
-    if (a_dtype == QMM_DTYPE_F32) {
-        if (c_dtype == QMM_DTYPE_F32) return dispatch_p<float, float>(ggml_type, A, W, C, M, N, K, stream);
-        return dispatch_p<float, __half>(ggml_type, A, W, C, M, N, K, stream);
-    }
-    if (c_dtype == QMM_DTYPE_F32) return dispatch_p<__half, float>(ggml_type, A, W, C, M, N, K, stream);
-    return dispatch_p<__half, __half>(ggml_type, A, W, C, M, N, K, stream);
+    const PfSeg seg{W, C, N};
+    return dispatch_dtypes(ggml_type, A, a_dtype, c_dtype, &seg, 1, M, K, stream);
+}
+
+int prefill_max_fused() { return kPfMaxSegs; }
+
+hipError_t launch_gemm_prefill_fused(int ggml_type, const void* A, int a_dtype, int c_dtype, int M, int K,
+                                     const void* const* W, void* const* C, const int* N, int count, hipStream_t stream) {
+    if (count < 1 || count > kPfMaxSegs) return hipErrorInvalidValue;
+    PfSeg segs[kPfMaxSegs];
+    for (int i = 0; i < count; ++i) segs[i] = PfSeg{W[i], C[i], N[i]};
+    return dispatch_dtypes(ggml_type, A, a_dtype, c_dtype, segs, count, M, K, stream);
 }
 
 }  // namespace qmm

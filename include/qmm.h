@@ -85,7 +85,12 @@ typedef struct qmm_gemm_desc {
 /* Validates every descriptor, then launches them back to back on `stream` in order
  * (no host synchronisation).  Replaces the per-projection launches of the reference's
  * device-resident layer pipeline (src/kernels/attention.hip:650-687, project_on_device
- * :572-599) for callers that keep weights resident. */
+ * :572-599) for callers that keep weights resident.
+ * Consecutive descriptors with the same A, a_dtype, c_dtype, ggml_type, M and K, no event
+ * between them and no output overlapping another output or any input (q/k/v, gate/up) run as
+ * one launch.  GEMV sizes (M < qmm_gemv_max_m()) give results bit-identical to separate calls;
+ * prefill sizes share one grid, which may change how K is split over workgroups and therefore
+ * the fp32 summation order (within the prefill accuracy bound). */
 int qmm_gemm_batch(const qmm_gemm_desc* descs, int count, void* stream);
 
 /* dequant(W) -> out[num_elements] in out_dtype (F16, BF16 or F32), bit-exact.

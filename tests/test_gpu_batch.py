@@ -1,10 +1,14 @@
-"""GPU tests of qmm_gemm_batch (C ABI), including the fused launch of consecutive GEMV
-descriptors that share their activations (the q/k/v and gate/up projections of a layer).
+"""GPU tests of qmm_gemm_batch (C ABI), including the fused launch of consecutive descriptors
+that share their activations (the q/k/v and gate/up projections of a layer).
 
 Bars (written into each check):
-* a batch computes exactly what the same descriptors launched one by one compute: outputs are
-  bit-identical to single qmm_gemm calls, fused or not;
-* every output is within max_i|y_i - y64_i| / max_i|y64_i| <= 1e-3 of fp64 on the exact weights;
+* GEMV sizes: a batch computes exactly what the same descriptors launched one by one compute:
+  outputs are bit-identical to single qmm_gemm calls, fused or not;
+* every GEMV output is within max_i|y_i - y64_i| / max_i|y64_i| <= 1e-3 of fp64 on the exact
+  weights;
+* prefill sizes: fused outputs are within 1e-5 (same measure) of single calls and of the fp64
+  product of the kernel's f16 operands (only the fp32 summation order may differ), and within
+  1e-2 of fp64 on the exact weights;
 * descriptors whose outputs overlap each other or the shared input keep sequential semantics.
 """
 
@@ -172,3 +176,77 @@ def test_batch_mixed_types_and_unaligned_weights(dev):
         assert O.max_rel_err(c.cpu().numpy().astype(np.float64), O.matmul_f64(t, x, raw, n, K)) <= GEMV_TOL
     assert torch.equal(Ca.cpu(), single(t4, A, Wa, 256, K, torch.float32))
     assert torch.equal(Cc.cpu(), single(t6, A, Wc, 192, K, torch.float32))
+
+
+PF_TOL_F16 = 1e-5
+PF_TOL_F64 = 1e-2
+
+
+def single_any(t, A, W, N, K, out_dtype):
+    return single(t, A, W, N, K, out_dtype).float().numpy().astype(np.float64)
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_batch_prefill_shared_input_fused(dev, t):
+    # q/k/v-like (8:2:2 rows) on one input, then a gate/up-like pair on another, M = 96.
+    import torch
+    import qmm
+    rng = np.random.default_rng(990 + t)
+    M, K = 96, 1024
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x2 = rng.standard_normal((M, K)).astype(np.float32)
+    A, A2 = to_dev(x, dev), to_dev(x2, dev)
+    shapes = [(512, A, x), (128, A, x), (128, A, x), (768, A2, x2), (768, A2, x2)]
+    raws = [O.synth_weights(t, n, K, rng) for n, _, _ in shapes]
+    Ws = [to_dev(r, dev) for r in raws]
+    Cs = [torch.full((M, n), float("nan"), device=dev) for n, _, _ in shapes]
+    qmm.gemm_batch(descs_of([(t, a, w, c, n, K) for (n, a, _), w, c in zip(shapes, Ws, Cs)]))
+    torch.cuda.synchronize()
+    for (n, a, xx), w, c, raw in zip(shapes, Ws, Cs, raws):
+        y = c.cpu().numpy().astype(np.float64)
+        assert O.max_rel_err(y, single_any(t, a, w, n, K, torch.float32)) <= PF_TOL_F16, (O.TYPE_NAMES[t], n)
+        assert O.max_rel_err(y, O.matmul_f16_operands(t, xx, raw, n, K)) <= PF_TOL_F16, (O.TYPE_NAMES[t], n)
+        assert O.max_rel_err(y, O.matmul_f64(t, xx, raw, n, K)) <= PF_TOL_F64, (O.TYPE_NAMES[t], n)
+
+
+@pytest.mark.parametrize("t", [O.GGML_Q4_K, O.GGML_Q6_K, O.GGML_Q8_0])
+def test_batch_prefill_gate_up_fused_wide_grid(dev, t):
+    # Two 16384-row matrices at M = 256: alone each fills 64 tiles of 256 x 256, fused 128, so
+    # the fused launch takes the wide tile while single calls do not.  Sampled columns are
+    # checked against the oracle and against single calls; fp16 activations and outputs.
+    import torch
+    import qmm
+    rng = np.random.default_rng(995 + t)
+    M, N, K = 256, 16384, 1024
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    A = to_dev(x.astype(np.float16), dev)
+    xa = x.astype(np.float16).astype(np.float32)
+    raws = [O.synth_weights(t, N, K, rng) for _ in range(2)]
+    Ws = [to_dev(r, dev) for r in raws]
+    Cs = [torch.empty((M, N), device=dev, dtype=torch.float16) for _ in range(2)]
+    qmm.gemm_batch(descs_of([(t, A, w, c, N, K) for w, c in zip(Ws, Cs)]))
+    torch.cuda.synchronize()
+    cols = np.array(sorted(set(rng.choice(N, size=40, replace=False).tolist()) | {0, N - 1}))
+    rb = O.weight_bytes(t, 1, K)
+    for w, c, raw in zip(Ws, Cs, raws):
+        y = c.float().cpu().numpy().astype(np.float64)
+        assert np.all(np.isfinite(y))
+        assert O.max_rel_err(y, single_any(t, A, w, N, K, torch.float16)) <= 1e-3  # fp16 outputs
+        sub = np.concatenate([raw[r * rb:(r + 1) * rb] for r in cols])
+        ys = y[:, cols]
+        assert O.max_rel_err(ys, O.matmul_f16_operands(t, xa, sub, cols.size, K)) <= 1e-3
+        assert O.max_rel_err(ys, O.matmul_f64(t, xa, sub, cols.size, K)) <= PF_TOL_F64
+
+
+def test_batch_prefill_overlapping_outputs_keep_sequential_order(dev):
+    import torch
+    import qmm
+    t = O.GGML_Q4_K
+    rng = np.random.default_rng(998)
+    M, N, K = 64, 256, 1024
+    A = to_dev(rng.standard_normal((M, K)).astype(np.float32), dev)
+    W1, W2 = (to_dev(O.synth_weights(t, N, K, rng), dev) for _ in range(2))
+    C = torch.empty((M, N), device=dev)
+    qmm.gemm_batch(descs_of([(t, A, W1, C, N, K), (t, A, W2, C, N, K)]))
+    torch.cuda.synchronize()
+    assert torch.equal(C.cpu(), single(t, A, W2, N, K, torch.float32))
