@@ -275,6 +275,18 @@ int qmm_gemm_batch(const qmm_gemm_desc* descs, int count, void* stream) {
     return QMM_OK;
 }
 
+int qmm_upload_file(const char* path, const qmm_file_range* ranges, int count, int64_t chunk_bytes, int depth,
+                    int threads, void* stream) {
+    const qmm::UploadStatus st =
+        qmm::upload_file_ranges(path, ranges, count, chunk_bytes, depth, threads, static_cast<hipStream_t>(stream));
+    return st.code == QMM_OK ? QMM_OK : fail(st.code, st.msg);
+}
+
+int qmm_read_file(const char* path, const qmm_file_range* ranges, int count, int threads) {
+    const qmm::UploadStatus st = qmm::read_file_ranges(path, ranges, count, threads);
+    return st.code == QMM_OK ? QMM_OK : fail(st.code, st.msg);
+}
+
 int qmm_embed(int ggml_type, const void* table, int64_t n_rows, int hidden, const int64_t* ids, int64_t n_ids,
               void* out, int out_dtype, int* bad, void* stream) {
     const bool dense = ggml_type == QMM_TYPE_F16 || ggml_type == QMM_TYPE_F32;
@@ -345,6 +357,7 @@ int qmm_dequantize_q4_k_host(const void* q, void* out, int n) { return dequant_h
 int qmm_dequantize_q6_k_host(const void* q, void* out, int n) { return dequant_host(QMM_TYPE_Q6_K, q, out, n); }
 
 int qmm_release_workspace(void) {
+    qmm::release_upload_staging();
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     int cur = 0;
     hipError_t e = hipGetDevice(&cur);

@@ -8,6 +8,8 @@
 
 #include "qmm.h"
 
+#include <string>
+
 namespace qmm {
 
 // GGUF block geometry (reference src/kernels/dequantize.h:6-22).
@@ -68,5 +70,17 @@ hipError_t launch_embed(int ggml_type, const void* table, int64_t n_rows, int64_
                         const int64_t* ids, int64_t n_ids, void* out, int out_dtype, int* bad, hipStream_t stream);
 hipError_t launch_dequantize(int ggml_type, const void* W, void* out, int out_dtype,
                              int64_t num_elements, hipStream_t stream);
+
+// File -> memory loading (qmm_upload.hip).  Status code (QMM_*) and message.
+struct UploadStatus {
+    int code;
+    std::string msg;
+};
+using FileRange = qmm_file_range;
+UploadStatus read_file_ranges(const char* path, const FileRange* ranges, int count, int threads);
+UploadStatus upload_file_ranges(const char* path, const FileRange* ranges, int count, int64_t chunk_bytes, int depth,
+                                int threads, hipStream_t stream);
+// Frees the pinned staging buffers that upload_file_ranges keeps between calls.
+void release_upload_staging();
 
 }  // namespace qmm

@@ -39,6 +39,7 @@ QMM_OK = 0
 QMM_ERR_INVALID_ARGUMENT = 1
 QMM_ERR_UNSUPPORTED = 2
 QMM_ERR_HIP = 3
+QMM_ERR_IO = 4
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -64,6 +65,12 @@ _i = ctypes.c_int
 _i64 = ctypes.c_int64
 
 
+class FileRange(ctypes.Structure):
+    """Mirror of qmm_file_range (include/qmm.h)."""
+
+    _fields_ = [("offset", _i64), ("bytes", _i64), ("dst", _vp)]
+
+
 class GemmDesc(ctypes.Structure):
     """Mirror of qmm_gemm_desc (include/qmm.h)."""
 
@@ -80,6 +87,8 @@ _SIGNATURES = {
     "qmm_embed": (_i, [_i, _vp, _i64, _i, _vp, _i64, _vp, _i, _vp, _vp]),
     "qmm_gemm_batch": (_i, [ctypes.POINTER(GemmDesc), _i, _vp]),
     "qmm_release_workspace": (_i, []),
+    "qmm_upload_file": (_i, [ctypes.c_char_p, ctypes.POINTER(FileRange), _i, _i64, _i, _i, _vp]),
+    "qmm_read_file": (_i, [ctypes.c_char_p, ctypes.POINTER(FileRange), _i, _i]),
 }
 for _t in ("q4_0", "q8_0", "q4_k", "q6_k"):
     _SIGNATURES[f"qmm_matmul_{_t}_device"] = (_i, [_vp, _vp, _vp, _i, _i, _i, _vp])
@@ -112,6 +121,8 @@ def check(rc: int) -> None:
     msg = last_error()
     if rc == QMM_ERR_INVALID_ARGUMENT:
         raise ValueError(msg)
+    if rc == QMM_ERR_IO:
+        raise OSError(msg)
     raise RuntimeError(msg)
 
 

@@ -28,7 +28,8 @@ enum qmm_status {
     QMM_OK = 0,
     QMM_ERR_INVALID_ARGUMENT = 1, /* maps to the reference's std::invalid_argument / ValueError */
     QMM_ERR_UNSUPPORTED = 2,      /* valid request this build does not implement */
-    QMM_ERR_HIP = 3               /* HIP runtime error; maps to std::runtime_error / RuntimeError */
+    QMM_ERR_HIP = 3,              /* HIP runtime error; maps to std::runtime_error / RuntimeError */
+    QMM_ERR_IO = 4                /* file open / read failure (qmm_upload_file, qmm_read_file); OSError */
 };
 
 enum qmm_ggml_type {
@@ -62,7 +63,7 @@ size_t qmm_weight_bytes(int ggml_type, int64_t n, int64_t k);
 
 /* C[M,N] (c_dtype) = A[M,K] (a_dtype) @ dequant(W)[N,K]^T with fp32 accumulation.
  * M < QMM_GEMV_MAX_M runs the bandwidth-bound GEMV family, whose row m result is
- * bit-identical for every M; larger M runs the bf16-MFMA prefill GEMM.
+ * bit-identical for every M; larger M runs the f16-MFMA prefill GEMM.
  * Generalises launch_matmul_q{4_0,8_0,4_k,6_k}_device (reference
  * src/kernels/dequantize.h:98-132, dispatch at dequantize.hip:778/896/1014/1132). */
 int qmm_gemm(int ggml_type, const void* A, int a_dtype, const void* W, void* C, int c_dtype,
@@ -152,6 +153,31 @@ int qmm_dequantize_q4_0_host(const void* h_q4, void* h_fp16_out, int num_element
 int qmm_dequantize_q8_0_host(const void* h_q8, void* h_fp16_out, int num_elements);
 int qmm_dequantize_q4_k_host(const void* h_q4k, void* h_fp16_out, int num_elements);
 int qmm_dequantize_q6_k_host(const void* h_q6k, void* h_fp16_out, int num_elements);
+
+/* One byte range of a file and its destination. */
+typedef struct qmm_file_range {
+    int64_t offset; /* byte offset in the file */
+    int64_t bytes;
+    void* dst;      /* device memory (qmm_upload_file) or host memory (qmm_read_file) */
+} qmm_file_range;
+
+/* Copies byte ranges of a file (the packed tensors of a GGUF model) into device memory once, so
+ * the model stays resident in HBM.  Replaces the reference's per-call weight copies (the host
+ * wrappers, src/kernels/dequantize.hip:729-762 and siblings; project_on_device,
+ * src/kernels/attention.hip:572-586) and its mmap weight streaming (WeightStreamer,
+ * src/weight_loader.py:99-187) for MI355X, whose HBM holds a whole quantized model.
+ * `threads` reader threads pread() pieces of each chunk of at most chunk_bytes (4 MiB .. 4 GiB)
+ * into one of `depth` (2..8) pinned staging buffers, and each chunk is copied with
+ * hipMemcpyAsync on `stream`, so reading the next chunk overlaps the copy of the previous one.
+ * Returns after every copy has completed.  Ranges must lie inside the file.  The staging
+ * buffers are kept for the next call (grow-only) and freed by qmm_release_workspace(); loads
+ * from several threads run one at a time. */
+int qmm_upload_file(const char* path, const qmm_file_range* ranges, int count, int64_t chunk_bytes, int depth,
+                    int threads, void* stream);
+
+/* The same parallel reader into host memory (no staging, no GPU).  The reference's analogue is
+ * the zero-copy mmap view (WeightStreamer.get_tensor_view, src/weight_loader.py:99-110). */
+int qmm_read_file(const char* path, const qmm_file_range* ranges, int count, int threads);
 
 /* Release the host-API workspace (the reference frees its static Q4Workspace at exit,
  * dequantize.hip:715-719) and the prefill workspaces of qmm_gemm (f16 activations, split-K
