@@ -4,6 +4,7 @@
 // Error conventions follow the reference launchers (src/kernels/dequantize.hip:7-15, 734-736,
 // 771-773): a shape the block format cannot represent is QMM_ERR_INVALID_ARGUMENT (the
 // reference's std::invalid_argument), a HIP failure is QMM_ERR_HIP (std::runtime_error).
+#include <cmath>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -275,6 +276,122 @@ int qmm_gemm_batch(const qmm_gemm_desc* descs, int count, void* stream) {
     return QMM_OK;
 }
 
+// ---- transformer layer -------------------------------------------------------------------
+static int layer_status(const qmm::LayerStatus& st) { return st.code == QMM_OK ? QMM_OK : fail(st.code, st.msg); }
+
+static int norm_dtype_ok(int dt) { return dt == QMM_DTYPE_F16 || dt == QMM_DTYPE_F32; }
+
+int qmm_rmsnorm(const void* x, const void* weight, int weight_dtype, void* out, int M, int K, float eps, void* stream) {
+    if (M < 0 || K < 0) return fail(QMM_ERR_INVALID_ARGUMENT, "M and K must be non-negative.");
+    if (!norm_dtype_ok(weight_dtype)) return fail(QMM_ERR_INVALID_ARGUMENT, "weight_dtype must be QMM_DTYPE_F16 or QMM_DTYPE_F32.");
+    if (M > 0 && K > 0 && (!x || !weight || !out)) return fail(QMM_ERR_INVALID_ARGUMENT, "x, weight and out must be non-null.");
+    hipError_t e = qmm::launch_rmsnorm(x, nullptr, weight, weight_dtype == QMM_DTYPE_F32, nullptr, out, M, K, eps,
+                                       static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? QMM_OK : hip_fail(e, "rmsnorm kernel launch");
+}
+
+int qmm_rmsnorm_residual(const void* x, const void* residual, const void* weight, int weight_dtype, void* h_out,
+                         void* norm_out, int M, int K, float eps, void* stream) {
+    if (M < 0 || K < 0) return fail(QMM_ERR_INVALID_ARGUMENT, "M and K must be non-negative.");
+    if (!norm_dtype_ok(weight_dtype)) return fail(QMM_ERR_INVALID_ARGUMENT, "weight_dtype must be QMM_DTYPE_F16 or QMM_DTYPE_F32.");
+    if (M > 0 && K > 0 && (!x || !residual || !weight || !h_out || !norm_out))
+        return fail(QMM_ERR_INVALID_ARGUMENT, "x, residual, weight, h_out and norm_out must be non-null.");
+    hipError_t e = qmm::launch_rmsnorm(x, residual, weight, weight_dtype == QMM_DTYPE_F32, h_out, norm_out, M, K, eps,
+                                       static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? QMM_OK : hip_fail(e, "rmsnorm_residual kernel launch");
+}
+
+int qmm_residual_add(const void* x, const void* residual, void* out, int64_t n, void* stream) {
+    if (n < 0) return fail(QMM_ERR_INVALID_ARGUMENT, "num_elements must be non-negative.");
+    if (n > 0 && (!x || !residual || !out)) return fail(QMM_ERR_INVALID_ARGUMENT, "x, residual and out must be non-null.");
+    hipError_t e = qmm::launch_residual_add(x, residual, out, n, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? QMM_OK : hip_fail(e, "residual_add kernel launch");
+}
+
+int qmm_swiglu(const void* gate, const void* up, void* out, int64_t n, void* stream) {
+    if (n < 0) return fail(QMM_ERR_INVALID_ARGUMENT, "num_elements must be non-negative.");
+    if (n > 0 && (!gate || !up || !out)) return fail(QMM_ERR_INVALID_ARGUMENT, "gate, up and out must be non-null.");
+    hipError_t e = qmm::launch_swiglu(gate, up, out, n, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? QMM_OK : hip_fail(e, "swiglu kernel launch");
+}
+
+int qmm_rope(const void* x_in, void* x_out, int seq_len, int num_heads, int head_dim, int pos_offset, float freq_base,
+             int neox, void* stream) {
+    if (seq_len < 0 || num_heads < 0 || pos_offset < 0)
+        return fail(QMM_ERR_INVALID_ARGUMENT, "seq_len, num_heads and pos_offset must be non-negative.");
+    if (head_dim <= 0 || head_dim % 2 != 0 || head_dim > 256)
+        return fail(QMM_ERR_INVALID_ARGUMENT, "head_dim must be even and in (0, 256] for rope.");
+    if (seq_len > 0 && num_heads > 0 && (!x_in || !x_out)) return fail(QMM_ERR_INVALID_ARGUMENT, "x_in and x_out must be non-null.");
+    hipError_t e = qmm::launch_rope(x_in, x_out, num_heads, nullptr, nullptr, nullptr, nullptr, 0, seq_len, head_dim,
+                                    pos_offset, freq_base, neox != 0, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? QMM_OK : hip_fail(e, "rope kernel launch");
+}
+
+static int attention_args(int q_len, int kv_len, int num_heads, int num_kv_heads, int head_dim, int start_pos) {
+    if (head_dim <= 0 || head_dim > 256) return fail(QMM_ERR_INVALID_ARGUMENT, "head_dim must be in (0, 256] for gqa_attention.");
+    if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0)
+        return fail(QMM_ERR_INVALID_ARGUMENT, "num_heads must be divisible by num_kv_heads.");
+    if (q_len < 0 || kv_len < 0 || start_pos < 0)
+        return fail(QMM_ERR_INVALID_ARGUMENT, "q_len, kv_len and start_pos must be non-negative.");
+    return QMM_OK;
+}
+
+int qmm_gqa_attention(const void* Q, const void* K, const void* V, void* out, int q_len, int kv_len, int num_heads,
+                      int num_kv_heads, int head_dim, int start_pos, float scale, int causal, void* stream) {
+    int rc = attention_args(q_len, kv_len, num_heads, num_kv_heads, head_dim, start_pos);
+    if (rc != QMM_OK) return rc;
+    if (q_len == 0) return QMM_OK;
+    if (!Q || !out || (kv_len > 0 && (!K || !V))) return fail(QMM_ERR_INVALID_ARGUMENT, "Q, K, V and Out must be non-null.");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    void* part = nullptr;
+    const size_t pb = qmm::attention_workspace_bytes(q_len, num_heads, head_dim, kv_len);
+    hipError_t e;
+    if (pb > 0 && (e = qmm::layer_scratch(s, pb, &part)) != hipSuccess) return hip_fail(e, "attention workspace");
+    const float sc = scale != 0.0f ? scale : 1.0f / std::sqrt(static_cast<float>(head_dim));
+    e = qmm::launch_attention(Q, K, V, out, part, q_len, kv_len, num_heads, num_kv_heads, head_dim, start_pos, sc,
+                              causal != 0, s);
+    return e == hipSuccess ? QMM_OK : hip_fail(e, "gqa_attention kernel launch");
+}
+
+int qmm_kv_cache_init(int num_layers, int max_seq_len, int num_kv_heads, int head_dim) {
+    return layer_status(qmm::kv_cache_init(num_layers, max_seq_len, num_kv_heads, head_dim));
+}
+
+int qmm_kv_cache_free(void) { return layer_status(qmm::kv_cache_free()); }
+
+int qmm_gqa_attention_cached(const void* Q, const void* K_new, const void* V_new, void* out, int layer_idx, int q_len,
+                             int start_pos, int num_heads, int num_kv_heads, int head_dim, float scale, int causal,
+                             void* stream) {
+    _Float16 *kc = nullptr, *vc = nullptr;
+    int rc = layer_status(qmm::kv_cache_layer(layer_idx, start_pos, q_len, num_kv_heads, head_dim, &kc, &vc, nullptr));
+    if (rc != QMM_OK) return rc;
+    if ((rc = attention_args(q_len, start_pos + q_len, num_heads, num_kv_heads, head_dim, start_pos)) != QMM_OK) return rc;
+    if (q_len == 0) return QMM_OK;
+    if (!Q || !K_new || !V_new || !out) return fail(QMM_ERR_INVALID_ARGUMENT, "Q, K_new, V_new and Out must be non-null.");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const size_t row = static_cast<size_t>(num_kv_heads) * head_dim;
+    const size_t bytes = static_cast<size_t>(q_len) * row * 2;
+    hipError_t e;
+    if ((e = hipMemcpyAsync(kc + static_cast<size_t>(start_pos) * row, K_new, bytes, hipMemcpyDeviceToDevice, s)) != hipSuccess ||
+        (e = hipMemcpyAsync(vc + static_cast<size_t>(start_pos) * row, V_new, bytes, hipMemcpyDeviceToDevice, s)) != hipSuccess)
+        return hip_fail(e, "KV cache update");
+    return qmm_gqa_attention(Q, kc, vc, out, q_len, start_pos + q_len, num_heads, num_kv_heads, head_dim, start_pos, scale,
+                             causal, stream);
+}
+
+int qmm_forward_layer(const qmm_layer_config* cfg, const qmm_layer_weights* w, const void* x_in, void* x_out,
+                      int layer_idx, int seq_len, int pos_offset, void* stream) {
+    if (!cfg || !w) return fail(QMM_ERR_INVALID_ARGUMENT, "cfg and w must be non-null.");
+    if (!norm_dtype_ok(w->attn_norm_dtype) || !norm_dtype_ok(w->ffn_norm_dtype))
+        return fail(QMM_ERR_INVALID_ARGUMENT, "norm weights must be QMM_DTYPE_F16 or QMM_DTYPE_F32.");
+    const int types[7] = {w->wq_type, w->wk_type, w->wv_type, w->wo_type, w->wgate_type, w->wup_type, w->wdown_type};
+    for (int t : types)
+        if (!known_type(t))
+            return fail(QMM_ERR_UNSUPPORTED, "projection weights must be Q4_0, Q8_0, Q4_K or Q6_K (type " + std::to_string(t) + ").");
+    return layer_status(qmm::forward_layer(*cfg, *w, x_in, x_out, layer_idx, seq_len, pos_offset,
+                                           static_cast<hipStream_t>(stream)));
+}
+
 int qmm_upload_file(const char* path, const qmm_file_range* ranges, int count, int64_t chunk_bytes, int depth,
                     int threads, void* stream) {
     const qmm::UploadStatus st =
@@ -358,6 +475,10 @@ int qmm_dequantize_q6_k_host(const void* q, void* out, int n) { return dequant_h
 
 int qmm_release_workspace(void) {
     qmm::release_upload_staging();
+    {
+        hipError_t le = qmm::release_layer_workspaces();
+        if (le != hipSuccess) return hip_fail(le, "releasing the layer workspaces");
+    }
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     int cur = 0;
     hipError_t e = hipGetDevice(&cur);

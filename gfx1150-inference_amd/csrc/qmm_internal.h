@@ -83,4 +83,26 @@ UploadStatus upload_file_ranges(const char* path, const FileRange* ranges, int c
 // Frees the pinned staging buffers that upload_file_ranges keeps between calls.
 void release_upload_staging();
 
+// Layer kernels and pipeline (qmm_layer.hip).  fp16 activations; launchers return the launch's
+// hipError_t, the pool / pipeline calls a status and message.
+using LayerStatus = UploadStatus;
+hipError_t launch_rmsnorm(const void* x, const void* res, const void* w, int w_f32, void* h_out, void* out, int M, int K,
+                          float eps, hipStream_t stream);
+hipError_t launch_residual_add(const void* x, const void* r, void* out, int64_t n, hipStream_t stream);
+hipError_t launch_swiglu(const void* g, const void* u, void* out, int64_t n, hipStream_t stream);
+hipError_t launch_rope(const void* q, void* q_out, int n_q, const void* k, void* k_out, const void* v, void* v_out, int n_k,
+                       int seq_len, int head_dim, int pos_offset, float freq_base, bool neox, hipStream_t stream);
+size_t attention_workspace_bytes(int q_len, int heads, int head_dim, int kv_len);
+hipError_t launch_attention(const void* Q, const void* K, const void* V, void* out, void* part, int q_len, int kv_len,
+                            int heads, int kv_heads, int head_dim, int start_pos, float scale, bool causal,
+                            hipStream_t stream);
+LayerStatus kv_cache_init(int layers, int max_seq, int kv_heads, int head_dim);
+LayerStatus kv_cache_free();
+LayerStatus kv_cache_layer(int layer, int start, int q_len, int kv_heads, int head_dim, _Float16** k, _Float16** v,
+                           int* max_seq);
+LayerStatus forward_layer(const qmm_layer_config& cfg, const qmm_layer_weights& w, const void* x_in, void* x_out,
+                          int layer_idx, int seq_len, int pos_offset, hipStream_t stream);
+hipError_t layer_scratch(hipStream_t stream, size_t bytes, void** out);
+hipError_t release_layer_workspaces();
+
 }  // namespace qmm

@@ -1,0 +1,629 @@
+// The transformer layer around the quantized projections, device-resident: RMSNorm (plain and
+// fused with the residual add), RoPE with the KV-cache write, grouped-query attention over the
+// cache, SwiGLU, the residual add, the KV-cache pool and the layer pipeline that chains them
+// with the fused projection launches.
+//
+// Reference: src/kernels/rmsnorm.hip, rope.hip, attention.hip (gqa_online_softmax_kernel :35-123,
+// DeviceKVCachePool :164-222, launch_forward_layer_cached_fp16 :603-695), mlp.hip.  Storage is
+// fp16 and arithmetic fp32 with one rounding per stored value, as there.
+//
+// MI355X design:
+//   * RMSNorm: one workgroup (4 waves) per row, 16-byte loads, wave64 DPP reductions.
+//   * RoPE: one launch rotates q into its buffer, rotates k straight into the layer's K cache
+//     at the token positions and copies v into the V cache (the reference copies K/V into the
+//     pool separately); inverse frequencies come from the host in fp32, as in the reference.
+//   * Attention: split over the KV length.  A wave owns (query row, query head, chunk of 256
+//     keys): lanes hold head_dim / 64 query dimensions, and for each key the wave forms the dot
+//     product (wave reduction), updates an fp32 online softmax and the running output.  Chunks
+//     are merged in a fixed order by a second pass (deterministic), skipped for one chunk.  The
+//     query heads of one KV head sit in one workgroup, so their K/V reads share the caches.
+//   * SwiGLU and the residual add: 8 values per thread.
+//   * Layer: q/k/v and gate/up each run as one fused projection launch (qmm_gemm_batch), all
+//     kernels on the caller's stream with no host synchronisation; activations live in a
+//     grow-only per-(device, stream) workspace.
+#include <cmath>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "qmm_device.h"
+
+namespace qmm {
+namespace {
+
+constexpr int kNormThreads = 256;
+constexpr int kAttnChunk = 256;      // keys per attention chunk
+constexpr int kMaxHeadDim = 256;
+constexpr int kMaxRopePairs = kMaxHeadDim / 2;
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float norm_weight(const void* w, int w_f32, int k) {
+    // an F32 norm weight is rounded to f16 first, as the reference's host does
+    if (w_f32) return static_cast<float>(static_cast<_Float16>(static_cast<const float*>(w)[k]));
+    return static_cast<float>(static_cast<const _Float16*>(w)[k]);
+}
+
+// out[m] = half(v * rsqrt(mean(v^2) + eps) * w) with v = x[m] (res == nullptr) or
+// v = half(x[m] + res[m]) (stored to h_out in the first pass and read back in the second, so
+// h_out may alias x or res; out may alias x).  Each thread reads and writes only its own
+// elements across the two passes.
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const _Float16* x, const _Float16* res,
+                                                              const void* __restrict__ w, int w_f32, _Float16* h_out,
+                                                              _Float16* out, int K, float eps) {
+    const int m = blockIdx.x;
+    const size_t base = static_cast<size_t>(m) * K;
+    const int tid = threadIdx.x;
+    const bool vec = (K % 8) == 0;
+    auto value = [&](int k) -> float {
+        if (res == nullptr) return static_cast<float>(x[base + k]);
+        return static_cast<float>(static_cast<_Float16>(static_cast<float>(x[base + k]) + static_cast<float>(res[base + k])));
+    };
+    float ss = 0.0f;
+    if (vec) {
+        for (int c = tid; c < K / 8; c += kNormThreads) {
+            const h8 a = *reinterpret_cast<const h8*>(x + base + 8 * c);
+            h8 v = a;
+            if (res != nullptr) {
+                const h8 r = *reinterpret_cast<const h8*>(res + base + 8 * c);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = static_cast<_Float16>(static_cast<float>(a[e]) + static_cast<float>(r[e]));
+                *reinterpret_cast<h8*>(h_out + base + 8 * c) = v;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float f = static_cast<float>(v[e]);
+                ss += f * f;
+            }
+        }
+    } else {
+        for (int k = tid; k < K; k += kNormThreads) {
+            const float f = value(k);
+            if (res != nullptr) h_out[base + k] = static_cast<_Float16>(f);
+            ss += f * f;
+        }
+    }
+    __shared__ float part[kNormThreads / 64];
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) part[tid >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kNormThreads / 64; ++i) tot += part[i];
+    const float scale = rsqrtf(tot / static_cast<float>(K) + eps);
+    const _Float16* src = res == nullptr ? x : h_out;
+    if (vec) {
+        for (int c = tid; c < K / 8; c += kNormThreads) {
+            const h8 v = *reinterpret_cast<const h8*>(src + base + 8 * c);
+            h8 o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = static_cast<_Float16>(static_cast<float>(v[e]) * scale * norm_weight(w, w_f32, 8 * c + e));
+            *reinterpret_cast<h8*>(out + base + 8 * c) = o;
+        }
+    } else {
+        for (int k = tid; k < K; k += kNormThreads)
+            out[base + k] = static_cast<_Float16>(static_cast<float>(src[base + k]) * scale * norm_weight(w, w_f32, k));
+    }
+}
+
+// out = half(x + r), 8 values per thread (n % 8 == 0) or one.
+__global__ __launch_bounds__(256) void residual_add_kernel(const _Float16* __restrict__ x, const _Float16* __restrict__ r,
+                                                          _Float16* __restrict__ out, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if ((n & 7) == 0) {
+        if (8 * i >= n) return;
+        const h8 a = *reinterpret_cast<const h8*>(x + 8 * i);
+        const h8 b = *reinterpret_cast<const h8*>(r + 8 * i);
+        h8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = static_cast<_Float16>(static_cast<float>(a[e]) + static_cast<float>(b[e]));
+        *reinterpret_cast<h8*>(out + 8 * i) = o;
+    } else if (i < n) {
+        out[i] = static_cast<_Float16>(static_cast<float>(x[i]) + static_cast<float>(r[i]));
+    }
+}
+
+// out = half(silu(g) * u), silu(g) = g / (1 + exp(-g)).
+__global__ __launch_bounds__(256) void swiglu_kernel(const _Float16* __restrict__ g, const _Float16* __restrict__ u,
+                                                    _Float16* __restrict__ out, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    auto f = [](float gv, float uv) { return static_cast<_Float16>(gv / (1.0f + expf(-gv)) * uv); };
+    if ((n & 7) == 0) {
+        if (8 * i >= n) return;
+        const h8 a = *reinterpret_cast<const h8*>(g + 8 * i);
+        const h8 b = *reinterpret_cast<const h8*>(u + 8 * i);
+        h8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = f(static_cast<float>(a[e]), static_cast<float>(b[e]));
+        *reinterpret_cast<h8*>(out + 8 * i) = o;
+    } else if (i < n) {
+        out[i] = f(static_cast<float>(g[i]), static_cast<float>(u[i]));
+    }
+}
+
+struct RopeFreq {
+    float inv[kMaxRopePairs];
+};
+
+// Rotates pairs of q (n_q heads) into q_out and of k (n_k heads) into k_out, and copies v
+// (n_k heads) into v_out; rows are token positions pos_offset + s.  q_out / k_out / v_out row
+// strides are given in elements (the KV cache rows hold n_k heads).  One thread per pair.
+__global__ __launch_bounds__(256) void rope_kernel(const _Float16* __restrict__ q, _Float16* __restrict__ q_out, int n_q,
+                                                  const _Float16* __restrict__ k, _Float16* __restrict__ k_out,
+                                                  const _Float16* __restrict__ v, _Float16* __restrict__ v_out, int n_k,
+                                                  int seq_len, int head_dim, int pos_offset, int neox, RopeFreq fr) {
+    const int half_dim = head_dim / 2;
+    const int heads = n_q + n_k;
+    const int64_t total = static_cast<int64_t>(seq_len) * heads * half_dim;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= total) return;
+    const int p = static_cast<int>(idx % half_dim);
+    const int64_t t = idx / half_dim;
+    const int hh = static_cast<int>(t % heads);
+    const int s = static_cast<int>(t / heads);
+    const float ang = static_cast<float>(pos_offset + s) * fr.inv[p];
+    const float c = cosf(ang), sn = sinf(ang);
+    const int i0 = neox ? p : 2 * p;
+    const int i1 = neox ? p + half_dim : 2 * p + 1;
+    const _Float16* src;
+    _Float16* dst;
+    if (hh < n_q) {
+        src = q + (static_cast<size_t>(s) * n_q + hh) * head_dim;
+        dst = q_out + (static_cast<size_t>(s) * n_q + hh) * head_dim;
+    } else {
+        const int kh = hh - n_q;
+        src = k + (static_cast<size_t>(s) * n_k + kh) * head_dim;
+        dst = k_out + (static_cast<size_t>(s) * n_k + kh) * head_dim;
+        if (v != nullptr) {
+            const _Float16* vs = v + (static_cast<size_t>(s) * n_k + kh) * head_dim;
+            _Float16* vd = v_out + (static_cast<size_t>(s) * n_k + kh) * head_dim;
+            vd[i0] = vs[i0];
+            vd[i1] = vs[i1];
+        }
+    }
+    const float a = static_cast<float>(src[i0]), b = static_cast<float>(src[i1]);
+    dst[i0] = static_cast<_Float16>(a * c - b * sn);
+    dst[i1] = static_cast<_Float16>(a * sn + b * c);
+}
+
+// Attention, one wave per (query row m, query head h, key chunk c); D = head_dim / 64 dims per
+// lane (lane l holds dims l + 64 i).  Partial results: running max, sum and unnormalised output
+// (fp32), or the final fp16 output when there is a single chunk.
+template <int D>
+__global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restrict__ Q, const _Float16* __restrict__ Kc,
+                                                       const _Float16* __restrict__ Vc, _Float16* __restrict__ out,
+                                                       float* __restrict__ part, int q_len, int kv_len, int heads,
+                                                       int kv_heads, int head_dim, int start_pos, float scale, int causal,
+                                                       int chunks) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int64_t total = static_cast<int64_t>(q_len) * heads * chunks;
+    if (wave >= total) return;
+    // waves of one workgroup: consecutive heads of the same (m, c), so the query heads that share
+    // a KV head (consecutive h) read the same keys
+    const int h = static_cast<int>(wave % heads);
+    const int64_t t = wave / heads;
+    const int c = static_cast<int>(t % chunks);
+    const int m = static_cast<int>(t / chunks);
+    const int group = heads / kv_heads;
+    const int kvh = h / group;
+    const int n_keys = causal ? min(kv_len, start_pos + m + 1) : kv_len;
+    const int s0 = c * kAttnChunk;
+    const int s1 = min(n_keys, s0 + kAttnChunk);
+
+    const _Float16* qp = Q + (static_cast<size_t>(m) * heads + h) * head_dim;
+    float qv[D], acc[D];
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+        const int d = lane + 64 * i;
+        qv[i] = d < head_dim ? static_cast<float>(qp[d]) : 0.0f;
+        acc[i] = 0.0f;
+    }
+    float mx = -INFINITY, sum = 0.0f;
+    const size_t row = static_cast<size_t>(kv_heads) * head_dim;
+    for (int s = s0; s < s1; ++s) {
+        const _Float16* kp = Kc + static_cast<size_t>(s) * row + static_cast<size_t>(kvh) * head_dim;
+        const _Float16* vp = Vc + static_cast<size_t>(s) * row + static_cast<size_t>(kvh) * head_dim;
+        float dot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            const int d = lane + 64 * i;
+            if (d < head_dim) dot += qv[i] * static_cast<float>(kp[d]);
+        }
+        const float sc = wave_sum(dot) * scale;
+        const float mn = fmaxf(mx, sc);
+        const float a = expf(mx - mn);  // exp(-inf) = 0 for the first key
+        const float e = expf(sc - mn);
+        sum = sum * a + e;
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            const int d = lane + 64 * i;
+            if (d < head_dim) acc[i] = acc[i] * a + e * static_cast<float>(vp[d]);
+        }
+        mx = mn;
+    }
+    if (chunks == 1) {
+        const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+        _Float16* op = out + (static_cast<size_t>(m) * heads + h) * head_dim;
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            const int d = lane + 64 * i;
+            if (d < head_dim) op[d] = static_cast<_Float16>(acc[i] * inv);
+        }
+        return;
+    }
+    float* pp = part + static_cast<size_t>(wave) * (head_dim + 2);
+    if (lane == 0) {
+        pp[0] = mx;
+        pp[1] = sum;
+    }
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+        const int d = lane + 64 * i;
+        if (d < head_dim) pp[2 + d] = acc[i];
+    }
+}
+
+// Merges the chunks of each (m, h) in chunk order.  One thread per output element.
+__global__ __launch_bounds__(256) void attention_combine_kernel(const float* __restrict__ part, _Float16* __restrict__ out,
+                                                              int q_len, int heads, int head_dim, int chunks) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t total = static_cast<int64_t>(q_len) * heads * head_dim;
+    if (idx >= total) return;
+    const int d = static_cast<int>(idx % head_dim);
+    const int64_t mh = idx / head_dim;
+    const int h = static_cast<int>(mh % heads);
+    const int m = static_cast<int>(mh / heads);
+    const size_t stride = static_cast<size_t>(head_dim) + 2;
+    auto at = [&](int c) { return part + ((static_cast<size_t>(m) * chunks + c) * heads + h) * stride; };
+    float mx = -INFINITY;
+    for (int c = 0; c < chunks; ++c) mx = fmaxf(mx, at(c)[0]);
+    float sum = 0.0f, acc = 0.0f;
+    for (int c = 0; c < chunks; ++c) {
+        const float* p = at(c);
+        if (p[1] > 0.0f) {
+            const float a = expf(p[0] - mx);
+            sum += p[1] * a;
+            acc += p[2 + d] * a;
+        }
+    }
+    out[idx] = static_cast<_Float16>(sum > 0.0f ? acc / sum : 0.0f);
+}
+
+// ---- KV cache pool (one per device) ----------------------------------------------------------
+struct KvPool {
+    _Float16* k = nullptr;
+    _Float16* v = nullptr;
+    int layers = 0, max_seq = 0, kv_heads = 0, head_dim = 0;
+    size_t cap = 0;
+};
+std::mutex g_kv_mutex;
+std::unordered_map<int, KvPool> g_kv;
+
+// ---- per-(device, stream) activation workspace of the layer pipeline --------------------------
+struct LayerWs {
+    void* buf = nullptr;
+    size_t cap = 0;
+};
+std::mutex g_lws_mutex;
+std::unordered_map<std::string, LayerWs> g_lws;
+
+hipError_t layer_workspace(hipStream_t stream, size_t bytes, char** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const std::string key = std::to_string(dev) + ":" + std::to_string(reinterpret_cast<uintptr_t>(stream));
+    std::lock_guard<std::mutex> lock(g_lws_mutex);
+    LayerWs& ws = g_lws[key];
+    if (ws.cap < bytes) {
+        if (ws.buf) {
+            if ((e = hipStreamSynchronize(stream)) != hipSuccess) return e;
+            if ((e = hipFree(ws.buf)) != hipSuccess) return e;
+            ws.buf = nullptr;
+            ws.cap = 0;
+        }
+        if ((e = hipMalloc(&ws.buf, bytes)) != hipSuccess) return e;
+        ws.cap = bytes;
+    }
+    *out = static_cast<char*>(ws.buf);
+    return hipSuccess;
+}
+
+int attn_chunks(int kv_len) { return kv_len <= 0 ? 1 : (kv_len + kAttnChunk - 1) / kAttnChunk; }
+
+size_t attn_part_bytes(int q_len, int heads, int head_dim, int kv_len) {
+    const int ch = attn_chunks(kv_len);
+    return ch > 1 ? static_cast<size_t>(q_len) * heads * ch * (head_dim + 2) * sizeof(float) : 0;
+}
+
+}  // namespace
+
+// ---- launchers (validated arguments) --------------------------------------------------------
+hipError_t launch_rmsnorm(const void* x, const void* res, const void* w, int w_f32, void* h_out, void* out, int M, int K,
+                          float eps, hipStream_t stream) {
+    if (M <= 0 || K <= 0) return hipSuccess;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(M), dim3(kNormThreads), 0, stream, static_cast<const _Float16*>(x),
+                       static_cast<const _Float16*>(res), w, w_f32, static_cast<_Float16*>(h_out),
+                       static_cast<_Float16*>(out), K, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_residual_add(const void* x, const void* r, void* out, int64_t n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const int64_t items = (n & 7) == 0 ? n / 8 : n;
+    hipLaunchKernelGGL(residual_add_kernel, dim3(static_cast<unsigned>((items + 255) / 256)), dim3(256), 0, stream,
+                       static_cast<const _Float16*>(x), static_cast<const _Float16*>(r), static_cast<_Float16*>(out), n);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const void* g, const void* u, void* out, int64_t n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const int64_t items = (n & 7) == 0 ? n / 8 : n;
+    hipLaunchKernelGGL(swiglu_kernel, dim3(static_cast<unsigned>((items + 255) / 256)), dim3(256), 0, stream,
+                       static_cast<const _Float16*>(g), static_cast<const _Float16*>(u), static_cast<_Float16*>(out), n);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(const void* q, void* q_out, int n_q, const void* k, void* k_out, const void* v, void* v_out, int n_k,
+                       int seq_len, int head_dim, int pos_offset, float freq_base, bool neox, hipStream_t stream) {
+    if (seq_len <= 0 || n_q + n_k <= 0) return hipSuccess;
+    RopeFreq fr;
+    for (int i = 0; i < head_dim / 2; ++i)
+        fr.inv[i] = 1.0f / std::pow(freq_base, static_cast<float>(2 * i) / static_cast<float>(head_dim));
+    const int64_t total = static_cast<int64_t>(seq_len) * (n_q + n_k) * (head_dim / 2);
+    hipLaunchKernelGGL(rope_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, stream,
+                       static_cast<const _Float16*>(q), static_cast<_Float16*>(q_out), n_q, static_cast<const _Float16*>(k),
+                       static_cast<_Float16*>(k_out), static_cast<const _Float16*>(v), static_cast<_Float16*>(v_out), n_k,
+                       seq_len, head_dim, pos_offset, neox ? 1 : 0, fr);
+    return hipGetLastError();
+}
+
+size_t attention_workspace_bytes(int q_len, int heads, int head_dim, int kv_len) {
+    return attn_part_bytes(q_len, heads, head_dim, kv_len);
+}
+
+hipError_t launch_attention(const void* Q, const void* K, const void* V, void* out, void* part, int q_len, int kv_len,
+                            int heads, int kv_heads, int head_dim, int start_pos, float scale, bool causal,
+                            hipStream_t stream) {
+    if (q_len <= 0 || heads <= 0) return hipSuccess;
+    const int chunks = attn_chunks(kv_len);
+    const int64_t waves = static_cast<int64_t>(q_len) * heads * chunks;
+    const dim3 grid(static_cast<unsigned>((waves + 3) / 4));
+    auto go = [&](auto dc) {
+        constexpr int D = decltype(dc)::value;
+        hipLaunchKernelGGL((attention_kernel<D>), grid, dim3(256), 0, stream, static_cast<const _Float16*>(Q),
+                           static_cast<const _Float16*>(K), static_cast<const _Float16*>(V), static_cast<_Float16*>(out),
+                           static_cast<float*>(part), q_len, kv_len, heads, kv_heads, head_dim, start_pos, scale,
+                           causal ? 1 : 0, chunks);
+    };
+    if (head_dim <= 64) go(std::integral_constant<int, 1>{});
+    else if (head_dim <= 128) go(std::integral_constant<int, 2>{});
+    else go(std::integral_constant<int, 4>{});
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || chunks == 1) return e;
+    const int64_t n = static_cast<int64_t>(q_len) * heads * head_dim;
+    hipLaunchKernelGGL(attention_combine_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream,
+                       static_cast<const float*>(part), static_cast<_Float16*>(out), q_len, heads, head_dim, chunks);
+    return hipGetLastError();
+}
+
+// ---- KV cache pool ----------------------------------------------------------------------------
+LayerStatus kv_cache_init(int layers, int max_seq, int kv_heads, int head_dim) {
+    if (layers <= 0 || max_seq <= 0 || kv_heads <= 0 || head_dim <= 0)
+        return {QMM_ERR_INVALID_ARGUMENT, "KV cache dimensions must all be positive."};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return {QMM_ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(e)};
+    std::lock_guard<std::mutex> lock(g_kv_mutex);
+    KvPool& p = g_kv[dev];
+    const size_t need = static_cast<size_t>(layers) * max_seq * kv_heads * head_dim * sizeof(_Float16);
+    if (need > p.cap) {
+        if (p.k) (void)hipFree(p.k);
+        if (p.v) (void)hipFree(p.v);
+        p = KvPool{};
+        if ((e = hipMalloc(reinterpret_cast<void**>(&p.k), need)) != hipSuccess) {
+            p.k = nullptr;
+            return {QMM_ERR_HIP, std::string("hipMalloc (KV cache): ") + hipGetErrorString(e)};
+        }
+        if ((e = hipMalloc(reinterpret_cast<void**>(&p.v), need)) != hipSuccess) {
+            (void)hipFree(p.k);
+            p = KvPool{};
+            return {QMM_ERR_HIP, std::string("hipMalloc (KV cache): ") + hipGetErrorString(e)};
+        }
+        p.cap = need;
+    }
+    p.layers = layers;
+    p.max_seq = max_seq;
+    p.kv_heads = kv_heads;
+    p.head_dim = head_dim;
+    return {QMM_OK, ""};
+}
+
+LayerStatus kv_cache_free() {
+    std::lock_guard<std::mutex> lock(g_kv_mutex);
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return {QMM_ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(e)};
+    for (auto& kv : g_kv) {
+        if (!kv.second.k) continue;
+        if ((e = hipSetDevice(kv.first)) != hipSuccess) return {QMM_ERR_HIP, hipGetErrorString(e)};
+        (void)hipDeviceSynchronize();  // queued kernels may still use the pool
+        (void)hipFree(kv.second.k);
+        (void)hipFree(kv.second.v);
+    }
+    g_kv.clear();
+    (void)hipSetDevice(cur);
+    return {QMM_OK, ""};
+}
+
+// Device K / V of layer `layer` for a call writing [start, start + q_len), checked against the
+// pool's geometry (the reference's DeviceKVCachePool checks, attention.hip:316-331).
+LayerStatus kv_cache_layer(int layer, int start, int q_len, int kv_heads, int head_dim, _Float16** k, _Float16** v,
+                           int* max_seq) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return {QMM_ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(e)};
+    std::lock_guard<std::mutex> lock(g_kv_mutex);
+    auto it = g_kv.find(dev);
+    if (it == g_kv.end() || !it->second.k)
+        return {QMM_ERR_UNSUPPORTED, "Device KV cache not initialized. Call kv_cache_init first."};
+    const KvPool& p = it->second;
+    if (layer < 0 || layer >= p.layers) return {QMM_ERR_OUT_OF_RANGE, "layer_idx out of range for DeviceKVCachePool."};
+    if (start < 0 || static_cast<int64_t>(start) + q_len > p.max_seq)
+        return {QMM_ERR_OUT_OF_RANGE, "start_pos + q_len exceeds max_seq_len in DeviceKVCachePool."};
+    if (kv_heads != p.kv_heads || head_dim != p.head_dim)
+        return {QMM_ERR_INVALID_ARGUMENT, "num_kv_heads or head_dim mismatch with DeviceKVCachePool."};
+    const size_t layer_elems = static_cast<size_t>(p.max_seq) * p.kv_heads * p.head_dim;
+    *k = p.k + static_cast<size_t>(layer) * layer_elems;
+    *v = p.v + static_cast<size_t>(layer) * layer_elems;
+    if (max_seq) *max_seq = p.max_seq;
+    return {QMM_OK, ""};
+}
+
+// ---- the layer pipeline --------------------------------------------------------------------
+LayerStatus forward_layer(const qmm_layer_config& cfg, const qmm_layer_weights& w, const void* x_in, void* x_out,
+                          int layer_idx, int seq_len, int pos_offset, hipStream_t stream) {
+    const int H = cfg.num_heads, KVH = cfg.num_kv_heads, D = cfg.head_dim;
+    const int hid = cfg.hidden_size, inter = cfg.intermediate_size;
+    if (seq_len <= 0 || hid <= 0 || inter <= 0 || H <= 0 || KVH <= 0 || D <= 0)
+        return {QMM_ERR_INVALID_ARGUMENT, "seq_len and the layer dimensions must be positive."};
+    if (H % KVH != 0) return {QMM_ERR_INVALID_ARGUMENT, "num_heads must be divisible by num_kv_heads."};
+    if (D > kMaxHeadDim || D % 2 != 0) return {QMM_ERR_INVALID_ARGUMENT, "head_dim must be even and in (0, 256]."};
+    if (x_in == nullptr || x_out == nullptr) return {QMM_ERR_INVALID_ARGUMENT, "x_in and x_out must be non-null."};
+    const int qd = H * D, kvd = KVH * D;
+    _Float16 *kc = nullptr, *vc = nullptr;
+    LayerStatus st = kv_cache_layer(layer_idx, pos_offset, seq_len, KVH, D, &kc, &vc, nullptr);
+    if (st.code != QMM_OK) return st;
+    const int kv_len = pos_offset + seq_len;
+
+    // activation workspace
+    const size_t S = static_cast<size_t>(seq_len);
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off += (bytes + 255) & ~size_t{255};
+        return at;
+    };
+    const size_t o_norm = take(S * hid * 2), o_q = take(S * qd * 2), o_k = take(S * kvd * 2), o_v = take(S * kvd * 2);
+    const size_t o_qr = take(S * qd * 2), o_att = take(S * qd * 2), o_proj = take(S * hid * 2), o_h = take(S * hid * 2);
+    const size_t o_g = take(S * inter * 2), o_u = take(S * inter * 2), o_act = take(S * inter * 2);
+    const size_t o_down = take(S * hid * 2), o_part = take(attn_part_bytes(seq_len, H, D, kv_len));
+    char* ws = nullptr;
+    hipError_t e = layer_workspace(stream, off, &ws);
+    if (e != hipSuccess) return {QMM_ERR_HIP, std::string("layer workspace: ") + hipGetErrorString(e)};
+    auto fail = [](hipError_t err, const char* what) {
+        return LayerStatus{QMM_ERR_HIP, std::string(what) + ": " + hipGetErrorString(err)};
+    };
+    auto gemms = [&](const qmm_gemm_desc* d, int n) -> LayerStatus {
+        const int rc = qmm_gemm_batch(d, n, stream);
+        if (rc != QMM_OK) return {rc, qmm_last_error()};
+        return {QMM_OK, ""};
+    };
+    auto desc = [&](int t, const void* A, const void* W, void* C, int M, int N, int K) {
+        qmm_gemm_desc d{};
+        d.ggml_type = t;
+        d.A = A;
+        d.a_dtype = QMM_DTYPE_F16;
+        d.W = W;
+        d.C = C;
+        d.c_dtype = QMM_DTYPE_F16;
+        d.M = M;
+        d.N = N;
+        d.K = K;
+        return d;
+    };
+    const int nw_f32 = w.attn_norm_dtype == QMM_DTYPE_F32 ? 1 : 0, fw_f32 = w.ffn_norm_dtype == QMM_DTYPE_F32 ? 1 : 0;
+
+    // 1. pre-attention RMSNorm
+    if ((e = launch_rmsnorm(x_in, nullptr, w.attn_norm, nw_f32, nullptr, ws + o_norm, seq_len, hid, cfg.rms_norm_eps,
+                            stream)) != hipSuccess)
+        return fail(e, "rmsnorm");
+    // 2. q, k, v (one fused launch)
+    const qmm_gemm_desc qkv[3] = {desc(w.wq_type, ws + o_norm, w.wq, ws + o_q, seq_len, qd, hid),
+                                  desc(w.wk_type, ws + o_norm, w.wk, ws + o_k, seq_len, kvd, hid),
+                                  desc(w.wv_type, ws + o_norm, w.wv, ws + o_v, seq_len, kvd, hid)};
+    if ((st = gemms(qkv, 3)).code != QMM_OK) return st;
+    // 3. RoPE on q and k; k and v land in the cache at their positions
+    const size_t cache_off = static_cast<size_t>(pos_offset) * kvd;
+    if ((e = launch_rope(ws + o_q, ws + o_qr, H, ws + o_k, kc + cache_off, ws + o_v, vc + cache_off, KVH, seq_len, D,
+                         pos_offset, cfg.rope_freq_base, cfg.rope_neox != 0, stream)) != hipSuccess)
+        return fail(e, "rope");
+    // 4. attention over the cache
+    const float scale = cfg.scale != 0.0f ? cfg.scale : 1.0f / std::sqrt(static_cast<float>(D));
+    if ((e = launch_attention(ws + o_qr, kc, vc, ws + o_att, ws + o_part, seq_len, kv_len, H, KVH, D, pos_offset, scale,
+                              true, stream)) != hipSuccess)
+        return fail(e, "attention");
+    // 5. output projection
+    const qmm_gemm_desc o = desc(w.wo_type, ws + o_att, w.wo, ws + o_proj, seq_len, hid, qd);
+    if ((st = gemms(&o, 1)).code != QMM_OK) return st;
+    // 6. residual + pre-FFN RMSNorm
+    if ((e = launch_rmsnorm(x_in, ws + o_proj, w.ffn_norm, fw_f32, ws + o_h, ws + o_norm, seq_len, hid, cfg.rms_norm_eps,
+                            stream)) != hipSuccess)
+        return fail(e, "rmsnorm_residual");
+    // 7. gate, up (one fused launch), SwiGLU, down
+    const qmm_gemm_desc gu[2] = {desc(w.wgate_type, ws + o_norm, w.wgate, ws + o_g, seq_len, inter, hid),
+                                 desc(w.wup_type, ws + o_norm, w.wup, ws + o_u, seq_len, inter, hid)};
+    if ((st = gemms(gu, 2)).code != QMM_OK) return st;
+    if ((e = launch_swiglu(ws + o_g, ws + o_u, ws + o_act, static_cast<int64_t>(S) * inter, stream)) != hipSuccess)
+        return fail(e, "swiglu");
+    const qmm_gemm_desc dn = desc(w.wdown_type, ws + o_act, w.wdown, ws + o_down, seq_len, hid, inter);
+    if ((st = gemms(&dn, 1)).code != QMM_OK) return st;
+    // 8. second residual
+    if ((e = launch_residual_add(ws + o_h, ws + o_down, x_out, static_cast<int64_t>(S) * hid, stream)) != hipSuccess)
+        return fail(e, "residual_add");
+    return {QMM_OK, ""};
+}
+
+// A second per-(device, stream) buffer for the standalone attention entry points (their
+// partial results), so they never resize the pipeline's activation workspace.
+namespace {
+std::unordered_map<std::string, LayerWs> g_scratch;
+}
+
+hipError_t layer_scratch(hipStream_t stream, size_t bytes, void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const std::string key = std::to_string(dev) + ":" + std::to_string(reinterpret_cast<uintptr_t>(stream));
+    std::lock_guard<std::mutex> lock(g_lws_mutex);
+    LayerWs& ws = g_scratch[key];
+    if (ws.cap < bytes) {
+        if (ws.buf) {
+            if ((e = hipStreamSynchronize(stream)) != hipSuccess) return e;
+            if ((e = hipFree(ws.buf)) != hipSuccess) return e;
+            ws.buf = nullptr;
+            ws.cap = 0;
+        }
+        if ((e = hipMalloc(&ws.buf, bytes)) != hipSuccess) return e;
+        ws.cap = bytes;
+    }
+    *out = ws.buf;
+    return hipSuccess;
+}
+
+hipError_t release_layer_workspaces() {
+    std::lock_guard<std::mutex> lock(g_lws_mutex);
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return e;
+    for (auto* m : {&g_lws, &g_scratch}) {
+        for (auto& kv : *m) {
+            if (!kv.second.buf) continue;
+            const int dev = std::stoi(kv.first.substr(0, kv.first.find(':')));
+            if ((e = hipSetDevice(dev)) != hipSuccess) return e;
+            if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+            if ((e = hipFree(kv.second.buf)) != hipSuccess) return e;
+        }
+        m->clear();
+    }
+    return hipSetDevice(cur);
+}
+
+}  // namespace qmm

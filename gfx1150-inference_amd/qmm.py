@@ -40,6 +40,7 @@ QMM_ERR_INVALID_ARGUMENT = 1
 QMM_ERR_UNSUPPORTED = 2
 QMM_ERR_HIP = 3
 QMM_ERR_IO = 4
+QMM_ERR_OUT_OF_RANGE = 5
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -71,6 +72,22 @@ class FileRange(ctypes.Structure):
     _fields_ = [("offset", _i64), ("bytes", _i64), ("dst", _vp)]
 
 
+class LayerConfig(ctypes.Structure):
+    """Mirror of qmm_layer_config (include/qmm.h)."""
+
+    _fields_ = [("hidden_size", _i), ("intermediate_size", _i), ("num_heads", _i), ("num_kv_heads", _i),
+                ("head_dim", _i), ("rms_norm_eps", ctypes.c_float), ("rope_freq_base", ctypes.c_float),
+                ("rope_neox", _i), ("scale", ctypes.c_float)]
+
+
+class LayerWeights(ctypes.Structure):
+    """Mirror of qmm_layer_weights (include/qmm.h)."""
+
+    _fields_ = [("attn_norm", _vp), ("attn_norm_dtype", _i), ("wq", _vp), ("wq_type", _i), ("wk", _vp), ("wk_type", _i),
+                ("wv", _vp), ("wv_type", _i), ("wo", _vp), ("wo_type", _i), ("ffn_norm", _vp), ("ffn_norm_dtype", _i),
+                ("wgate", _vp), ("wgate_type", _i), ("wup", _vp), ("wup_type", _i), ("wdown", _vp), ("wdown_type", _i)]
+
+
 class GemmDesc(ctypes.Structure):
     """Mirror of qmm_gemm_desc (include/qmm.h)."""
 
@@ -89,6 +106,16 @@ _SIGNATURES = {
     "qmm_release_workspace": (_i, []),
     "qmm_upload_file": (_i, [ctypes.c_char_p, ctypes.POINTER(FileRange), _i, _i64, _i, _i, _vp]),
     "qmm_read_file": (_i, [ctypes.c_char_p, ctypes.POINTER(FileRange), _i, _i]),
+    "qmm_rmsnorm": (_i, [_vp, _vp, _i, _vp, _i, _i, ctypes.c_float, _vp]),
+    "qmm_rmsnorm_residual": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _i, ctypes.c_float, _vp]),
+    "qmm_residual_add": (_i, [_vp, _vp, _vp, _i64, _vp]),
+    "qmm_swiglu": (_i, [_vp, _vp, _vp, _i64, _vp]),
+    "qmm_rope": (_i, [_vp, _vp, _i, _i, _i, _i, ctypes.c_float, _i, _vp]),
+    "qmm_gqa_attention": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, ctypes.c_float, _i, _vp]),
+    "qmm_kv_cache_init": (_i, [_i, _i, _i, _i]),
+    "qmm_kv_cache_free": (_i, []),
+    "qmm_gqa_attention_cached": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, ctypes.c_float, _i, _vp]),
+    "qmm_forward_layer": (_i, [ctypes.POINTER(LayerConfig), ctypes.POINTER(LayerWeights), _vp, _vp, _i, _i, _i, _vp]),
 }
 for _t in ("q4_0", "q8_0", "q4_k", "q6_k"):
     _SIGNATURES[f"qmm_matmul_{_t}_device"] = (_i, [_vp, _vp, _vp, _i, _i, _i, _vp])
@@ -123,6 +150,8 @@ def check(rc: int) -> None:
         raise ValueError(msg)
     if rc == QMM_ERR_IO:
         raise OSError(msg)
+    if rc == QMM_ERR_OUT_OF_RANGE:
+        raise IndexError(msg)
     raise RuntimeError(msg)
 
 

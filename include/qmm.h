@@ -29,7 +29,8 @@ enum qmm_status {
     QMM_ERR_INVALID_ARGUMENT = 1, /* maps to the reference's std::invalid_argument / ValueError */
     QMM_ERR_UNSUPPORTED = 2,      /* valid request this build does not implement */
     QMM_ERR_HIP = 3,              /* HIP runtime error; maps to std::runtime_error / RuntimeError */
-    QMM_ERR_IO = 4                /* file open / read failure (qmm_upload_file, qmm_read_file); OSError */
+    QMM_ERR_IO = 4,               /* file open / read failure (qmm_upload_file, qmm_read_file); OSError */
+    QMM_ERR_OUT_OF_RANGE = 5      /* index outside the KV cache pool (std::out_of_range); IndexError */
 };
 
 enum qmm_ggml_type {
@@ -153,6 +154,88 @@ int qmm_dequantize_q4_0_host(const void* h_q4, void* h_fp16_out, int num_element
 int qmm_dequantize_q8_0_host(const void* h_q8, void* h_fp16_out, int num_elements);
 int qmm_dequantize_q4_k_host(const void* h_q4k, void* h_fp16_out, int num_elements);
 int qmm_dequantize_q6_k_host(const void* h_q6k, void* h_fp16_out, int num_elements);
+
+/* ---------------------------------------------------------------------------------
+ * Transformer layer around the projections (device pointers, fp16 activations,
+ * asynchronous on `stream`).  fp32 arithmetic, one rounding per stored fp16 value, as the
+ * reference's kernels (src/kernels/rmsnorm.hip, rope.hip, attention.hip, mlp.hip).
+ * --------------------------------------------------------------------------------- */
+
+/* out[m, :] = half(x[m, :] * rsqrt(mean(x[m, :]^2) + eps) * weight); weight_dtype F16 or F32
+ * (an F32 weight is rounded to f16 first, as the reference's host does).
+ * Replaces launch_rmsnorm_fp16_device (src/kernels/rmsnorm.h:42-50). */
+int qmm_rmsnorm(const void* x, const void* weight, int weight_dtype, void* out, int M, int K, float eps,
+                void* stream);
+/* h_out = half(x + residual); norm_out = rmsnorm(h_out).  Replaces
+ * launch_rmsnorm_residual_fp16_device (src/kernels/rmsnorm.h:52-61). */
+int qmm_rmsnorm_residual(const void* x, const void* residual, const void* weight, int weight_dtype, void* h_out,
+                         void* norm_out, int M, int K, float eps, void* stream);
+/* out = half(x + residual), n elements.  Replaces launch_residual_add_fp16_device (:63-68). */
+int qmm_residual_add(const void* x, const void* residual, void* out, int64_t n, void* stream);
+/* out = half(silu(gate) * up), n elements.  Replaces launch_swiglu_fp16_device (src/kernels/mlp.h). */
+int qmm_swiglu(const void* gate, const void* up, void* out, int64_t n, void* stream);
+/* RoPE of x [seq_len, num_heads, head_dim] at positions pos_offset + row: pairs (2i, 2i + 1), or
+ * (i, i + head_dim / 2) when neox != 0; inv_freq_i = 1 / freq_base^(2i / head_dim).
+ * Replaces launch_rope_fp16_device (src/kernels/rope.h:21-30). */
+int qmm_rope(const void* x_in, void* x_out, int seq_len, int num_heads, int head_dim, int pos_offset,
+             float freq_base, int neox, void* stream);
+/* Grouped-query attention: Q [q_len, num_heads, head_dim], K / V [kv_len, num_kv_heads, head_dim],
+ * query head h reads KV head h / (num_heads / num_kv_heads); causal rows m see keys
+ * < min(kv_len, start_pos + m + 1); scale 0 means 1 / sqrt(head_dim); head_dim <= 256.
+ * Replaces launch_gqa_attention_fp16 (src/kernels/attention.hip:228-284). */
+int qmm_gqa_attention(const void* Q, const void* K, const void* V, void* out, int q_len, int kv_len, int num_heads,
+                      int num_kv_heads, int head_dim, int start_pos, float scale, int causal, void* stream);
+
+/* KV cache pool of the current device: [num_layers][max_seq_len][num_kv_heads][head_dim] fp16 for
+ * K and for V (grow-only).  Replace init_device_kv_cache_fp16 / free_device_kv_cache_fp16
+ * (src/kernels/attention.hip:286-300). */
+int qmm_kv_cache_init(int num_layers, int max_seq_len, int num_kv_heads, int head_dim);
+int qmm_kv_cache_free(void);
+/* Writes K_new / V_new ([q_len, num_kv_heads, head_dim], rotated) into layer `layer_idx` of the
+ * pool at start_pos, then attends over [0, start_pos + q_len).  Replaces
+ * launch_gqa_attention_cached_fp16_device (src/kernels/attention.hip:376-440). */
+int qmm_gqa_attention_cached(const void* Q, const void* K_new, const void* V_new, void* out, int layer_idx, int q_len,
+                             int start_pos, int num_heads, int num_kv_heads, int head_dim, float scale, int causal,
+                             void* stream);
+
+typedef struct qmm_layer_config {
+    int hidden_size, intermediate_size, num_heads, num_kv_heads, head_dim;
+    float rms_norm_eps, rope_freq_base;
+    int rope_neox;
+    float scale; /* 0: 1 / sqrt(head_dim) */
+} qmm_layer_config;
+
+/* Device-resident weights of one layer: norms are F16 or F32 vectors (dtype QMM_DTYPE_*);
+ * projections are packed GGUF matrices of type 2 / 8 / 12 / 14, N x K as in qmm_gemm. */
+typedef struct qmm_layer_weights {
+    const void* attn_norm;
+    int attn_norm_dtype;
+    const void* wq;
+    int wq_type;
+    const void* wk;
+    int wk_type;
+    const void* wv;
+    int wv_type;
+    const void* wo;
+    int wo_type;
+    const void* ffn_norm;
+    int ffn_norm_dtype;
+    const void* wgate;
+    int wgate_type;
+    const void* wup;
+    int wup_type;
+    const void* wdown;
+    int wdown_type;
+} qmm_layer_weights;
+
+/* x_out [seq_len, hidden] = one Llama layer on x_in (fp16, device): RMSNorm, q/k/v (one fused
+ * launch), RoPE with the K/V cache write at pos_offset, causal GQA over the cache, o, residual +
+ * RMSNorm, gate/up (one fused launch), SwiGLU, down, residual.  Weights stay where they are (no
+ * per-call copies); activations use a grow-only per-stream workspace.  Replaces
+ * launch_forward_layer_cached_fp16 (src/kernels/attention.hip:603-695), which copies the hidden
+ * state and every weight from the host per call. */
+int qmm_forward_layer(const qmm_layer_config* cfg, const qmm_layer_weights* w, const void* x_in, void* x_out,
+                      int layer_idx, int seq_len, int pos_offset, void* stream);
 
 /* One byte range of a file and its destination. */
 typedef struct qmm_file_range {

@@ -1,0 +1,280 @@
+"""GPU parity of the layer kernels and of the device-resident layer pipeline (C ABI).
+
+Bars, as the reference's own tests set them (tests/test_layer.py): each kernel within 2e-3
+absolute of the CPU restatement (oracle/layer_oracle.py), the whole layer within 5e-3 absolute
+for a prefill and for the decode step that follows it through the KV cache.  The layer oracle
+uses the reference's fp16 dequantized weights; the prefill projections (M >= 32) use f16
+operands with f16-rounded scales, which the same bar covers.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+import gguf_oracle as O
+import layer_oracle as L
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev(cuda):
+    import qmm  # noqa: F401
+    return cuda
+
+
+def t16(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def maxerr(a, b):
+    return float(np.max(np.abs(np.asarray(a, np.float32) - np.asarray(b, np.float32))))
+
+
+def stream():
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+@pytest.mark.parametrize("M,K", [(1, 4096), (16, 2048), (7, 1024), (3, 100)])
+@pytest.mark.parametrize("w_f32", [False, True])
+def test_rmsnorm(dev, M, K, w_f32):
+    import torch
+    import qmm
+    r = np.random.default_rng(10 + K + M)
+    x = r.standard_normal((M, K)).astype(np.float16)
+    w32 = (1 + 0.1 * r.standard_normal(K)).astype(np.float32)
+    w = w32 if w_f32 else w32.astype(np.float16)
+    out = torch.empty((M, K), dtype=torch.float16, device=dev)
+    X, Wt = t16(x, dev), t16(w, dev)
+    qmm.check(qmm.lib().qmm_rmsnorm(X.data_ptr(), Wt.data_ptr(), qmm.DTYPE_F32 if w_f32 else qmm.DTYPE_F16,
+                                    out.data_ptr(), M, K, 1e-5, stream()))
+    want = L.rmsnorm(x, w32.astype(np.float16), 1e-5)
+    assert maxerr(host(out), want) < 2e-3
+    # in place
+    qmm.check(qmm.lib().qmm_rmsnorm(X.data_ptr(), Wt.data_ptr(), qmm.DTYPE_F32 if w_f32 else qmm.DTYPE_F16,
+                                    X.data_ptr(), M, K, 1e-5, stream()))
+    assert np.array_equal(host(X), host(out))
+
+
+@pytest.mark.parametrize("M,K", [(4, 4096), (5, 100)])
+def test_rmsnorm_residual_and_residual_add(dev, M, K):
+    import torch
+    import qmm
+    r = np.random.default_rng(20 + K)
+    x = r.standard_normal((M, K)).astype(np.float16)
+    res = r.standard_normal((M, K)).astype(np.float16)
+    w = (1 + 0.1 * r.standard_normal(K)).astype(np.float16)
+    X, R, Wt = t16(x, dev), t16(res, dev), t16(w, dev)
+    h = torch.empty_like(X)
+    nrm = torch.empty_like(X)
+    qmm.check(qmm.lib().qmm_rmsnorm_residual(X.data_ptr(), R.data_ptr(), Wt.data_ptr(), qmm.DTYPE_F16, h.data_ptr(),
+                                             nrm.data_ptr(), M, K, 1e-5, stream()))
+    wh, wn = L.rmsnorm_residual(x, res, w, 1e-5)
+    assert np.array_equal(host(h), wh)
+    assert maxerr(host(nrm), wn) < 2e-3
+    # h_out aliasing x (in place), as a caller may do
+    X2 = t16(x, dev)
+    qmm.check(qmm.lib().qmm_rmsnorm_residual(X2.data_ptr(), R.data_ptr(), Wt.data_ptr(), qmm.DTYPE_F16, X2.data_ptr(),
+                                             nrm.data_ptr(), M, K, 1e-5, stream()))
+    assert np.array_equal(host(X2), wh) and maxerr(host(nrm), wn) < 2e-3
+    out = torch.empty_like(X)
+    qmm.check(qmm.lib().qmm_residual_add(X.data_ptr(), R.data_ptr(), out.data_ptr(), M * K, stream()))
+    assert np.array_equal(host(out), L.residual_add(x, res))
+
+
+@pytest.mark.parametrize("n", [16 * 1024, 1003])
+def test_swiglu(dev, n):
+    import torch
+    import qmm
+    r = np.random.default_rng(40 + n)
+    g = (r.standard_normal(n) * 3).astype(np.float16)
+    u = r.standard_normal(n).astype(np.float16)
+    out = torch.empty(n, dtype=torch.float16, device=dev)
+    G, U = t16(g, dev), t16(u, dev)  # keep the inputs alive until the kernel has run
+    qmm.check(qmm.lib().qmm_swiglu(G.data_ptr(), U.data_ptr(), out.data_ptr(), n, stream()))
+    assert maxerr(host(out), L.swiglu(g, u)) < 2e-3
+
+
+@pytest.mark.parametrize("neox", [False, True])
+@pytest.mark.parametrize("seq,pos,heads,d,base", [(8, 0, 16, 64, 10000.0), (1, 17, 16, 64, 10000.0),
+                                                  (5, 4090, 32, 128, 500000.0)])
+def test_rope(dev, neox, seq, pos, heads, d, base):
+    import torch
+    import qmm
+    r = np.random.default_rng(seq * 100 + pos + d)
+    x = r.standard_normal((seq, heads, d)).astype(np.float16)
+    out = torch.empty((seq, heads, d), dtype=torch.float16, device=dev)
+    X = t16(x, dev)
+    qmm.check(qmm.lib().qmm_rope(X.data_ptr(), out.data_ptr(), seq, heads, d, pos, base, int(neox), stream()))
+    assert maxerr(host(out), L.rope(x, pos, base, neox)) < 2e-3
+
+
+@pytest.mark.parametrize("q_len,kv_len,start,heads,kvh,d", [(12, 12, 0, 16, 4, 64), (1, 25, 24, 16, 4, 64),
+                                                            (1, 1000, 999, 32, 8, 128), (40, 300, 260, 8, 2, 128),
+                                                            (3, 3, 0, 4, 4, 256)])
+def test_gqa_attention(dev, q_len, kv_len, start, heads, kvh, d):
+    import torch
+    import qmm
+    r = np.random.default_rng(30 + kv_len + d)
+    Q = (r.standard_normal((q_len, heads, d)) * 0.5).astype(np.float16)
+    K = (r.standard_normal((kv_len, kvh, d)) * 0.5).astype(np.float16)
+    V = (r.standard_normal((kv_len, kvh, d)) * 0.5).astype(np.float16)
+    out = torch.empty((q_len, heads, d), dtype=torch.float16, device=dev)
+    scale = 1.0 / math.sqrt(d)
+    Qd, Kd, Vd = t16(Q, dev), t16(K, dev), t16(V, dev)
+    qmm.check(qmm.lib().qmm_gqa_attention(Qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), out.data_ptr(), q_len, kv_len,
+                                          heads, kvh, d, start, scale, 1, stream()))
+    assert maxerr(host(out), L.gqa_attention(Q, K, V, start, scale, True)) < 2e-3
+
+
+def test_kv_cache_pool_and_cached_attention(dev):
+    import torch
+    import qmm
+    lib = qmm.lib()
+    qmm.check(lib.qmm_kv_cache_free())
+    Q = torch.zeros((1, 8, 64), dtype=torch.float16, device=dev)
+    with pytest.raises(RuntimeError):   # not initialized
+        qmm.check(lib.qmm_gqa_attention_cached(Q.data_ptr(), Q.data_ptr(), Q.data_ptr(), Q.data_ptr(), 0, 1, 0, 8, 2, 64,
+                                               0.0, 1, stream()))
+    with pytest.raises(ValueError):
+        qmm.check(lib.qmm_kv_cache_init(0, 16, 2, 64))
+    qmm.check(lib.qmm_kv_cache_init(2, 16, 2, 64))
+    r = np.random.default_rng(60)
+    K = (r.standard_normal((16, 2, 64)) * 0.5).astype(np.float16)
+    V = (r.standard_normal((16, 2, 64)) * 0.5).astype(np.float16)
+    Qs = (r.standard_normal((16, 8, 64)) * 0.5).astype(np.float16)
+    out = torch.empty((16, 8, 64), dtype=torch.float16, device=dev)
+    Kd, Vd, Qd = t16(K, dev), t16(V, dev), t16(Qs, dev)
+    # prefill 10 rows of layer 1, then decode row 10
+    qmm.check(lib.qmm_gqa_attention_cached(Qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), out.data_ptr(), 1, 10, 0, 8, 2, 64,
+                                           0.0, 1, stream()))
+    assert maxerr(host(out)[:10], L.gqa_attention(Qs[:10], K[:10], V[:10], 0)) < 2e-3
+    qmm.check(lib.qmm_gqa_attention_cached(Qd[10:].data_ptr(), Kd[10:].data_ptr(), Vd[10:].data_ptr(), out.data_ptr(), 1, 1,
+                                           10, 8, 2, 64, 0.0, 1, stream()))
+    assert maxerr(host(out)[:1], L.gqa_attention(Qs[10:11], K[:11], V[:11], 10)) < 2e-3
+    with pytest.raises(IndexError):
+        qmm.check(lib.qmm_gqa_attention_cached(Qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), out.data_ptr(), 2, 1, 0, 8, 2,
+                                               64, 0.0, 1, stream()))
+    with pytest.raises(IndexError):
+        qmm.check(lib.qmm_gqa_attention_cached(Qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), out.data_ptr(), 0, 2, 15, 8, 2,
+                                               64, 0.0, 1, stream()))
+    with pytest.raises(ValueError):
+        qmm.check(lib.qmm_gqa_attention_cached(Qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), out.data_ptr(), 0, 1, 0, 8, 4,
+                                               64, 0.0, 1, stream()))
+    qmm.check(lib.qmm_kv_cache_free())
+
+
+QUANT = {O.GGML_Q4_0: O.quantize_q4_0, O.GGML_Q8_0: O.quantize_q8_0, O.GGML_Q4_K: O.quantize_q4_k,
+         O.GGML_Q6_K: O.quantize_q6_k}
+
+
+def make_layer(r, hidden, inter, heads, kvh, d, types):
+    """Packed weights and their fp16 dequantization for one layer; `types` maps projection -> type."""
+    shapes = {"q": (heads * d, hidden), "k": (kvh * d, hidden), "v": (kvh * d, hidden), "o": (hidden, heads * d),
+              "gate": (inter, hidden), "up": (inter, hidden), "down": (hidden, inter)}
+    packed, deq = {}, {}
+    for name, (n, k) in shapes.items():
+        t = types[name]
+        w = (r.standard_normal((n, k)) / math.sqrt(k)).astype(np.float32)
+        raw = QUANT[t](w.reshape(-1))
+        packed[name] = (t, raw)
+        deq[name] = O.dequantize_f16(t, raw, n * k).reshape(n, k)
+    deq["attn_norm"] = (1 + 0.05 * r.standard_normal(hidden)).astype(np.float16)
+    deq["ffn_norm"] = (1 + 0.05 * r.standard_normal(hidden)).astype(np.float16)
+    return packed, deq
+
+
+@pytest.mark.parametrize("prefill", [4, 40])
+def test_forward_layer_prefill_then_decode(dev, prefill):
+    import torch
+    import qmm
+    r = np.random.default_rng(50 + prefill)
+    hidden, inter, heads, kvh, d = 256, 512, 8, 2, 32
+    types = {"q": O.GGML_Q4_K, "k": O.GGML_Q4_K, "v": O.GGML_Q6_K, "o": O.GGML_Q8_0, "gate": O.GGML_Q4_K,
+             "up": O.GGML_Q4_0, "down": O.GGML_Q6_K}
+    packed, deq = make_layer(r, hidden, inter, heads, kvh, d, types)
+    dev_w = {n: t16(raw, dev) for n, (t, raw) in packed.items()}
+    norms = {n: t16(deq[n], dev) for n in ("attn_norm", "ffn_norm")}
+    w = qmm.LayerWeights()
+    w.attn_norm, w.attn_norm_dtype = norms["attn_norm"].data_ptr(), qmm.DTYPE_F16
+    w.ffn_norm, w.ffn_norm_dtype = norms["ffn_norm"].data_ptr(), qmm.DTYPE_F16
+    for f, n in (("wq", "q"), ("wk", "k"), ("wv", "v"), ("wo", "o"), ("wgate", "gate"), ("wup", "up"), ("wdown", "down")):
+        setattr(w, f, dev_w[n].data_ptr())
+        setattr(w, f + "_type", packed[n][0])
+    c = qmm.LayerConfig()
+    c.hidden_size, c.intermediate_size, c.num_heads, c.num_kv_heads, c.head_dim = hidden, inter, heads, kvh, d
+    c.rms_norm_eps, c.rope_freq_base, c.rope_neox, c.scale = 1e-5, 10000.0, 0, 0.0
+    cfg = {"num_heads": heads, "num_kv_heads": kvh, "head_dim": d, "rms_norm_eps": 1e-5, "rope_freq_base": 10000.0,
+           "rope_neox": False}
+    total = prefill + 1
+    x = (r.standard_normal((total, hidden)) * 0.5).astype(np.float16)
+    kc, vc = np.zeros((64, kvh, d), np.float16), np.zeros((64, kvh, d), np.float16)
+    want_pre = L.layer_forward(x[:prefill], deq, cfg, kc, vc, 0)
+    want_dec = L.layer_forward(x[prefill:], deq, cfg, kc, vc, prefill)
+    lib = qmm.lib()
+    qmm.check(lib.qmm_kv_cache_init(3, 64, kvh, d))
+    try:
+        X = t16(x, dev)
+        Y = torch.empty_like(X)
+        qmm.check(lib.qmm_forward_layer(c, w, X.data_ptr(), Y.data_ptr(), 2, prefill, 0, stream()))
+        qmm.check(lib.qmm_forward_layer(c, w, X[prefill:].data_ptr(), Y[prefill:].data_ptr(), 2, 1, prefill, stream()))
+        y = host(Y)
+        assert maxerr(y[:prefill], want_pre) < 5e-3
+        assert maxerr(y[prefill:], want_dec) < 5e-3
+        with pytest.raises(IndexError):
+            qmm.check(lib.qmm_forward_layer(c, w, X.data_ptr(), Y.data_ptr(), 3, 1, 0, stream()))
+    finally:
+        qmm.check(lib.qmm_kv_cache_free())
+
+
+def test_transformer_layer_over_resident_weights(dev, tmp_path):
+    import torch
+    import gguf
+    import layer
+    import resident
+    r = np.random.default_rng(70)
+    hidden, inter, heads, kvh, d = 256, 512, 8, 2, 32
+    types = {n: O.GGML_Q4_K for n in ("q", "k", "v", "o", "gate", "up")}
+    types["down"] = O.GGML_Q6_K
+    packed, deq = make_layer(r, hidden, inter, heads, kvh, d, types)
+    names = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output", "gate": "ffn_gate", "up": "ffn_up",
+             "down": "ffn_down"}
+    shapes = {"q": (heads * d, hidden), "k": (kvh * d, hidden), "v": (kvh * d, hidden), "o": (hidden, heads * d),
+              "gate": (inter, hidden), "up": (inter, hidden), "down": (hidden, inter)}
+    tensors = [("blk.0.attn_norm.weight", (hidden,), gguf.GGMLType.F32, deq["attn_norm"].astype(np.float32).tobytes()),
+               ("blk.0.ffn_norm.weight", (hidden,), gguf.GGMLType.F16, deq["ffn_norm"].tobytes())]
+    for n, (t, raw) in packed.items():
+        tensors.append((f"blk.0.{names[n]}.weight", (shapes[n][1], shapes[n][0]), gguf.GGMLType(t), raw.tobytes()))
+    V = gguf.GGUFValueType
+    meta = {"general.architecture": (V.STRING, "llama"), "llama.block_count": (V.UINT32, 1),
+            "llama.embedding_length": (V.UINT32, hidden), "llama.feed_forward_length": (V.UINT32, inter),
+            "llama.attention.head_count": (V.UINT32, heads), "llama.attention.head_count_kv": (V.UINT32, kvh),
+            "llama.rope.dimension_count": (V.UINT32, d), "llama.attention.layer_norm_rms_epsilon": (V.FLOAT32, 1e-5),
+            "llama.rope.freq_base": (V.FLOAT32, 10000.0)}
+    path = tmp_path / "layer.gguf"
+    with open(path, "wb") as f:
+        gguf.write_synthetic_gguf(f, meta, tensors)
+    rw = resident.ResidentWeights(str(path))
+    cfg = layer.LlamaLayerConfig.from_gguf_metadata(rw.gguf.metadata)
+    assert (cfg.hidden_size, cfg.num_kv_heads, cfg.head_dim, cfg.rope_neox) == (hidden, kvh, d, False)
+    x = (r.standard_normal((5, hidden)) * 0.5).astype(np.float16)
+    kc, vc = np.zeros((16, kvh, d), np.float16), np.zeros((16, kvh, d), np.float16)
+    ocfg = {"num_heads": heads, "num_kv_heads": kvh, "head_dim": d, "rms_norm_eps": 1e-5, "rope_freq_base": 10000.0,
+            "rope_neox": False}
+    want = np.concatenate([L.layer_forward(x[:4], deq, ocfg, kc, vc, 0), L.layer_forward(x[4:], deq, ocfg, kc, vc, 4)])
+    tl = layer.TransformerLayer(cfg)
+    with layer.DeviceKVCache(1, 16, kvh, d) as kv:
+        X = t16(x, dev)
+        y0, _ = tl.forward_resident(X[:4].contiguous(), rw, 0, 0, kv)
+        y1, _ = tl.forward_resident(X[4:].contiguous(), rw, 0, 4, kv)
+        y = np.concatenate([host(y0), host(y1)])
+    assert maxerr(y, want) < 5e-3
