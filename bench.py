@@ -21,6 +21,7 @@ Q4_0 4096 x 4096 case, prefill M = 512 with the vendor f16 GEMM on dense weights
 GEMV ones on rotated weight copies larger than the 256 MB MALL.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-extra] [--no-cpu-baseline] [--pmc-workload]
+       [--full-layers-only]
        [--prefill-only]
 """
 
@@ -317,6 +318,80 @@ def run_prefill(torch, qmm, hip, gen, dev, steps, warmup):
     return res
 
 
+def run_full_layers(torch, qmm, hip, wl, layers, proj_ms, dev, gen, steps, context=1024):
+    """Whole Llama-3-70B layers (qmm_forward_layer: RMSNorm, q/k/v, RoPE + KV write, attention
+    over the cache, o, residual + RMSNorm, gate/up, SwiGLU, down, residual) on the decode
+    benchmark's 80 resident Q4_K_M layers: a (context - 1)-token prefill through all layers fills
+    the KV cache (timed: prefill tokens/s), then decode steps of one token at position
+    context - 1 attend over `context` keys (timed: ms per token), beside the projections-only
+    step of the same weights."""
+    hidden, inter, heads, kvh, d = 8192, 28672, 64, 8, 128
+    c = qmm.LayerConfig()
+    c.hidden_size, c.intermediate_size, c.num_heads, c.num_kv_heads, c.head_dim = hidden, inter, heads, kvh, d
+    c.rms_norm_eps, c.rope_freq_base, c.rope_neox, c.scale = 1e-5, 500000.0, 0, 0.0
+    norm = torch.ones(hidden, dtype=torch.float16, device=dev)
+    ws = []
+    for layer in range(layers):
+        w = qmm.LayerWeights()
+        w.attn_norm, w.attn_norm_dtype, w.ffn_norm, w.ffn_norm_dtype = norm.data_ptr(), qmm.DTYPE_F16, norm.data_ptr(), \
+            qmm.DTYPE_F16
+        for i, f in enumerate(("wq", "wk", "wv", "wo", "wgate", "wup", "wdown")):
+            t, _, wt, _, _, _ = wl.descs_py[7 * layer + i]
+            setattr(w, f, wt.data_ptr())
+            setattr(w, f + "_type", t)
+        ws.append(w)
+    stream = torch.cuda.current_stream().cuda_stream
+    lib = qmm.lib()
+    qmm.check(lib.qmm_kv_cache_init(layers, context, kvh, d))
+    try:
+        P = context - 1
+        xa = (torch.randn((P, hidden), device=dev, generator=gen) * 0.5).half()
+        xb = torch.empty_like(xa)
+
+        def prefill():
+            a, b = xa, xb
+            for layer in range(layers):
+                qmm.check(lib.qmm_forward_layer(c, ws[layer], a.data_ptr(), b.data_ptr(), layer, P, 0, stream))
+                a, b = b, a
+
+        prefill()  # warm-up (workspace growth, first touch)
+        torch.cuda.synchronize()
+        e0, e1 = hip.event(), hip.event()
+        hip.record(e0, stream)
+        prefill()
+        hip.record(e1, stream)
+        torch.cuda.synchronize()
+        pre_ms = hip.elapsed_ms(e0, e1)
+        ya, yb = xa[:1].clone(), xa[:1].clone()
+
+        def decode():
+            a, b = ya, yb
+            for layer in range(layers):
+                qmm.check(lib.qmm_forward_layer(c, ws[layer], a.data_ptr(), b.data_ptr(), layer, 1, P, stream))
+                a, b = b, a
+
+        decode()
+        torch.cuda.synchronize()
+        hip.record(e0, stream)
+        for _ in range(steps):
+            decode()
+        hip.record(e1, stream)
+        torch.cuda.synchronize()
+        dec_ms = hip.elapsed_ms(e0, e1) / steps
+        hip.destroy(e0)
+        hip.destroy(e1)
+    finally:
+        qmm.check(lib.qmm_kv_cache_free())
+        qmm.check(lib.qmm_release_workspace())
+    res = {"layers": layers, "context": context, "decode_ms_per_token": round(dec_ms, 3),
+           "decode_tokens_per_s": round(1e3 / dec_ms, 1), "projections_only_ms_per_token": round(proj_ms, 3),
+           "prefill_tokens": P, "prefill_ms": round(pre_ms, 2), "prefill_tokens_per_s": round(P / (pre_ms * 1e-3), 1),
+           "note": "whole layers; weights of the decode benchmark; fp16 activations; embedding and lm_head excluded"}
+    log(f"70B full layers: decode {dec_ms:.3f} ms/token at context {context} (projections alone {proj_ms:.3f}); "
+        f"prefill {P} tokens {pre_ms:.1f} ms = {res['prefill_tokens_per_s']} tokens/s")
+    return res
+
+
 def run_upload(torch, qmm, dev, layers=2):
     """Weight residency: a GGUF file holding `layers` Llama-3-70B Q4_K_M layers (7 packed
     matrices each, 542 MB per layer, random bytes) is loaded into HBM from the page cache
@@ -458,6 +533,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the prefill section (8B M=512 shapes) and print its results as JSON")
+    ap.add_argument("--full-layers-only", action="store_true",
+                    help="run only the whole-layer 70B section (prefill through the KV cache, then decode) and "
+                         "print its results as JSON")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run only the counter-collection workload (copy calibration + dominant GEMV)")
     args = ap.parse_args()
@@ -492,6 +570,11 @@ def main():
     wl = Workload(torch, qmm, "70b", [specs70], args.layers, 1, dev, gen, dominant=dominant)
     torch.cuda.synchronize()
     log(f"70B weights ready: {wl.weight_bytes / 1e9:.2f} GB in {time.perf_counter() - t0:.1f} s")
+    if args.full_layers_only:
+        ms, _ = run_workload(torch, qmm, hip, wl, max(3, args.steps // 2), 2)
+        print(json.dumps({"70b_q4_k_m_full_layers": run_full_layers(torch, qmm, hip, wl, args.layers, ms, dev, gen,
+                                                                    max(3, args.steps // 2))}), flush=True)
+        return
     step_ms = []
     ms, wall = run_workload(torch, qmm, hip, wl, args.steps, args.warmup, per_step=step_ms)
     step_ms.sort()
@@ -524,6 +607,9 @@ def main():
         extra["70b_q4_k_m_m4"] = {"GB/s": round(wl4.algo_bytes / (ms4 * 1e-3) / 1e9, 1), "ms_per_token": round(ms4, 3),
                                   "frac_hbm": round(wl4.algo_bytes / (ms4 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         log(f"70B M=4: {ms4:.3f} ms/step, {extra['70b_q4_k_m_m4']['GB/s']} GB/s")
+    if not args.no_extra:
+        extra["70b_q4_k_m_full_layers"] = run_full_layers(torch, qmm, hip, wl, args.layers, ms, dev, gen,
+                                                          max(3, args.steps // 2))
     wl.free()
     del wl
     torch.cuda.empty_cache()

@@ -12,11 +12,12 @@
 //   * RoPE: one launch rotates q into its buffer, rotates k straight into the layer's K cache
 //     at the token positions and copies v into the V cache (the reference copies K/V into the
 //     pool separately); inverse frequencies come from the host in fp32, as in the reference.
-//   * Attention: split over the KV length.  A wave owns (query row, query head, chunk of 256
-//     keys): lanes hold head_dim / 64 query dimensions, and for each key the wave forms the dot
-//     product (wave reduction), updates an fp32 online softmax and the running output.  Chunks
-//     are merged in a fixed order by a second pass (deterministic), skipped for one chunk.  The
-//     query heads of one KV head sit in one workgroup, so their K/V reads share the caches.
+//   * Attention: split over the KV length.  A wave owns (query row, query head, chunk of 64
+//     keys): lanes hold head_dim / 64 consecutive query dimensions; keys are loaded 8 at a time
+//     (8 rows in flight per wave), their dot products reduced across the wave together, and an
+//     fp32 online softmax updates the running output.  Chunks are merged in a fixed order by a
+//     second pass (deterministic), skipped for one chunk.  The query heads of one KV head sit
+//     in one workgroup, so their K/V reads share the caches.
 //   * SwiGLU and the residual add: 8 values per thread.
 //   * Layer: q/k/v and gate/up each run as one fused projection launch (qmm_gemm_batch), all
 //     kernels on the caller's stream with no host synchronisation; activations live in a
@@ -33,11 +34,21 @@ namespace qmm {
 namespace {
 
 constexpr int kNormThreads = 256;
-constexpr int kAttnChunk = 256;      // keys per attention chunk
+constexpr int kAttnChunk = 64;       // keys per attention chunk (one wave each)
 constexpr int kMaxHeadDim = 256;
 constexpr int kMaxRopePairs = kMaxHeadDim / 2;
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// fp32 acc + the dot product of two f16 pairs (v_dot2_f32_f16)
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+    h2v x, y;
+    __builtin_memcpy(&x, &a, 4);
+    __builtin_memcpy(&y, &b, 4);
+    return __builtin_amdgcn_fdot2(x, y, acc, false);
+}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -193,15 +204,19 @@ __global__ __launch_bounds__(256) void rope_kernel(const _Float16* __restrict__ 
     dst[i1] = static_cast<_Float16>(a * sn + b * c);
 }
 
-// Attention, one wave per (query row m, query head h, key chunk c); D = head_dim / 64 dims per
-// lane (lane l holds dims l + 64 i).  Partial results: running max, sum and unnormalised output
-// (fp32), or the final fp16 output when there is a single chunk.
+// Attention, one wave per (query row m, query head h, key chunk c).  Lane l holds the D
+// consecutive dimensions D*l .. D*l + D - 1 of the head (head_dim <= 64 D), so a key row is one
+// coalesced read across the wave.  Keys are taken 8 at a time: the 8 K and V rows are loaded
+// together (8 reads in flight per wave instead of one), the 8 dot products are reduced across
+// the wave together, then the fp32 online softmax takes them in key order.  Partial results
+// (running max, sum and unnormalised output), or the fp16 output when there is one chunk.
 template <int D>
 __global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restrict__ Q, const _Float16* __restrict__ Kc,
                                                        const _Float16* __restrict__ Vc, _Float16* __restrict__ out,
                                                        float* __restrict__ part, int q_len, int kv_len, int heads,
                                                        int kv_heads, int head_dim, int start_pos, float scale, int causal,
                                                        int chunks) {
+    constexpr int G = 8;  // keys per batch
     const int lane = threadIdx.x & 63;
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     const int64_t total = static_cast<int64_t>(q_len) * heads * chunks;
@@ -217,46 +232,75 @@ __global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restri
     const int n_keys = causal ? min(kv_len, start_pos + m + 1) : kv_len;
     const int s0 = c * kAttnChunk;
     const int s1 = min(n_keys, s0 + kAttnChunk);
+    const bool full = head_dim == 64 * D;  // every lane owns D valid dims: vector reads
+    const int d0 = D * lane;
 
-    const _Float16* qp = Q + (static_cast<size_t>(m) * heads + h) * head_dim;
-    float qv[D], acc[D];
+    auto load = [&](const _Float16* p, float (&o)[D]) {
+        if (full) {
+            _Float16 v[D];
+            __builtin_memcpy(v, p + d0, sizeof(v));
 #pragma unroll
-    for (int i = 0; i < D; ++i) {
-        const int d = lane + 64 * i;
-        qv[i] = d < head_dim ? static_cast<float>(qp[d]) : 0.0f;
-        acc[i] = 0.0f;
-    }
+            for (int i = 0; i < D; ++i) o[i] = static_cast<float>(v[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < D; ++i) o[i] = d0 + i < head_dim ? static_cast<float>(p[d0 + i]) : 0.0f;
+        }
+    };
+    float qv[D], acc[D];
+    load(Q + (static_cast<size_t>(m) * heads + h) * head_dim, qv);
+#pragma unroll
+    for (int i = 0; i < D; ++i) acc[i] = 0.0f;
     float mx = -INFINITY, sum = 0.0f;
     const size_t row = static_cast<size_t>(kv_heads) * head_dim;
-    for (int s = s0; s < s1; ++s) {
-        const _Float16* kp = Kc + static_cast<size_t>(s) * row + static_cast<size_t>(kvh) * head_dim;
-        const _Float16* vp = Vc + static_cast<size_t>(s) * row + static_cast<size_t>(kvh) * head_dim;
-        float dot = 0.0f;
+    const _Float16* kbase = Kc + static_cast<size_t>(kvh) * head_dim;
+    const _Float16* vbase = Vc + static_cast<size_t>(kvh) * head_dim;
+    for (int s = s0; s < s1; s += G) {
+        const int n = min(G, s1 - s);
+        float kk[G][D], vv[G][D];
 #pragma unroll
-        for (int i = 0; i < D; ++i) {
-            const int d = lane + 64 * i;
-            if (d < head_dim) dot += qv[i] * static_cast<float>(kp[d]);
+        for (int j = 0; j < G; ++j) {
+            const size_t r = static_cast<size_t>(s + min(j, n - 1));  // rows past the end re-read the last
+            load(kbase + r * row, kk[j]);
+            load(vbase + r * row, vv[j]);
         }
-        const float sc = wave_sum(dot) * scale;
-        const float mn = fmaxf(mx, sc);
-        const float a = expf(mx - mn);  // exp(-inf) = 0 for the first key
-        const float e = expf(sc - mn);
-        sum = sum * a + e;
+        float dot[G];
 #pragma unroll
-        for (int i = 0; i < D; ++i) {
-            const int d = lane + 64 * i;
-            if (d < head_dim) acc[i] = acc[i] * a + e * static_cast<float>(vp[d]);
+        for (int j = 0; j < G; ++j) {
+            dot[j] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < D; ++i) dot[j] += qv[i] * kk[j][i];
         }
-        mx = mn;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+            for (int j = 0; j < G; ++j) dot[j] += __shfl_xor(dot[j], o, 64);
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            if (j < n) {
+                const float sc = dot[j] * scale;
+                const float mn = fmaxf(mx, sc);
+                const float a = expf(mx - mn);  // exp(-inf) = 0 for the first key
+                const float e = expf(sc - mn);
+                sum = sum * a + e;
+#pragma unroll
+                for (int i = 0; i < D; ++i) acc[i] = acc[i] * a + e * vv[j][i];
+                mx = mn;
+            }
+        }
     }
+    auto store = [&](auto* dst, auto cvt) {
+        if (full) {
+#pragma unroll
+            for (int i = 0; i < D; ++i) dst[d0 + i] = cvt(acc[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < D; ++i)
+                if (d0 + i < head_dim) dst[d0 + i] = cvt(acc[i]);
+        }
+    };
     if (chunks == 1) {
         const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-        _Float16* op = out + (static_cast<size_t>(m) * heads + h) * head_dim;
-#pragma unroll
-        for (int i = 0; i < D; ++i) {
-            const int d = lane + 64 * i;
-            if (d < head_dim) op[d] = static_cast<_Float16>(acc[i] * inv);
-        }
+        store(out + (static_cast<size_t>(m) * heads + h) * head_dim, [&](float v) { return static_cast<_Float16>(v * inv); });
         return;
     }
     float* pp = part + static_cast<size_t>(wave) * (head_dim + 2);
@@ -264,10 +308,98 @@ __global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restri
         pp[0] = mx;
         pp[1] = sum;
     }
+    store(pp + 2, [](float v) { return v; });
+}
+
+// Attention for head_dim a multiple of 8 up to 128, one wave per (query row m, query head h, chunk
+// of 64 keys), with lanes over keys for the scores and over dimensions for the output:
+//   * lane j reads the whole K row of key s0 + j (16-byte loads, all in flight at once) and
+//     forms q . k with v_dot2 on f16 pairs (q is the same for every lane);
+//   * one wave max and one wave sum give the chunk's softmax statistics;
+//   * lane l then owns dims 2l, 2l + 1 of the output, reads the V rows of all the chunk's keys at
+//     once and accumulates p_j v_j with p_j broadcast from lane j.
+// Output: partial results (max, sum, unnormalised output) as attention_kernel, or fp16 output
+// when there is one chunk.
+__global__ __launch_bounds__(256) void attention_keys_kernel(const _Float16* __restrict__ Q, const _Float16* __restrict__ Kc,
+                                                            const _Float16* __restrict__ Vc, _Float16* __restrict__ out,
+                                                            float* __restrict__ part, int q_len, int kv_len, int heads,
+                                                            int kv_heads, int head_dim, int start_pos, float scale,
+                                                            int causal, int chunks) {
+    constexpr int kMaxPairs = 64;  // head_dim <= 128
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int64_t total = static_cast<int64_t>(q_len) * heads * chunks;
+    if (wave >= total) return;
+    const int h = static_cast<int>(wave % heads);
+    const int64_t t = wave / heads;
+    const int c = static_cast<int>(t % chunks);
+    const int m = static_cast<int>(t / chunks);
+    const int kvh = h / (heads / kv_heads);
+    const int n_keys = causal ? min(kv_len, start_pos + m + 1) : kv_len;
+    const int s0 = c * kAttnChunk;
+    const int n = max(0, min(n_keys, s0 + kAttnChunk) - s0);  // keys of this chunk
+    const int pairs = head_dim / 2;
+    const size_t row = static_cast<size_t>(kv_heads) * head_dim;
+
+    // scores: lane j <-> key s0 + j (lanes past the chunk re-read its first key and are masked)
+    const uint32_t* qp = reinterpret_cast<const uint32_t*>(Q + (static_cast<size_t>(m) * heads + h) * head_dim);
+    const int sj = s0 + (lane < n ? lane : 0);
+    const u32x4* kr = reinterpret_cast<const u32x4*>(Kc + static_cast<size_t>(sj) * row + static_cast<size_t>(kvh) * head_dim);
+    u32x4 kv[kMaxPairs / 4];
 #pragma unroll
-    for (int i = 0; i < D; ++i) {
-        const int d = lane + 64 * i;
-        if (d < head_dim) pp[2 + d] = acc[i];
+    for (int i = 0; i < kMaxPairs / 4; ++i)
+        if (4 * i < pairs) kv[i] = kr[i];
+    float dot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxPairs / 4; ++i) {
+        if (4 * i < pairs) {
+            const uint32_t w[4] = {kv[i].x, kv[i].y, kv[i].z, kv[i].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dot = dot2(qp[4 * i + e], w[e], dot);
+        }
+    }
+    const float sc = lane < n ? dot * scale : -INFINITY;
+    float mx = sc;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    const float e = n > 0 ? expf(sc - mx) : 0.0f;  // 0 on masked lanes
+    const float sum = wave_sum(e);
+
+    // output: lane l <-> dims 2l, 2l + 1
+    float acc0 = 0.0f, acc1 = 0.0f;
+    const bool own = 2 * lane < head_dim;
+    const uint32_t* vbase = reinterpret_cast<const uint32_t*>(Vc + static_cast<size_t>(kvh) * head_dim) + (own ? lane : 0);
+    const size_t vrow = row / 2;  // in f16 pairs
+    for (int j0 = 0; j0 < n; j0 += 16) {
+        uint32_t vv[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) vv[j] = vbase[static_cast<size_t>(s0 + min(j0 + j, n - 1)) * vrow];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const float pj = __shfl(e, j0 + j, 64);  // 0 beyond the chunk's keys
+            h2v v;
+            __builtin_memcpy(&v, &vv[j], 4);
+            acc0 += pj * static_cast<float>(v[0]);
+            acc1 += pj * static_cast<float>(v[1]);
+        }
+    }
+    if (chunks == 1) {
+        if (own) {
+            const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+            _Float16* op = out + (static_cast<size_t>(m) * heads + h) * head_dim + 2 * lane;
+            op[0] = static_cast<_Float16>(acc0 * inv);
+            op[1] = static_cast<_Float16>(acc1 * inv);
+        }
+        return;
+    }
+    float* pp = part + static_cast<size_t>(wave) * (head_dim + 2);
+    if (lane == 0) {
+        pp[0] = n > 0 ? mx : -INFINITY;
+        pp[1] = sum;
+    }
+    if (own) {
+        pp[2 + 2 * lane] = acc0;
+        pp[3 + 2 * lane] = acc1;
     }
 }
 
@@ -403,7 +535,13 @@ hipError_t launch_attention(const void* Q, const void* K, const void* V, void* o
                            static_cast<float*>(part), q_len, kv_len, heads, kv_heads, head_dim, start_pos, scale,
                            causal ? 1 : 0, chunks);
     };
-    if (head_dim <= 64) go(std::integral_constant<int, 1>{});
+    const bool aligned = (reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(K) | reinterpret_cast<uintptr_t>(V)) % 16 == 0;
+    if (head_dim % 8 == 0 && head_dim <= 128 && aligned)
+        hipLaunchKernelGGL(attention_keys_kernel, grid, dim3(256), 0, stream, static_cast<const _Float16*>(Q),
+                           static_cast<const _Float16*>(K), static_cast<const _Float16*>(V), static_cast<_Float16*>(out),
+                           static_cast<float*>(part), q_len, kv_len, heads, kv_heads, head_dim, start_pos, scale,
+                           causal ? 1 : 0, chunks);
+    else if (head_dim <= 64) go(std::integral_constant<int, 1>{});
     else if (head_dim <= 128) go(std::integral_constant<int, 2>{});
     else go(std::integral_constant<int, 4>{});
     hipError_t e = hipGetLastError();

@@ -120,7 +120,7 @@ def test_rope(dev, neox, seq, pos, heads, d, base):
 
 @pytest.mark.parametrize("q_len,kv_len,start,heads,kvh,d", [(12, 12, 0, 16, 4, 64), (1, 25, 24, 16, 4, 64),
                                                             (1, 1000, 999, 32, 8, 128), (40, 300, 260, 8, 2, 128),
-                                                            (3, 3, 0, 4, 4, 256)])
+                                                            (3, 3, 0, 4, 4, 256), (5, 130, 125, 4, 2, 96)])
 def test_gqa_attention(dev, q_len, kv_len, start, heads, kvh, d):
     import torch
     import qmm
