@@ -30,6 +30,7 @@ const char* type_name(int t) {
         case QMM_TYPE_Q8_0: return "Q8_0";
         case QMM_TYPE_Q4_K: return "Q4_K";
         case QMM_TYPE_Q6_K: return "Q6_K";
+        case QMM_TYPE_F16: return "F16";
         default: return "unknown";
     }
 }
@@ -38,9 +39,13 @@ bool known_type(int t) {
     return t == QMM_TYPE_Q4_0 || t == QMM_TYPE_Q8_0 || t == QMM_TYPE_Q4_K || t == QMM_TYPE_Q6_K;
 }
 
+// Weight types of the GEMM entry points: the quantized formats and dense F16 rows (the
+// reference's matmul_nt operand, w_type 1 of its layer pipeline).
+bool gemm_type(int t) { return known_type(t) || t == QMM_TYPE_F16; }
+
 int check_gemm_args(int t, const void* A, int a_dtype, const void* W, void* C, int c_dtype, int M, int N,
                     int K) {
-    if (!known_type(t)) return fail(QMM_ERR_INVALID_ARGUMENT, "Unsupported ggml_type " + std::to_string(t) + ".");
+    if (!gemm_type(t)) return fail(QMM_ERR_INVALID_ARGUMENT, "Unsupported ggml_type " + std::to_string(t) + ".");
     if (a_dtype != QMM_DTYPE_F32 && a_dtype != QMM_DTYPE_F16)
         return fail(QMM_ERR_INVALID_ARGUMENT, "a_dtype must be QMM_DTYPE_F32 or QMM_DTYPE_F16.");
     if (c_dtype != QMM_DTYPE_F32 && c_dtype != QMM_DTYPE_F16)
@@ -198,6 +203,8 @@ int dequant_host(int t, const void* hq, void* hout, int num_elements) {
 
 }  // namespace
 
+int qmm::set_last_error(int code, const std::string& msg) { return fail(code, msg); }
+
 extern "C" {
 
 const char* qmm_last_error(void) { return g_last_error.c_str(); }
@@ -207,7 +214,7 @@ int qmm_version(void) { return 1000; }
 int qmm_gemv_max_m(void) { return qmm::kGemvMaxM; }
 
 size_t qmm_weight_bytes(int ggml_type, int64_t n, int64_t k) {
-    if (!known_type(ggml_type) || n < 0 || k < 0) return 0;
+    if (!gemm_type(ggml_type) || n < 0 || k < 0) return 0;
     const int qk = qmm::block_elems(ggml_type);
     if (k % qk != 0) return 0;
     return static_cast<size_t>(n) * static_cast<size_t>(k / qk) * static_cast<size_t>(qmm::block_bytes(ggml_type));
@@ -319,8 +326,9 @@ int qmm_rope(const void* x_in, void* x_out, int seq_len, int num_heads, int head
              int neox, void* stream) {
     if (seq_len < 0 || num_heads < 0 || pos_offset < 0)
         return fail(QMM_ERR_INVALID_ARGUMENT, "seq_len, num_heads and pos_offset must be non-negative.");
-    if (head_dim <= 0 || head_dim % 2 != 0 || head_dim > 256)
-        return fail(QMM_ERR_INVALID_ARGUMENT, "head_dim must be even and in (0, 256] for rope.");
+    if (head_dim <= 0 || head_dim % 2 != 0)
+        return fail(QMM_ERR_INVALID_ARGUMENT, "head_dim must be a positive even integer for RoPE.");
+    if (head_dim > 256) return fail(QMM_ERR_INVALID_ARGUMENT, "head_dim must be at most 256 for RoPE.");
     if (seq_len > 0 && num_heads > 0 && (!x_in || !x_out)) return fail(QMM_ERR_INVALID_ARGUMENT, "x_in and x_out must be non-null.");
     hipError_t e = qmm::launch_rope(x_in, x_out, num_heads, nullptr, nullptr, nullptr, nullptr, 0, seq_len, head_dim,
                                     pos_offset, freq_base, neox != 0, static_cast<hipStream_t>(stream));
@@ -386,8 +394,8 @@ int qmm_forward_layer(const qmm_layer_config* cfg, const qmm_layer_weights* w, c
         return fail(QMM_ERR_INVALID_ARGUMENT, "norm weights must be QMM_DTYPE_F16 or QMM_DTYPE_F32.");
     const int types[7] = {w->wq_type, w->wk_type, w->wv_type, w->wo_type, w->wgate_type, w->wup_type, w->wdown_type};
     for (int t : types)
-        if (!known_type(t))
-            return fail(QMM_ERR_UNSUPPORTED, "projection weights must be Q4_0, Q8_0, Q4_K or Q6_K (type " + std::to_string(t) + ").");
+        if (!gemm_type(t))
+            return fail(QMM_ERR_UNSUPPORTED, "projection weights must be F16, Q4_0, Q8_0, Q4_K or Q6_K (type " + std::to_string(t) + ").");
     return layer_status(qmm::forward_layer(*cfg, *w, x_in, x_out, layer_idx, seq_len, pos_offset,
                                            static_cast<hipStream_t>(stream)));
 }
@@ -478,6 +486,7 @@ int qmm_release_workspace(void) {
     {
         hipError_t le = qmm::release_layer_workspaces();
         if (le != hipSuccess) return hip_fail(le, "releasing the layer workspaces");
+        if ((le = qmm::release_host_staging()) != hipSuccess) return hip_fail(le, "releasing the host staging buffer");
     }
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     int cur = 0;

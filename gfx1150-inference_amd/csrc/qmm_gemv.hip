@@ -343,6 +343,47 @@ struct GQ40 {
     }
 };
 
+// F16 (dense fp16 rows, the operand of the reference's matmul_nt): lane slot = 64 consecutive
+// weights, eight 16-byte loads.  No scales: the dot products are the result (mac_window takes
+// the dense branch).  Needs K % 16 == 0, so that a 16-value activation staging item and a
+// 16-byte weight chunk are either wholly inside K or wholly outside it; chunks outside read
+// the window's first bytes (a valid address) and meet zero activations.
+struct GF16 {
+    static constexpr int kType = QMM_TYPE_F16;
+    static constexpr int kQK = 8;                      // row bytes = K / 8 * 16 = 2K
+    static constexpr int kBlockBytes = 16;
+    static constexpr int kWinBytes = 2 * kGemvWindow;  // 8192
+    static constexpr int kG = 1;
+    static constexpr bool kAligned = false;
+    struct Raw {
+        u32x4 w[kChunks];
+    };
+    __device__ static int xk(int lane, int cj) { return 64 * lane + 8 * cj; }
+    __device__ static bool group_valid(int lane, int, int kwin_valid) { return 64 * lane < kwin_valid; }
+    __device__ static Raw load(const uint8_t* win, int lane, int kwin_valid) {
+        Raw r;
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c) {
+            const int k = 64 * lane + 8 * c;
+            r.w[c] = ldg16(win + (k < kwin_valid ? 2 * k : 0));
+        }
+        return r;
+    }
+    // dwords (w0,w1), (w2,w3), (w4,w5), (w6,w7) -> pairs (w0,w2), (w1,w3), (w4,w6), (w5,w7), the
+    // order of the staged activation pairs
+    __device__ static void chunk_codes(const Raw& r, int cj, const Consts&, uint32_t out[4]) {
+        const u32x4& d = r.w[cj];
+        out[0] = __builtin_amdgcn_perm(d.y, d.x, 0x05040100u);
+        out[1] = __builtin_amdgcn_perm(d.y, d.x, 0x07060302u);
+        out[2] = __builtin_amdgcn_perm(d.w, d.z, 0x05040100u);
+        out[3] = __builtin_amdgcn_perm(d.w, d.z, 0x07060302u);
+    }
+    __device__ static void group_scales(const Raw&, int, bool, float a[kG], float B[kG]) {
+        a[0] = 1.0f;
+        B[0] = 0.0f;
+    }
+};
+
 // ------------------------------------------------------------------------------------------
 // Activation staging: chunk cj of lane l holds fp16 pairs (x0,x2), (x1,x3), (x4,x6), (x5,x7)
 // of the 8 activations at window k = F::xk(l, cj); xsum[l][q] = sum of the 16 fp16 values of
@@ -450,6 +491,30 @@ __device__ __forceinline__ void store_out<__half>(__half* p, float v) {
 template <class F, int MR, int YT, bool FULL>
 __device__ __forceinline__ void mac_window(const typename F::Raw (&cur)[YT], int nslots, int slot, int lane, int kv,
                                            const Consts& KC, float (&acc)[MR][YT]) {
+    if constexpr (F::kType == QMM_TYPE_F16) {
+        // dense weights: no group scales; activations outside K are staged as zeros
+#pragma unroll
+        for (int cj = 0; cj < kChunks; ++cj) {
+            u32x4 xp[MR];
+#pragma unroll
+            for (int m = 0; m < MR; ++m) xp[m] = gemv_lds[x_index(slot, m, MR, cj, lane)];
+#pragma unroll
+            for (int y = 0; y < YT; ++y) {
+                uint32_t w[4];
+                F::chunk_codes(cur[y], cj, KC, w);
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    float s = acc[m][y];
+                    s = dot2(xp[m].x, w[0], s);
+                    s = dot2(xp[m].y, w[1], s);
+                    s = dot2(xp[m].z, w[2], s);
+                    s = dot2(xp[m].w, w[3], s);
+                    acc[m][y] = s;
+                }
+            }
+        }
+        return;
+    }
     constexpr int G = F::kG;
     constexpr int CPG = kChunks / G;  // chunks per group
     float a[YT][G], B[YT][G];
@@ -776,22 +841,32 @@ void gemv_fallback_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ 
     const int n = blockIdx.x * 4 + threadIdx.x / 64;
     const int m = blockIdx.y;
     if (n >= N || m >= M) return;
-    const int qk = (T == QMM_TYPE_Q4_0 || T == QMM_TYPE_Q8_0) ? 32 : 256;
-    const int bb = T == QMM_TYPE_Q4_0 ? kBytesQ4_0 : T == QMM_TYPE_Q8_0 ? kBytesQ8_0
-                 : T == QMM_TYPE_Q4_K ? kBytesQ4_K : kBytesQ6_K;
-    const uint8_t* row = W + static_cast<size_t>(n) * (K / qk) * bb;
     const TA* x = A + static_cast<size_t>(m) * K;
-    const int groups = K / 32;
     float acc = 0.0f;
-    for (int g = lane; g < groups; g += 64) {
-        float w[32];
-        group_weights_bytewise<T>(row, g, w);
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
+    if constexpr (T == QMM_TYPE_F16) {  // dense fp16 rows, any K
+        const uint8_t* row = W + static_cast<size_t>(n) * K * 2;
+        for (int k = lane; k < K; k += 64) {
             float xv;
-            if constexpr (sizeof(TA) == 4) xv = x[32 * g + i];
-            else xv = __half2float(x[32 * g + i]);
-            acc = __fmaf_rn(xv, w[i], acc);
+            if constexpr (sizeof(TA) == 4) xv = x[k];
+            else xv = __half2float(x[k]);
+            acc = __fmaf_rn(xv, half_bits_to_float(row[2 * k] | (row[2 * k + 1] << 8)), acc);
+        }
+    } else {
+        const int qk = (T == QMM_TYPE_Q4_0 || T == QMM_TYPE_Q8_0) ? 32 : 256;
+        const int bb = T == QMM_TYPE_Q4_0 ? kBytesQ4_0 : T == QMM_TYPE_Q8_0 ? kBytesQ8_0
+                     : T == QMM_TYPE_Q4_K ? kBytesQ4_K : kBytesQ6_K;
+        const uint8_t* row = W + static_cast<size_t>(n) * (K / qk) * bb;
+        const int groups = K / 32;
+        for (int g = lane; g < groups; g += 64) {
+            float w[32];
+            group_weights_bytewise<T>(row, g, w);
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                float xv;
+                if constexpr (sizeof(TA) == 4) xv = x[32 * g + i];
+                else xv = __half2float(x[32 * g + i]);
+                acc = __fmaf_rn(xv, w[i], acc);
+            }
         }
     }
     acc = wave_sum_to_lane63(acc);
@@ -955,7 +1030,7 @@ hipError_t launch_fallback(const void* A, const void* W, void* C, int M, int N, 
 }
 
 // Fast-path eligibility of a weight pointer: Q4_K headers are read as 16-byte vectors, the other
-// formats need 2-byte alignment (fp16 scales).
+// formats need 2-byte alignment (fp16 scales or values).
 bool fast_weights(int t, const void* W) {
     const uintptr_t wa = reinterpret_cast<uintptr_t>(W);
     return t == QMM_TYPE_Q4_K ? (wa & 15u) == 0 : (wa & 1u) == 0;
@@ -965,7 +1040,7 @@ template <typename TA, typename TC>
 hipError_t dispatch_types(int t, const void* A, const Seg* segs, int nseg, int M, int K, hipStream_t stream) {
     const bool a_ok = (reinterpret_cast<uintptr_t>(A) & (sizeof(TA) - 1)) == 0;
     const bool a_vec = (reinterpret_cast<uintptr_t>(A) & 15u) == 0;
-    bool fast = a_ok;
+    bool fast = a_ok && (t != QMM_TYPE_F16 || K % 16 == 0);
     for (int j = 0; j < nseg; ++j) fast = fast && fast_weights(t, segs[j].W);
     if (!fast) {
         if (nseg != 1) return hipErrorNotSupported;
@@ -977,6 +1052,7 @@ hipError_t dispatch_types(int t, const void* A, const Seg* segs, int nseg, int M
             case QMM_TYPE_Q6_K: return launch_fallback<QMM_TYPE_Q6_K, TA, TC>(A, W, C, M, N, K, stream);
             case QMM_TYPE_Q8_0: return launch_fallback<QMM_TYPE_Q8_0, TA, TC>(A, W, C, M, N, K, stream);
             case QMM_TYPE_Q4_0: return launch_fallback<QMM_TYPE_Q4_0, TA, TC>(A, W, C, M, N, K, stream);
+            case QMM_TYPE_F16: return launch_fallback<QMM_TYPE_F16, TA, TC>(A, W, C, M, N, K, stream);
             default: return hipErrorInvalidValue;
         }
     }
@@ -985,6 +1061,7 @@ hipError_t dispatch_types(int t, const void* A, const Seg* segs, int nseg, int M
         case QMM_TYPE_Q6_K: return dispatch_fast<GQ6K, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
         case QMM_TYPE_Q8_0: return dispatch_fast<GQ80, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
         case QMM_TYPE_Q4_0: return dispatch_fast<GQ40, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
+        case QMM_TYPE_F16: return dispatch_fast<GF16, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
         default: return hipErrorInvalidValue;
     }
 }

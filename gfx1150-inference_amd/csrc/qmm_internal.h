@@ -17,10 +17,12 @@ constexpr int kQK4_0 = 32, kBytesQ4_0 = 18;
 constexpr int kQK8_0 = 32, kBytesQ8_0 = 34;
 constexpr int kQK_K = 256, kBytesQ4_K = 144, kBytesQ6_K = 210;
 
-// Every GEMV wave walks K in windows of 2048 weights: 64 lanes x 32-weight slots.
-constexpr int kWave = 64;
-constexpr int kWindow = 2048;
-constexpr int kSlot = 32;
+// Sets the calling thread's qmm_last_error() text and returns `code` (for entry points defined
+// outside the file that owns the error state).
+int set_last_error(int code, const std::string& msg);
+
+// Frees the host-pointer entry points' staging buffers (after synchronizing each device).
+hipError_t release_host_staging();
 
 // M below this runs the GEMV family (bit-identical per row for every M);
 // M at or above it runs the MFMA prefill GEMM.
@@ -32,6 +34,7 @@ inline int block_elems(int t) {
         case QMM_TYPE_Q8_0: return kQK8_0;
         case QMM_TYPE_Q4_K: return kQK_K;
         case QMM_TYPE_Q6_K: return kQK_K;
+        case QMM_TYPE_F16: return 1;
         default: return 0;
     }
 }
@@ -42,6 +45,7 @@ inline int block_bytes(int t) {
         case QMM_TYPE_Q8_0: return kBytesQ8_0;
         case QMM_TYPE_Q4_K: return kBytesQ4_K;
         case QMM_TYPE_Q6_K: return kBytesQ6_K;
+        case QMM_TYPE_F16: return 2;
         default: return 0;
     }
 }

@@ -320,6 +320,44 @@ struct PQ40 {
     }
 };
 
+// F16 (dense fp16 rows, the operand of the reference's matmul_nt): a lane loads the 8 weights
+// of each of its sub-steps straight into the fragment (natural k order, no conversion).  Needs
+// K % 8 == 0: a chunk is wholly inside K or wholly outside it; one outside reads the row's first
+// bytes (a valid address) and is zeroed in scales(), when its sub-step comes.
+template <int H>
+struct PF16 {
+    static constexpr int kQK = 8, kBytes = 16;  // row bytes = K / 8 * 16 = 2K
+    struct Raw { u32x4p w[H][4]; };
+    struct Sc { uint32_t keep[4]; };
+    __device__ static constexpr int off(int U, int S, int h) { return 64 * U + 32 * (S >> 1) + 16 * h + 8 * (S & 1); }
+    __device__ static Raw load(const uint8_t* row, int k0, int h, int kv) {
+        Raw r;
+#pragma unroll
+        for (int U = 0; U < H; ++U)
+#pragma unroll
+            for (int S = 0; S < 4; ++S) {
+                const int o = off(U, S, h);
+                r.w[U][S] = ld16(row + 2 * static_cast<size_t>(o < kv ? k0 + o : 0));
+            }
+        return r;
+    }
+    template <int U>
+    __device__ static Sc scales(const Raw&, int, int h, int kv) {
+        Sc s;
+#pragma unroll
+        for (int S = 0; S < 4; ++S) s.keep[S] = off(U, S, h) < kv ? 0xFFFFFFFFu : 0u;
+        return s;
+    }
+    template <int U, int S>
+    __device__ static void frag(const Raw& r, const Sc& sc, int, uint32_t f[4]) {
+        const u32x4p w = r.w[U][S];
+        f[0] = w.x & sc.keep[S];
+        f[1] = w.y & sc.keep[S];
+        f[2] = w.z & sc.keep[S];
+        f[3] = w.w & sc.keep[S];
+    }
+};
+
 // Output segments of one launch: consecutive weight matrices that multiply the same activations
 // (q/k/v, gate/up).  Their n-tiles are concatenated; tile_end[s] is the cumulative n-tile count
 // through segment s (INT_MAX for unused entries), part_off[s] the offset of segment s's split-K
@@ -1000,6 +1038,7 @@ hipError_t dispatch_p(int t, const void* A, const PfSeg* segs, int nseg, int M, 
         case QMM_TYPE_Q6_K: return launch_family<PQ6K, TA, TC>(A, segs, nseg, M, K, stream);
         case QMM_TYPE_Q8_0: return launch_family<PQ80, TA, TC>(A, segs, nseg, M, K, stream);
         case QMM_TYPE_Q4_0: return launch_family<PQ40, TA, TC>(A, segs, nseg, M, K, stream);
+        case QMM_TYPE_F16: return launch_family<PF16, TA, TC>(A, segs, nseg, M, K, stream);
         default: return hipErrorInvalidValue;
     }
 }
@@ -1020,10 +1059,11 @@ bool gemm_prefill_supported(int ggml_type, int a_dtype, int c_dtype, int M, int 
                             const void*) {
     (void)a_dtype; (void)c_dtype;
     // Q4_K headers and qs pieces are read with 16-byte aligned loads; other formats need 2-byte
-    // alignment (fp16 scales).
+    // alignment (fp16 scales or values); F16 rows are read in 8-value chunks.
     const uintptr_t wa = reinterpret_cast<uintptr_t>(W);
     if (ggml_type == QMM_TYPE_Q4_K && (wa & 15u) != 0) return false;
     if ((wa & 1u) != 0) return false;
+    if (ggml_type == QMM_TYPE_F16 && K % 8 != 0) return false;
     return M > 0 && N > 0 && K > 0;
 }
 

@@ -24,13 +24,12 @@ _REPO_DIR = os.path.dirname(_PKG_DIR)
 LIB_PATH = os.path.join(_PKG_DIR, "libqmm_gfx950.so")
 HEADER_PATH = os.path.join(_REPO_DIR, "include", "qmm.h")
 
-GGML_F16 = 1
+GGML_F32 = 0   # token-embedding tables only
+GGML_F16 = 1   # dense fp16 rows: GEMM weights (matmul_nt) and token-embedding tables
 GGML_Q4_0 = 2
 GGML_Q8_0 = 8
 GGML_Q4_K = 12
 GGML_Q6_K = 14
-GGML_F32 = 0   # token-embedding tables only
-GGML_F16 = 1   # token-embedding tables only
 
 # (block_elems, block_bytes) of every supported type (src/kernels/dequantize.h:6-22).
 BLOCK_INFO = {GGML_Q4_0: (32, 18), GGML_Q8_0: (32, 34), GGML_Q4_K: (256, 144), GGML_Q6_K: (256, 210)}
@@ -116,6 +115,17 @@ _SIGNATURES = {
     "qmm_kv_cache_free": (_i, []),
     "qmm_gqa_attention_cached": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, ctypes.c_float, _i, _vp]),
     "qmm_forward_layer": (_i, [ctypes.POINTER(LayerConfig), ctypes.POINTER(LayerWeights), _vp, _vp, _i, _i, _i, _vp]),
+    "qmm_matmul_fp16_nt_device": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "qmm_matmul_fp16_nt_host": (_i, [_vp, _vp, _vp, _i, _i, _i]),
+    "qmm_matmul_fp16_host": (_i, [_vp, _vp, _vp, _i, _i, _i]),
+    "qmm_rmsnorm_host": (_i, [_vp, _vp, _vp, _i, _i, ctypes.c_float]),
+    "qmm_rmsnorm_residual_host": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, ctypes.c_float]),
+    "qmm_residual_add_host": (_i, [_vp, _vp, _vp, _i64]),
+    "qmm_swiglu_host": (_i, [_vp, _vp, _vp, _i64]),
+    "qmm_rope_host": (_i, [_vp, _vp, _i, _i, _i, _i, ctypes.c_float, _i]),
+    "qmm_gqa_attention_host": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, ctypes.c_float, _i]),
+    "qmm_gqa_attention_cached_host": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, ctypes.c_float, _i]),
+    "qmm_forward_layer_host": (_i, [ctypes.POINTER(LayerConfig), ctypes.POINTER(LayerWeights), _vp, _vp, _i, _i, _i]),
 }
 for _t in ("q4_0", "q8_0", "q4_k", "q6_k"):
     _SIGNATURES[f"qmm_matmul_{_t}_device"] = (_i, [_vp, _vp, _vp, _i, _i, _i, _vp])
@@ -186,13 +196,16 @@ def _dtype_code(t) -> int:
 
 
 def gemm(ggml_type: int, A, W, N: int, K: int, out=None, out_dtype=None, stream=None):
-    """C[M, N] = A[M, K] @ dequant(W)[N, K]^T on the GPU (device tensors, asynchronous)."""
+    """C[M, N] = A[M, K] @ dequant(W)[N, K]^T on the GPU (device tensors, asynchronous).
+    W holds packed GGUF blocks (uint8), or fp16 values [N, K] for GGML_F16 (the matmul_nt
+    operand)."""
     torch = _torch()
     if A.dim() != 2 or A.shape[1] != K or not A.is_contiguous():
         raise ValueError("A must be a contiguous [M, K] device tensor")
-    if W.dtype != torch.uint8 or not W.is_contiguous():
-        raise ValueError("W must be a contiguous uint8 device tensor")
-    if W.numel() < weight_bytes(ggml_type, N, K):
+    dense = ggml_type == GGML_F16
+    if not W.is_contiguous() or W.dtype not in ((torch.uint8, torch.float16) if dense else (torch.uint8,)):
+        raise ValueError("W must be a contiguous uint8 device tensor (or float16 for GGML_F16)")
+    if W.numel() * W.element_size() < weight_bytes(ggml_type, N, K):
         raise ValueError("W is smaller than N * (K / block) * block_bytes")
     M = A.shape[0]
     if out is None:

@@ -35,7 +35,7 @@ enum qmm_status {
 
 enum qmm_ggml_type {
     QMM_TYPE_F32 = 0,   /* token-embedding tables only (qmm_embed) */
-    QMM_TYPE_F16 = 1,   /* token-embedding tables only (qmm_embed) */
+    QMM_TYPE_F16 = 1,   /* dense fp16 rows: GEMM weights (matmul_nt) and embedding tables */
     QMM_TYPE_Q4_0 = 2,
     QMM_TYPE_Q8_0 = 8,
     QMM_TYPE_Q4_K = 12,
@@ -131,6 +131,9 @@ int qmm_matmul_q4_k_device(const void* d_A_fp16, const void* d_B_q4k, void* d_C_
                            int M, int N, int K, void* stream);
 int qmm_matmul_q6_k_device(const void* d_A_fp16, const void* d_B_q6k, void* d_C_fp16,
                            int M, int N, int K, void* stream);
+/* Dense fp16: C[M,N] = A[M,K] @ B_nt[N,K]^T (qmm_gemm with QMM_TYPE_F16).  Replaces
+ * launch_matmul_fp16_nt_device (reference src/kernels/matmul.hip:397-439). */
+int qmm_matmul_fp16_nt_device(const void* d_A, const void* d_B_nt, void* d_C, int M, int N, int K, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * Host-pointer API: the reference's synchronous copy-in / compute / copy-out
@@ -163,16 +166,16 @@ int qmm_dequantize_q6_k_host(const void* h_q6k, void* h_fp16_out, int num_elemen
 
 /* out[m, :] = half(x[m, :] * rsqrt(mean(x[m, :]^2) + eps) * weight); weight_dtype F16 or F32
  * (an F32 weight is rounded to f16 first, as the reference's host does).
- * Replaces launch_rmsnorm_fp16_device (src/kernels/rmsnorm.h:42-50). */
+ * Replaces launch_rmsnorm_fp16_device (src/kernels/rmsnorm.h:44-51). */
 int qmm_rmsnorm(const void* x, const void* weight, int weight_dtype, void* out, int M, int K, float eps,
                 void* stream);
 /* h_out = half(x + residual); norm_out = rmsnorm(h_out).  Replaces
- * launch_rmsnorm_residual_fp16_device (src/kernels/rmsnorm.h:52-61). */
+ * launch_rmsnorm_residual_fp16_device (src/kernels/rmsnorm.h:53-62). */
 int qmm_rmsnorm_residual(const void* x, const void* residual, const void* weight, int weight_dtype, void* h_out,
                          void* norm_out, int M, int K, float eps, void* stream);
-/* out = half(x + residual), n elements.  Replaces launch_residual_add_fp16_device (:63-68). */
+/* out = half(x + residual), n elements.  Replaces launch_residual_add_fp16_device (:64-69). */
 int qmm_residual_add(const void* x, const void* residual, void* out, int64_t n, void* stream);
-/* out = half(silu(gate) * up), n elements.  Replaces launch_swiglu_fp16_device (src/kernels/mlp.h). */
+/* out = half(silu(gate) * up), n elements.  Replaces launch_swiglu_fp16_device (src/kernels/mlp.h:13-18). */
 int qmm_swiglu(const void* gate, const void* up, void* out, int64_t n, void* stream);
 /* RoPE of x [seq_len, num_heads, head_dim] at positions pos_offset + row: pairs (2i, 2i + 1), or
  * (i, i + head_dim / 2) when neox != 0; inv_freq_i = 1 / freq_base^(2i / head_dim).
@@ -206,7 +209,7 @@ typedef struct qmm_layer_config {
 } qmm_layer_config;
 
 /* Device-resident weights of one layer: norms are F16 or F32 vectors (dtype QMM_DTYPE_*);
- * projections are packed GGUF matrices of type 2 / 8 / 12 / 14, N x K as in qmm_gemm. */
+ * projections are F16 rows or packed GGUF matrices (type 1 / 2 / 8 / 12 / 14), N x K as in qmm_gemm. */
 typedef struct qmm_layer_weights {
     const void* attn_norm;
     int attn_norm_dtype;
@@ -236,6 +239,41 @@ typedef struct qmm_layer_weights {
  * state and every weight from the host per call. */
 int qmm_forward_layer(const qmm_layer_config* cfg, const qmm_layer_weights* w, const void* x_in, void* x_out,
                       int layer_idx, int seq_len, int pos_offset, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Host-pointer forms of the dense matmuls and layer operations: the reference's synchronous
+ * launchers (operands copied in, result copied out, null stream).  fp16 throughout; the KV
+ * pool is the device pool above.
+ * --------------------------------------------------------------------------------- */
+
+/* C[M,N] = A[M,K] @ B_nt[N,K]^T.  Replaces launch_matmul_fp16_nt (src/kernels/matmul.hip:441-463). */
+int qmm_matmul_fp16_nt_host(const void* h_A, const void* h_B_nt, void* h_C, int M, int N, int K);
+/* C[M,N] = A[M,K] @ B[K,N] (B transposed on the device, then as above).  Replaces
+ * launch_matmul_fp16 (src/kernels/matmul.hip:340-395). */
+int qmm_matmul_fp16_host(const void* h_A, const void* h_B, void* h_C, int M, int N, int K);
+/* Replace launch_rmsnorm_fp16, launch_rmsnorm_residual_fp16, launch_residual_add_fp16
+ * (src/kernels/rmsnorm.h:10-42). */
+int qmm_rmsnorm_host(const void* h_x, const void* h_weight, void* h_out, int M, int K, float eps);
+int qmm_rmsnorm_residual_host(const void* h_x, const void* h_residual, const void* h_weight, void* h_h_out,
+                              void* h_norm_out, int M, int K, float eps);
+int qmm_residual_add_host(const void* h_x, const void* h_residual, void* h_out, int64_t num_elements);
+/* Replaces launch_swiglu_fp16 (src/kernels/mlp.h:6-11). */
+int qmm_swiglu_host(const void* h_gate, const void* h_up, void* h_out, int64_t num_elements);
+/* Replaces launch_rope_fp16 (src/kernels/rope.h:10-19). */
+int qmm_rope_host(const void* h_in, void* h_out, int seq_len, int num_heads, int head_dim, int pos_offset,
+                  float freq_base, int neox);
+/* Replaces launch_gqa_attention_fp16 (src/kernels/attention.hip:228-284). */
+int qmm_gqa_attention_host(const void* h_Q, const void* h_K, const void* h_V, void* h_out, int q_len, int kv_len,
+                           int num_heads, int num_kv_heads, int head_dim, int start_pos, float scale, int causal);
+/* Replaces launch_gqa_attention_cached_fp16 (src/kernels/attention.hip:302-374). */
+int qmm_gqa_attention_cached_host(const void* h_Q, const void* h_K_new, const void* h_V_new, void* h_out, int layer_idx,
+                                  int q_len, int start_pos, int num_heads, int num_kv_heads, int head_dim, float scale,
+                                  int causal);
+/* qmm_forward_layer with host activations and host weights (all copied to the device per call,
+ * as the reference does).  Replaces launch_forward_layer_cached_fp16
+ * (src/kernels/attention.hip:603-695). */
+int qmm_forward_layer_host(const qmm_layer_config* cfg, const qmm_layer_weights* w, const void* h_x_in, void* h_x_out,
+                           int layer_idx, int seq_len, int pos_offset);
 
 /* One byte range of a file and its destination. */
 typedef struct qmm_file_range {
