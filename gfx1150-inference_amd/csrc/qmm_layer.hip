@@ -468,6 +468,208 @@ hipError_t layer_workspace(hipStream_t stream, size_t bytes, char** out) {
     return hipSuccess;
 }
 
+// ---- prefill attention on the matrix cores --------------------------------------------------
+// Flash-attention form for many query rows.  A workgroup of 4 waves owns 128 query rows: the
+// 128 / G positions of a position tile times the G query heads of one KV head, which share every
+// K and V row.  It walks the keys its rows can see in tiles of 64, staged through LDS
+// (double-buffered, one barrier per tile):
+//   * S = K Q^T on v_mfma_f32_32x32x16_f16.  A wave's 32 rows x 64 keys are two 32 x 32 tiles; K
+//     fragments come from LDS, Q fragments stay in registers for the whole loop.  In an S tile a
+//     lane holds one query row (lane mod 32) and 16 of the 32 keys, so the row's softmax
+//     statistics need one exchange with the partner lane (lane ^ 32).
+//   * fp32 online softmax in base 2 (scores multiplied by scale * log2 e).
+//   * O^T += V^T P^T on the same instruction.  P goes from the S registers into the B fragment
+//     without leaving the lane: the k order of each 16-key block is the order the lane holds its
+//     keys in.  V is staged transposed ([dim][key]) so an A fragment is two 8-byte LDS reads.
+// Rows are divided by their softmax sum and rounded to fp16 once.  Position tiles run longest
+// first (causal rows near the end see the most keys); with 8 KV heads the workgroups of one KV
+// head land on one XCD and share its L2.
+constexpr int kFaRows = 128, kFaKeys = 64, kFaThreads = 256;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int D>
+struct FaGeom {
+    static constexpr int kRowK = D + 8;                      // f16 per staged K row (16-byte pad)
+    static constexpr int kRowV = kFaKeys + 4;                // f16 per staged V^T row (8-byte pad)
+    static constexpr int kK = kFaKeys * kRowK;               // f16 per K buffer
+    static constexpr int kV = D * kRowV;                     // f16 per V^T buffer
+    static constexpr int kBuf = kK + kV;
+    static constexpr size_t kLdsBytes = 2 * static_cast<size_t>(kBuf) * sizeof(_Float16);
+    static constexpr int kChunks = D / 8;                    // 16-byte chunks per row
+    static constexpr int kKUnits = kFaKeys * kChunks / kFaThreads;        // K chunks per thread
+    static constexpr int kVUnits = (kFaKeys / 2) * kChunks / kFaThreads;  // V (key pair, chunk) per thread
+    static_assert(kKUnits >= 1 && kVUnits >= 1, "head_dim 64 or 128");
+};
+
+extern __shared__ __align__(16) _Float16 fa_lds[];
+
+template <int D>
+__global__ __launch_bounds__(kFaThreads, 2) void attention_mfma_kernel(
+    const _Float16* __restrict__ Q, const _Float16* __restrict__ Kc, const _Float16* __restrict__ Vc,
+    _Float16* __restrict__ out, int q_len, int kv_len, int heads, int kv_heads, int start_pos, float scale_log2,
+    int causal, int ptiles) {
+    using FG = FaGeom<D>;
+    const int group = heads / kv_heads;
+    const int ppw = kFaRows / group;  // positions per workgroup
+    const int g = static_cast<int>(blockIdx.x % kv_heads);
+    const int pt = ptiles - 1 - static_cast<int>(blockIdx.x / kv_heads);
+    const int p0 = pt * ppw;
+    const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+    const int r = 32 * (tid >> 6) + l32;  // row of the workgroup
+    const int pos = p0 + r / group;
+    const int head = g * group + r % group;
+    const int p_last = min(p0 + ppw, q_len) - 1;
+    const int n_keys = causal ? min(kv_len, start_pos + p_last + 1) : kv_len;
+    const int n_tiles = (n_keys + kFaKeys - 1) / kFaKeys;
+    const int vis_all = causal ? min(kv_len, start_pos + p0 + 1) : kv_len;    // keys every row sees
+    const int row_end = causal ? min(kv_len, start_pos + pos + 1) : kv_len;   // keys this row sees
+    const size_t kv_row = static_cast<size_t>(kv_heads) * D;
+    const _Float16* kbase = Kc + static_cast<size_t>(g) * D;
+    const _Float16* vbase = Vc + static_cast<size_t>(g) * D;
+
+    // Q fragments of row (pos, head): dims 16 db + 8 h .. + 7 (rows past q_len read the last row)
+    f16x8 qf[D / 16];
+    {
+        const _Float16* qrow = Q + (static_cast<size_t>(min(pos, q_len - 1)) * heads + head) * D + 8 * h;
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db) __builtin_memcpy(&qf[db], qrow + 16 * db, 16);
+    }
+
+    // Staging of key tile t: thread units of K (key, chunk) and of V (key pair, chunk); keys past
+    // kv_len read the last key (finite values, masked out of the softmax).
+    u32x4 kr[FG::kKUnits], vr[FG::kVUnits][2];
+    auto load = [&](int t) {
+        const int kb = t * kFaKeys;
+#pragma unroll
+        for (int i = 0; i < FG::kKUnits; ++i) {
+            const int u = tid + kFaThreads * i, key = u / FG::kChunks, c = u % FG::kChunks;
+            const int k = min(kb + key, kv_len - 1);
+            kr[i] = *reinterpret_cast<const u32x4*>(kbase + static_cast<size_t>(k) * kv_row + 8 * c);
+        }
+#pragma unroll
+        for (int i = 0; i < FG::kVUnits; ++i) {
+            const int u = tid + kFaThreads * i, kp = u % (kFaKeys / 2), c = u / (kFaKeys / 2);
+            const int k0 = min(kb + 2 * kp, kv_len - 1), k1 = min(kb + 2 * kp + 1, kv_len - 1);
+            vr[i][0] = *reinterpret_cast<const u32x4*>(vbase + static_cast<size_t>(k0) * kv_row + 8 * c);
+            vr[i][1] = *reinterpret_cast<const u32x4*>(vbase + static_cast<size_t>(k1) * kv_row + 8 * c);
+        }
+    };
+    auto store = [&](int buf) {
+        _Float16* sk = fa_lds + buf * FG::kBuf;
+        _Float16* sv = sk + FG::kK;
+#pragma unroll
+        for (int i = 0; i < FG::kKUnits; ++i) {
+            const int u = tid + kFaThreads * i, key = u / FG::kChunks, c = u % FG::kChunks;
+            *reinterpret_cast<u32x4*>(sk + key * FG::kRowK + 8 * c) = kr[i];
+        }
+#pragma unroll
+        for (int i = 0; i < FG::kVUnits; ++i) {
+            const int u = tid + kFaThreads * i, kp = u % (kFaKeys / 2), c = u / (kFaKeys / 2);
+            // V^T[8c + e][2kp, 2kp + 1] = (V[k0][8c + e], V[k1][8c + e]); dword m of a row chunk
+            // holds dims 2m, 2m + 1
+            uint32_t* col = reinterpret_cast<uint32_t*>(sv + 8 * c * FG::kRowV + 2 * kp);
+            const u32x4 a = vr[i][0], b = vr[i][1];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                col[(2 * m) * (FG::kRowV / 2)] = __builtin_amdgcn_perm(b[m], a[m], 0x05040100u);
+                col[(2 * m + 1) * (FG::kRowV / 2)] = __builtin_amdgcn_perm(b[m], a[m], 0x07060302u);
+            }
+        }
+    };
+
+    f32x16 o[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[dt][v] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int t = 0; t < n_tiles; ++t) {
+        if (t + 1 < n_tiles) load(t + 1);
+        const _Float16* sk = fa_lds + (t & 1) * FG::kBuf;
+        const _Float16* sv = sk + FG::kK;
+        // S^T tiles: register v of tile tt is key 32 tt + 8 (v / 4) + 4 h + v % 4 of the row l32
+        f32x16 s[2];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) s[tt][v] = 0.0f;
+#pragma unroll
+            for (int db = 0; db < D / 16; ++db) {
+                f16x8 kf;
+                __builtin_memcpy(&kf, sk + (32 * tt + l32) * FG::kRowK + 16 * db + 8 * h, 16);
+                s[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[db], s[tt], 0, 0, 0);
+            }
+        }
+        const int kb = t * kFaKeys;
+        const bool full = kb + kFaKeys <= vis_all;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                float x = s[tt][v] * scale_log2;
+                if (!full && kb + 32 * tt + 8 * (v >> 2) + 4 * h + (v & 3) >= row_end) x = -INFINITY;
+                s[tt][v] = x;
+                mx = fmaxf(mx, x);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run, mx);  // finite: key 0 is visible to every row
+        const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+        float sum = 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const float p = __builtin_amdgcn_exp2f(s[tt][v] - m_new);
+                s[tt][v] = p;
+                sum += p;
+            }
+        sum += __shfl_xor(sum, 32, 64);
+        l_run = l_run * corr + sum;
+        m_run = m_new;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) o[dt][v] *= corr;
+        // 16-key block b: lane half h holds keys 16 b + 4 h + (0..3) and 16 b + 8 + 4 h + (0..3)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            f16x8 pf;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) pf[e] = static_cast<_Float16>(s[b >> 1][8 * (b & 1) + e]);
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) {
+                const _Float16* vrow = sv + (32 * dt + l32) * FG::kRowV + 16 * b + 4 * h;
+                f16x8 vf;
+                __builtin_memcpy(&vf, vrow, 8);
+                __builtin_memcpy(reinterpret_cast<char*>(&vf) + 8, vrow + 8, 8);
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[dt], 0, 0, 0);
+            }
+        }
+        if (t + 1 < n_tiles) store((t + 1) & 1);
+        __syncthreads();
+    }
+
+    if (pos < q_len) {
+        const float inv = 1.0f / l_run;
+        _Float16* orow = out + (static_cast<size_t>(pos) * heads + head) * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                _Float16 v4[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v4[i] = static_cast<_Float16>(o[dt][4 * q4 + i] * inv);
+                __builtin_memcpy(orow + 32 * dt + 8 * q4 + 4 * h, v4, 8);
+            }
+    }
+}
+
 int attn_chunks(int kv_len) { return kv_len <= 0 ? 1 : (kv_len + kAttnChunk - 1) / kAttnChunk; }
 
 size_t attn_part_bytes(int q_len, int heads, int head_dim, int kv_len) {
@@ -521,10 +723,52 @@ size_t attention_workspace_bytes(int q_len, int heads, int head_dim, int kv_len)
     return attn_part_bytes(q_len, heads, head_dim, kv_len);
 }
 
+namespace {
+
+// The matrix-core kernel serves head_dim 64 and 128, query groups dividing 128, at least
+// kFaMinRows query positions (fewer rows leave the 32-row MFMA tiles mostly empty) and 16-byte
+// aligned Q / K / V.
+constexpr int kFaMinRows = 16;
+
+template <int D>
+hipError_t launch_attention_mfma(const void* Q, const void* K, const void* V, void* out, int q_len, int kv_len, int heads,
+                                 int kv_heads, int start_pos, float scale, bool causal, hipStream_t stream) {
+    using FG = FaGeom<D>;
+    static std::once_flag once;
+    static hipError_t attr = hipSuccess;
+    std::call_once(once, [] {
+        attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_mfma_kernel<D>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(FG::kLdsBytes));
+    });
+    if (attr != hipSuccess) return attr;
+    const int ppw = kFaRows / (heads / kv_heads);
+    const int ptiles = (q_len + ppw - 1) / ppw;
+    const float scale_log2 = scale * 1.4426950408889634f;
+    hipLaunchKernelGGL((attention_mfma_kernel<D>), dim3(static_cast<unsigned>(ptiles * kv_heads)), dim3(kFaThreads),
+                       FG::kLdsBytes, stream, static_cast<const _Float16*>(Q), static_cast<const _Float16*>(K),
+                       static_cast<const _Float16*>(V), static_cast<_Float16*>(out), q_len, kv_len, heads, kv_heads,
+                       start_pos, scale_log2, causal ? 1 : 0, ptiles);
+    return hipGetLastError();
+}
+
+bool attention_mfma_ok(const void* Q, const void* K, const void* V, int q_len, int kv_len, int heads, int kv_heads,
+                       int head_dim) {
+    const bool aligned = (reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(K) | reinterpret_cast<uintptr_t>(V)) % 16 == 0;
+    const int group = heads / kv_heads;
+    return (head_dim == 64 || head_dim == 128) && kFaRows % group == 0 && q_len >= kFaMinRows && kv_len > 0 && aligned;
+}
+
+}  // namespace
+
 hipError_t launch_attention(const void* Q, const void* K, const void* V, void* out, void* part, int q_len, int kv_len,
                             int heads, int kv_heads, int head_dim, int start_pos, float scale, bool causal,
                             hipStream_t stream) {
     if (q_len <= 0 || heads <= 0) return hipSuccess;
+    if (attention_mfma_ok(Q, K, V, q_len, kv_len, heads, kv_heads, head_dim)) {
+        if (head_dim == 128)
+            return launch_attention_mfma<128>(Q, K, V, out, q_len, kv_len, heads, kv_heads, start_pos, scale, causal, stream);
+        return launch_attention_mfma<64>(Q, K, V, out, q_len, kv_len, heads, kv_heads, start_pos, scale, causal, stream);
+    }
     const int chunks = attn_chunks(kv_len);
     const int64_t waves = static_cast<int64_t>(q_len) * heads * chunks;
     const dim3 grid(static_cast<unsigned>((waves + 3) / 4));

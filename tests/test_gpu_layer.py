@@ -136,6 +136,49 @@ def test_gqa_attention(dev, q_len, kv_len, start, heads, kvh, d):
     assert maxerr(host(out), L.gqa_attention(Q, K, V, start, scale, True)) < 2e-3
 
 
+def _attention(dev, Q, K, V, start, scale, causal):
+    import torch
+    import qmm
+    q_len, heads, d = Q.shape
+    kv_len, kvh, _ = K.shape
+    out = torch.empty((q_len, heads, d), dtype=torch.float16, device=dev)
+    Qd, Kd, Vd = t16(Q, dev), t16(K, dev), t16(V, dev)
+    qmm.check(qmm.lib().qmm_gqa_attention(Qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), out.data_ptr(), q_len, kv_len,
+                                          heads, kvh, d, start, scale, int(causal), stream()))
+    return host(out)
+
+
+# Prefill sizes (>= 16 query rows, head_dim 64 / 128, groups dividing 128) run the matrix-core
+# kernel: position tiles of 128 / G rows, key tiles of 64, causal and key-count tails.
+@pytest.mark.parametrize("q_len,kv_len,start,heads,kvh,d,causal",
+                         [(64, 64, 0, 8, 1, 128, True), (100, 130, 30, 32, 8, 128, True), (17, 17, 0, 4, 4, 64, True),
+                          (200, 200, 0, 16, 2, 64, True), (33, 70, 0, 8, 2, 128, False), (16, 1000, 984, 64, 8, 128, True),
+                          (130, 129, 0, 6, 3, 64, True), (48, 48, 0, 32, 1, 128, True)])
+def test_gqa_attention_prefill_mfma(dev, q_len, kv_len, start, heads, kvh, d, causal):
+    r = np.random.default_rng(70 + q_len + kv_len + d)
+    Q = (r.standard_normal((q_len, heads, d)) * 0.5).astype(np.float16)
+    K = (r.standard_normal((kv_len, kvh, d)) * 0.5).astype(np.float16)
+    V = (r.standard_normal((kv_len, kvh, d)) * 0.5).astype(np.float16)
+    scale = 1.0 / math.sqrt(d)
+    got = _attention(dev, Q, K, V, start, scale, causal)
+    assert maxerr(got, L.gqa_attention(Q, K, V, start, scale, causal)) < 2e-3
+
+
+def test_gqa_attention_prefill_70b_shape(dev):
+    """1023 query rows, 64 query heads over 8 KV heads of 128 (a 70B prefill); sampled rows
+    against the oracle, larger scores (x 1.5) so the softmax is peaked."""
+    q_len, heads, kvh, d = 1023, 64, 8, 128
+    r = np.random.default_rng(99)
+    Q = (r.standard_normal((q_len, heads, d)) * 1.5).astype(np.float16)
+    K = (r.standard_normal((q_len, kvh, d)) * 1.5).astype(np.float16)
+    V = r.standard_normal((q_len, kvh, d)).astype(np.float16)
+    scale = 1.0 / math.sqrt(d)
+    got = _attention(dev, Q, K, V, 0, scale, True)
+    for m in (0, 1, 15, 16, 63, 64, 65, 500, 511, 1000, 1022):
+        want = L.gqa_attention(Q[m:m + 1], K[:m + 1], V[:m + 1], m, scale, True)
+        assert maxerr(got[m:m + 1], want) < 2e-3, m
+
+
 def test_kv_cache_pool_and_cached_attention(dev):
     import torch
     import qmm
