@@ -49,6 +49,15 @@ constexpr int kChunks = 8;          // 8-weight activation chunks per lane slot
 #define QMM_GEMV_NW 8
 #endif
 // Items of weight bytes in flight while one is multiplied (0, 1 or 2).
+#ifndef QMM_GEMV_STREAM
+#define QMM_GEMV_STREAM 1   // streamed-window kernel where its conditions hold
+#endif
+#ifndef QMM_GEMV_F16_STREAM
+#define QMM_GEMV_F16_STREAM 1
+#endif
+#ifndef QMM_GEMV_NS
+#define QMM_GEMV_NS 2       // LDS window slots per wave of the streamed kernel
+#endif
 #ifndef QMM_GEMV_DEPTH
 #define QMM_GEMV_DEPTH 0
 #endif
@@ -121,6 +130,7 @@ struct GQ4K {
     static constexpr int kWinBytes = 16 * kBytesQ4_K;  // 2304
     static constexpr int kG = 2;
     static constexpr bool kAligned = true;
+    static constexpr bool kStream = false;  // lane-slot loads measured faster than the streamed window
     struct Raw {
         u32x4 h, q0, q1;
     };
@@ -184,6 +194,7 @@ struct GQ6K {
     static constexpr int kWinBytes = 16 * kBytesQ6_K;  // 3360
     static constexpr int kG = 4;
     static constexpr bool kAligned = false;
+    static constexpr bool kStream = false;
     struct Raw {
         u32x4 la, lb, qh;
         uint32_t s0, s1, d;
@@ -252,6 +263,7 @@ struct GQ80 {
     static constexpr int kWinBytes = 128 * kBytesQ8_0;  // 4352
     static constexpr int kG = 2;
     static constexpr bool kAligned = false;
+    static constexpr bool kStream = true;  // 34-byte blocks: the streamed window is 12 % faster
     struct Raw {
         u32x4 q[2][2];
         uint32_t d[2];
@@ -300,6 +312,7 @@ struct GQ40 {
     static constexpr int kWinBytes = 128 * kBytesQ4_0;  // 2304
     static constexpr int kG = 4;
     static constexpr bool kAligned = false;
+    static constexpr bool kStream = false;
     struct Raw {
         u32x4 q[2];
         uint32_t d[2];
@@ -355,6 +368,7 @@ struct GF16 {
     static constexpr int kWinBytes = 2 * kGemvWindow;  // 8192
     static constexpr int kG = 1;
     static constexpr bool kAligned = false;
+    static constexpr bool kStream = QMM_GEMV_F16_STREAM != 0;
     struct Raw {
         u32x4 w[kChunks];
     };
@@ -754,6 +768,133 @@ void gemv_resident_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int 
     }
 }
 
+// Streamed-window variant of the resident kernel: a wave copies each item's packed window
+// (kWinBytes contiguous bytes of a row) into a private LDS slot with direct-to-LDS 16-byte
+// loads, lanes on consecutive pieces, so every load instruction reads 1 KiB of contiguous
+// memory; the lane slots are then read from LDS and multiplied exactly as in the resident kernel
+// (same arithmetic, same order: results are bit-identical).  NS slots per wave: NS - 1 items are
+// in flight while one is multiplied.  Needs 16-byte aligned weights and row sizes.
+// Dynamic LDS: the resident kernel's activations, then NW * NS * YT window slots.
+template <class F>
+struct WinSlot {
+    static constexpr int kPieces = (F::kWinBytes + 15) / 16;  // 16-byte pieces of a window
+    static constexpr int kInstr = (kPieces + 63) / 64;        // load instructions per window row
+    static constexpr int kBytes = kPieces * 16;
+};
+
+// 16 bytes at global address g -> LDS at m0 + 16 * lane (m0 = the wave-uniform `lds`).  The
+// compiler does not track these loads: the caller waits for them with an explicit vmcnt.
+__device__ __forceinline__ void win_direct_load16(const void* g, const void* lds) {
+    const uint32_t la = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+    __asm__ volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(la) : "memory", "m0");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <class F, int MR, int YT, int NW, int NS, typename TA, typename TC>
+__global__ __launch_bounds__(64 * NW, QMM_GEMV_MIN_WAVES)
+void gemv_stream_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K, int a_vec, int nrg) {
+    using WS = WinSlot<F>;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int m0 = blockIdx.y * MR;
+    const bool vec = a_vec != 0;
+    const size_t row_bytes = static_cast<size_t>(K / F::kQK) * F::kBlockBytes;
+    const int nwin = (K + kGemvWindow - 1) / kGemvWindow;
+    const int stride = gridDim.x * NW;
+    const Consts KC = make_consts();
+    const int act_u4 = nwin * MR * (kChunks * 64 + 64);  // activation entries (x and sx) of the LDS
+    uint8_t* wslots = reinterpret_cast<uint8_t*>(gemv_lds + act_u4) + static_cast<size_t>(wv) * NS * YT * WS::kBytes;
+
+    // Copies item (g, w) into slot s: YT windows of WS::kPieces pieces (past the wave's last item:
+    // a valid row group is re-read, so every wave issues the same number of loads).
+    auto issue = [&](int g, int w, int slot) {
+        g = min(g, nrg - 1);
+        const SegRef<TC> sr = seg_of(sg, g);
+        const size_t woff = static_cast<size_t>(w) * F::kWinBytes;
+        const int valid = static_cast<int>(min(static_cast<size_t>(F::kWinBytes), row_bytes - woff));
+#pragma unroll
+        for (int y = 0; y < YT; ++y) {
+            const uint8_t* rp = sr.W + static_cast<size_t>(min((g - sr.g0) * YT + y, sr.N - 1)) * row_bytes + woff;
+            uint8_t* dst = wslots + (slot * YT + y) * WS::kBytes;
+#pragma unroll
+            for (int i = 0; i < WS::kInstr; ++i) {
+                const int piece = 64 * i + lane;
+                const int off = 16 * piece < valid ? 16 * piece : 0;
+                if (piece < WS::kPieces) win_direct_load16(rp + off, dst + 1024 * i);
+            }
+        }
+    };
+    auto next = [&](int& g, int& w) {
+        if (++w == nwin) {
+            w = 0;
+            g += stride;
+        }
+    };
+
+    int gc = blockIdx.x * NW + wv, wc = 0;
+    int gl = gc, wl = 0;
+    const bool active = gc < nrg;
+
+    // the first NS - 1 items are requested before the activations are staged
+#pragma unroll
+    for (int j = 0; j < NS - 1; ++j) {
+        issue(gl, wl, j);
+        next(gl, wl);
+    }
+    const int items = nwin * MR * 256;
+    for (int it = tid; it < items; it += 64 * NW) {
+        const int w = it / (MR * 256), item = it - w * (MR * 256);
+        StageItem<F, MR, TA> s2;
+        s2.load(A, M, K, m0, w, item, vec);
+        s2.store(nwin, w, item);
+    }
+    __syncthreads();
+    if (!active) {
+        wait_vmcnt<0>();  // no LDS DMA outstanding when the wave ends
+        return;
+    }
+
+    float acc[MR][YT];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int y = 0; y < YT; ++y) acc[m][y] = 0.0f;
+
+    typedef typename F::Raw Raw;
+    const int total = ((nrg - gc + stride - 1) / stride) * nwin;
+    int slot = 0;
+    for (int i = 0; i < total; ++i) {
+        // request item i + NS - 1 into the slot item i - 1 used (its LDS reads are complete: their
+        // values were consumed), then wait until item i's copies have landed
+        issue(gl, wl, (slot + NS - 1) % NS);
+        next(gl, wl);
+        wait_vmcnt<(NS - 1) * YT * WS::kInstr>();
+        const int kv = min(K - wc * kGemvWindow, kGemvWindow);
+        Raw b[YT];
+#pragma unroll
+        for (int y = 0; y < YT; ++y) b[y] = F::load(wslots + (slot * YT + y) * WS::kBytes, lane, kv);
+        if (kv == kGemvWindow) mac_window<F, MR, YT, true>(b, nwin, wc, lane, kv, KC, acc);
+        else mac_window<F, MR, YT, false>(b, nwin, wc, lane, kv, KC, acc);
+        if (wc == nwin - 1) {
+            const SegRef<TC> sr = seg_of(sg, gc);
+            reduce_store<MR, YT, TC>(acc, sr.C, M, sr.N, m0, (gc - sr.g0) * YT, lane);
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+                for (int y = 0; y < YT; ++y) acc[m][y] = 0.0f;
+        }
+        next(gc, wc);
+        slot = slot + 1 == NS ? 0 : slot + 1;
+    }
+    wait_vmcnt<0>();  // the trailing copies land before the wave ends
+}
+
 // Windowed kernel (activations too large to keep resident): one workgroup owns NW * YT rows;
 // window w + 1's activations are staged into the other of two LDS slots and its weight bytes
 // loaded while window w is multiplied; one barrier per window.  Dynamic LDS: MR * 2 * 9216.
@@ -948,6 +1089,42 @@ hipError_t launch_fast(const void* A, const Seg* segs, int nseg, int M, int K, b
     const int mblocks = (M + MR - 1) / MR;
     const size_t res_lds = static_cast<size_t>(MR) * nwin * kSlotBytes;
     const int threads = 64 * NW;
+#if QMM_GEMV_STREAM
+    if constexpr (F::kStream) {
+        constexpr int NS = QMM_GEMV_NS;
+        const size_t row_bytes = static_cast<size_t>(K / F::kQK) * F::kBlockBytes;
+        const size_t st_lds = res_lds + static_cast<size_t>(NW) * NS * YT * WinSlot<F>::kBytes;
+        bool ok = row_bytes % 16 == 0 && st_lds <= di.max_lds;
+        for (int j = 0; j < nseg; ++j) ok = ok && (reinterpret_cast<uintptr_t>(segs[j].W) & 15u) == 0;
+        if (ok) {
+            const void* kern = reinterpret_cast<const void*>(&gemv_stream_kernel<F, MR, YT, NW, NS, TA, TC>);
+            int occ = 0;
+            if ((e = occupancy(kern, threads, st_lds, occ)) != hipSuccess) return e;
+            GemvSegs<TC> sg;
+            int nrg = 0;
+            for (int j = 0; j < kMaxSegs; ++j) {
+                if (j < nseg) {
+                    sg.W[j] = static_cast<const uint8_t*>(segs[j].W);
+                    sg.C[j] = static_cast<TC*>(segs[j].C);
+                    sg.N[j] = segs[j].N;
+                    nrg += (segs[j].N + YT - 1) / YT;
+                    sg.gend[j] = nrg;
+                } else {
+                    sg.W[j] = sg.W[0];
+                    sg.C[j] = sg.C[0];
+                    sg.N[j] = sg.N[0];
+                    sg.gend[j] = INT_MAX;
+                }
+            }
+            const int need = (nrg + NW - 1) / NW;
+            const int fill = max(1, occ * di.cus / mblocks);
+            const dim3 grid(min(need, fill), mblocks);
+            hipLaunchKernelGGL((gemv_stream_kernel<F, MR, YT, NW, NS, TA, TC>), grid, dim3(threads), st_lds, stream,
+                               static_cast<const TA*>(A), sg, M, K, a_vec ? 1 : 0, nrg);
+            return hipGetLastError();
+        }
+    }
+#endif
     if (res_lds <= di.max_lds) {
         const void* kern = reinterpret_cast<const void*>(&gemv_resident_kernel<F, MR, YT, NW, TA, TC>);
         int occ = 0;
