@@ -57,6 +57,13 @@ int check_gemm_args(int t, const void* A, int a_dtype, const void* W, void* C, i
     if (M < 0 || N < 0) return fail(QMM_ERR_INVALID_ARGUMENT, "M and N must be non-negative.");
     if (M > 0 && N > 0 && (A == nullptr || W == nullptr || C == nullptr))
         return fail(QMM_ERR_INVALID_ARGUMENT, "A, W and C must be non-null device pointers.");
+    if (M > 0 && N > 0) {
+        // every workgroup reads all of A while others write C: an output over the input would race
+        const uintptr_t a0 = reinterpret_cast<uintptr_t>(A), c0 = reinterpret_cast<uintptr_t>(C);
+        const uintptr_t a1 = a0 + static_cast<size_t>(M) * K * (a_dtype == QMM_DTYPE_F32 ? 4 : 2);
+        const uintptr_t c1 = c0 + static_cast<size_t>(M) * N * (c_dtype == QMM_DTYPE_F32 ? 4 : 2);
+        if (a0 < c1 && c0 < a1) return fail(QMM_ERR_INVALID_ARGUMENT, "C must not overlap A (in-place GEMM is not supported).");
+    }
     return QMM_OK;
 }
 

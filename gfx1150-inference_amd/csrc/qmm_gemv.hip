@@ -591,9 +591,109 @@ __device__ __forceinline__ void mac_window(const typename F::Raw (&cur)[YT], int
     }
 }
 
+// Staging with a prologue (GemvFuse kind 1 or 2; one fp16 activation row): every load of the
+// thread's items (16 consecutive activations each, at most kFuseOwn) is issued first (A, R and
+// the norm weights, 16-byte vectors), then v is formed, v^2 is reduced over the workgroup for the
+// norm kinds, and the staged fp16 pairs and sums are written as StageItem::store does.
+constexpr int kFuseOwn = 2;
+// The folded staging exists for one fp16 activation row (decode) and where its registers fit
+// beside the kernel's own (1024-thread workgroups have 128 per lane: one row per item there,
+// and not for F16); other instantiations keep their register budget.
+template <class F, int MR, int YT, int NW, typename TA>
+constexpr bool kFoldable = MR == 1 && std::is_same<TA, __half>::value && (NW <= 8 || (YT == 1 && F::kType != QMM_TYPE_F16));
+typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
+
+template <class F, int MR, int NW>
+__device__ __forceinline__ void stage_fused(const __half* A, const GemvFuse& fz, int M, int K, int m0, int nwin, int tid) {
+    static_assert(MR == 1, "one activation row");
+    __shared__ float red[NW];
+    const int items = nwin * 256;
+    const _Float16* a16 = reinterpret_cast<const _Float16*>(A) + static_cast<size_t>(m0) * K;
+    const _Float16* r16 = static_cast<const _Float16*>(fz.R) + static_cast<size_t>(m0) * K;
+    const bool two = fz.kind == 2;
+    h16x8 av[kFuseOwn][2], rv[kFuseOwn][2], wv[kFuseOwn][2];
+    int kk[kFuseOwn];
+#pragma unroll
+    for (int j = 0; j < kFuseOwn; ++j) {
+        const int it = min(tid + 64 * NW * j, items - 1);
+        const int w = it >> 8, q = (it >> 6) & 3, ln = it & 63;
+        const int k = w * kGemvWindow + F::xk(ln, 2 * q);
+        kk[j] = k;
+        const int off = m0 < M && k < K ? k : 0;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            av[j][hh] = *reinterpret_cast<const h16x8*>(a16 + off + 8 * hh);
+            if (two) rv[j][hh] = *reinterpret_cast<const h16x8*>(r16 + off + 8 * hh);
+            {
+                if (fz.w_f32) {  // an F32 norm weight is rounded to f16 first, as the reference's host does
+                    const float* wf = static_cast<const float*>(fz.w) + off + 8 * hh;
+                    const float4 lo = *reinterpret_cast<const float4*>(wf), hi = *reinterpret_cast<const float4*>(wf + 4);
+                    wv[j][hh] = h16x8{static_cast<_Float16>(lo.x), static_cast<_Float16>(lo.y), static_cast<_Float16>(lo.z),
+                                      static_cast<_Float16>(lo.w), static_cast<_Float16>(hi.x), static_cast<_Float16>(hi.y),
+                                      static_cast<_Float16>(hi.z), static_cast<_Float16>(hi.w)};
+                } else {
+                    wv[j][hh] = *reinterpret_cast<const h16x8*>(static_cast<const _Float16*>(fz.w) + off + 8 * hh);
+                }
+            }
+        }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kFuseOwn; ++j) {
+        const bool ok = tid + 64 * NW * j < items && m0 < M && kk[j] < K;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            h16x8 v = av[j][hh];
+            if (two) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    v[e] = static_cast<_Float16>(static_cast<float>(v[e]) + static_cast<float>(rv[j][hh][e]));
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                v[e] = ok ? v[e] : static_cast<_Float16>(0.0f);
+                const float f = static_cast<float>(v[e]);
+                ss += f * f;
+            }
+            av[j][hh] = v;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) t += red[i];
+    const float scale = rsqrtf(t / static_cast<float>(K) + fz.eps);
+#pragma unroll
+    for (int j = 0; j < kFuseOwn; ++j) {
+        const int it = tid + 64 * NW * j;
+        if (it < items) {
+            uint32_t wd[8];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                h16x8 v = av[j][hh];
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    v[e] = static_cast<_Float16>(static_cast<float>(v[e]) * scale * static_cast<float>(wv[j][hh][e]));
+                __builtin_memcpy(&wd[4 * hh], &v, 16);
+            }
+            StageItem<F, MR, __half> st;
+            // dwords (x0,x1), (x2,x3) -> (x0,x2), (x1,x3), the staged pair order
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                st.h[2 * c] = __builtin_amdgcn_perm(wd[2 * c + 1], wd[2 * c], 0x05040100u);
+                st.h[2 * c + 1] = __builtin_amdgcn_perm(wd[2 * c + 1], wd[2 * c], 0x07060302u);
+            }
+            st.store(nwin, it >> 8, it & 255);
+        }
+    }
+}
+
 template <int MR, int YT, typename TC>
 __device__ __forceinline__ void reduce_store(float (&acc)[MR][YT], TC* __restrict__ C, int M, int N, int m0, int row0,
-                                             int lane) {
+                                             int lane, const GemvFuse& fz) {
     float v[MR][YT];
 #pragma unroll
     for (int m = 0; m < MR; ++m)
@@ -604,7 +704,19 @@ __device__ __forceinline__ void reduce_store(float (&acc)[MR][YT], TC* __restric
         for (int m = 0; m < MR; ++m)
 #pragma unroll
             for (int y = 0; y < YT; ++y)
-                if (m0 + m < M && row0 + y < N) store_out<TC>(C + static_cast<size_t>(m0 + m) * N + row0 + y, v[m][y]);
+                if (m0 + m < M && row0 + y < N) {
+                    const size_t o = static_cast<size_t>(m0 + m) * N + row0 + y;
+                    float r = v[m][y];
+                    if constexpr (sizeof(TC) == 2) {
+                        if (fz.ea != nullptr) {  // residual: half(half(ea + eb) + half(acc))
+                            const float h = static_cast<float>(static_cast<_Float16>(
+                                static_cast<float>(static_cast<const _Float16*>(fz.ea)[o]) +
+                                static_cast<float>(static_cast<const _Float16*>(fz.eb)[o])));
+                            r = h + static_cast<float>(static_cast<_Float16>(r));
+                        }
+                    }
+                    store_out<TC>(C + o, r);
+                }
     }
 }
 
@@ -644,7 +756,7 @@ __device__ __forceinline__ SegRef<TC> seg_of(const GemvSegs<TC>& sg, int g) {
 // Dynamic LDS: MR * nwin * 9216 bytes.
 template <class F, int MR, int YT, int NW, typename TA, typename TC>
 __global__ __launch_bounds__(64 * NW, QMM_GEMV_MIN_WAVES)
-void gemv_resident_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K, int a_vec, int nrg) {
+void gemv_resident_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K, int a_vec, int nrg, GemvFuse fz) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -683,32 +795,42 @@ void gemv_resident_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int 
     // then the LDS writes; the weight loads stay in flight through the barrier.
     constexpr int kFirst = 2;  // activation items per thread issued before the weight loads
     const int items = nwin * MR * 256;
-    StageItem<F, MR, TA> st[kFirst];
-#pragma unroll
-    for (int j = 0; j < kFirst; ++j) {
-        const int it = min(tid + 64 * NW * j, items - 1);  // loads always issued (static counts)
-        const int w = it / (MR * 256);
-        st[j].load(A, M, K, m0, w, it - w * (MR * 256), vec);
-    }
     constexpr int PD = QMM_GEMV_DEPTH;
     Raw b0[YT], b1[YT], b2[YT];
-    // issued by every wave (inactive waves re-read a valid row group) to keep counts static
-    load_item(gl, wl, b0); next(gl, wl);
-    if constexpr (PD >= 1) { load_item(gl, wl, b1); next(gl, wl); }
-    if constexpr (PD >= 2) { load_item(gl, wl, b2); next(gl, wl); }
+    bool fused = false;
+    if constexpr (kFoldable<F, MR, YT, NW, TA>) fused = fz.kind != 0;
+    if (fused) {
+        // weight bytes first, then the activations with their prologue
+        load_item(gl, wl, b0); next(gl, wl);
+        if constexpr (PD >= 1) { load_item(gl, wl, b1); next(gl, wl); }
+        if constexpr (PD >= 2) { load_item(gl, wl, b2); next(gl, wl); }
+        if constexpr (kFoldable<F, MR, YT, NW, TA>) stage_fused<F, MR, NW>(A, fz, M, K, m0, nwin, tid);
+    } else {
+        StageItem<F, MR, TA> st[kFirst];
 #pragma unroll
-    for (int j = 0; j < kFirst; ++j) {
-        const int it = tid + 64 * NW * j;
-        if (it < items) {
+        for (int j = 0; j < kFirst; ++j) {
+            const int it = min(tid + 64 * NW * j, items - 1);  // loads always issued (static counts)
             const int w = it / (MR * 256);
-            st[j].store(nwin, w, it - w * (MR * 256));
+            st[j].load(A, M, K, m0, w, it - w * (MR * 256), vec);
         }
-    }
-    for (int it = tid + 64 * NW * kFirst; it < items; it += 64 * NW) {
-        const int w = it / (MR * 256), item = it - w * (MR * 256);
-        StageItem<F, MR, TA> s2;
-        s2.load(A, M, K, m0, w, item, vec);
-        s2.store(nwin, w, item);
+        // issued by every wave (inactive waves re-read a valid row group) to keep counts static
+        load_item(gl, wl, b0); next(gl, wl);
+        if constexpr (PD >= 1) { load_item(gl, wl, b1); next(gl, wl); }
+        if constexpr (PD >= 2) { load_item(gl, wl, b2); next(gl, wl); }
+#pragma unroll
+        for (int j = 0; j < kFirst; ++j) {
+            const int it = tid + 64 * NW * j;
+            if (it < items) {
+                const int w = it / (MR * 256);
+                st[j].store(nwin, w, it - w * (MR * 256));
+            }
+        }
+        for (int it = tid + 64 * NW * kFirst; it < items; it += 64 * NW) {
+            const int w = it / (MR * 256), item = it - w * (MR * 256);
+            StageItem<F, MR, TA> s2;
+            s2.load(A, M, K, m0, w, item, vec);
+            s2.store(nwin, w, item);
+        }
     }
     __syncthreads();
     if (!active) return;
@@ -725,7 +847,7 @@ void gemv_resident_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int 
         else mac_window<F, MR, YT, false>(b, nwin, wc, lane, kv, KC, acc);
         if (wc == nwin - 1) {
             const SegRef<TC> sr = seg_of(sg, gc);
-            reduce_store<MR, YT, TC>(acc, sr.C, M, sr.N, m0, (gc - sr.g0) * YT, lane);
+            reduce_store<MR, YT, TC>(acc, sr.C, M, sr.N, m0, (gc - sr.g0) * YT, lane, fz);
 #pragma unroll
             for (int m = 0; m < MR; ++m)
 #pragma unroll
@@ -797,7 +919,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 template <class F, int MR, int YT, int NW, int NS, typename TA, typename TC>
 __global__ __launch_bounds__(64 * NW, QMM_GEMV_MIN_WAVES)
-void gemv_stream_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K, int a_vec, int nrg) {
+void gemv_stream_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K, int a_vec, int nrg, GemvFuse fz) {
     using WS = WinSlot<F>;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -848,11 +970,17 @@ void gemv_stream_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K,
         next(gl, wl);
     }
     const int items = nwin * MR * 256;
-    for (int it = tid; it < items; it += 64 * NW) {
-        const int w = it / (MR * 256), item = it - w * (MR * 256);
-        StageItem<F, MR, TA> s2;
-        s2.load(A, M, K, m0, w, item, vec);
-        s2.store(nwin, w, item);
+    bool fused = false;
+    if constexpr (kFoldable<F, MR, YT, NW, TA>) fused = fz.kind != 0;
+    if (fused) {
+        if constexpr (kFoldable<F, MR, YT, NW, TA>) stage_fused<F, MR, NW>(A, fz, M, K, m0, nwin, tid);
+    } else {
+        for (int it = tid; it < items; it += 64 * NW) {
+            const int w = it / (MR * 256), item = it - w * (MR * 256);
+            StageItem<F, MR, TA> s2;
+            s2.load(A, M, K, m0, w, item, vec);
+            s2.store(nwin, w, item);
+        }
     }
     __syncthreads();
     if (!active) {
@@ -883,7 +1011,7 @@ void gemv_stream_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K,
         else mac_window<F, MR, YT, false>(b, nwin, wc, lane, kv, KC, acc);
         if (wc == nwin - 1) {
             const SegRef<TC> sr = seg_of(sg, gc);
-            reduce_store<MR, YT, TC>(acc, sr.C, M, sr.N, m0, (gc - sr.g0) * YT, lane);
+            reduce_store<MR, YT, TC>(acc, sr.C, M, sr.N, m0, (gc - sr.g0) * YT, lane, fz);
 #pragma unroll
             for (int m = 0; m < MR; ++m)
 #pragma unroll
@@ -968,7 +1096,7 @@ void gemv_window_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W,
         for (int y = 0; y < YT; ++y) cur[y] = nxt[y];
         __syncthreads();
     }
-    reduce_store<MR, YT, TC>(acc, C, M, N, m0, row0, lane);
+    reduce_store<MR, YT, TC>(acc, C, M, N, m0, row0, lane, GemvFuse{});
 }
 
 // Alignment-agnostic fallback: one wave per (row n, A row m), lanes over 32-weight groups,
@@ -1081,7 +1209,8 @@ struct Seg {
 };
 
 template <class F, int MR, int YT, int NW, typename TA, typename TC>
-hipError_t launch_fast(const void* A, const Seg* segs, int nseg, int M, int K, bool a_vec, hipStream_t stream) {
+hipError_t launch_fast(const void* A, const Seg* segs, int nseg, int M, int K, bool a_vec, const GemvFuse& fz,
+                       hipStream_t stream) {
     DevInfo di;
     hipError_t e = device_info(di);
     if (e != hipSuccess) return e;
@@ -1089,6 +1218,10 @@ hipError_t launch_fast(const void* A, const Seg* segs, int nseg, int M, int K, b
     const int mblocks = (M + MR - 1) / MR;
     const size_t res_lds = static_cast<size_t>(MR) * nwin * kSlotBytes;
     const int threads = 64 * NW;
+    const bool folded = fz.kind != 0 || fz.ea != nullptr;
+    if (folded && !kFoldable<F, MR, YT, NW, TA>) return hipErrorNotSupported;
+    if (fz.kind != 0 && static_cast<int64_t>(nwin) * MR * 256 > static_cast<int64_t>(kFuseOwn) * threads)
+        return hipErrorNotSupported;
 #if QMM_GEMV_STREAM
     if constexpr (F::kStream) {
         constexpr int NS = QMM_GEMV_NS;
@@ -1120,7 +1253,7 @@ hipError_t launch_fast(const void* A, const Seg* segs, int nseg, int M, int K, b
             const int fill = max(1, occ * di.cus / mblocks);
             const dim3 grid(min(need, fill), mblocks);
             hipLaunchKernelGGL((gemv_stream_kernel<F, MR, YT, NW, NS, TA, TC>), grid, dim3(threads), st_lds, stream,
-                               static_cast<const TA*>(A), sg, M, K, a_vec ? 1 : 0, nrg);
+                               static_cast<const TA*>(A), sg, M, K, a_vec ? 1 : 0, nrg, fz);
             return hipGetLastError();
         }
     }
@@ -1149,10 +1282,10 @@ hipError_t launch_fast(const void* A, const Seg* segs, int nseg, int M, int K, b
         const int fill = max(1, occ * di.cus / mblocks);
         const dim3 grid(min(need, fill), mblocks);
         hipLaunchKernelGGL((gemv_resident_kernel<F, MR, YT, NW, TA, TC>), grid, dim3(threads), res_lds, stream,
-                           static_cast<const TA*>(A), sg, M, K, a_vec ? 1 : 0, nrg);
+                           static_cast<const TA*>(A), sg, M, K, a_vec ? 1 : 0, nrg, fz);
         return hipGetLastError();
     }
-    if (nseg != 1) return hipErrorNotSupported;
+    if (nseg != 1 || folded) return hipErrorNotSupported;
     const int N = segs[0].N;
     const size_t win_lds = static_cast<size_t>(MR) * 2 * kSlotBytes;
     const void* kern = reinterpret_cast<const void*>(&gemv_window_kernel<F, MR, YT, NW, TA, TC>);
@@ -1168,25 +1301,26 @@ hipError_t launch_fast(const void* A, const Seg* segs, int nseg, int M, int K, b
 
 template <class F, int NW, typename TA, typename TC>
 hipError_t dispatch_rows(const void* A, const Seg* segs, int nseg, int M, int N, int K, bool a_vec,
-                         hipStream_t stream) {
+                         const GemvFuse& fz, hipStream_t stream) {
     // Rows per wave item by the total row count (enough items to cover the 256 CUs several times).
     constexpr int YB = QMM_GEMV_YT_BIG;
     if (M == 1) {
-        if (N >= 8192) return launch_fast<F, 1, YB, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
-        if (N >= 2048) return launch_fast<F, 1, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
-        return launch_fast<F, 1, 1, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
+        if (N >= 8192) return launch_fast<F, 1, YB, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
+        if (N >= 2048) return launch_fast<F, 1, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
+        return launch_fast<F, 1, 1, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
     }
     if (M == 2) {
-        if (N >= 8192) return launch_fast<F, 2, YB, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
-        if (N >= 2048) return launch_fast<F, 2, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
-        return launch_fast<F, 2, 1, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
+        if (N >= 8192) return launch_fast<F, 2, YB, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
+        if (N >= 2048) return launch_fast<F, 2, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
+        return launch_fast<F, 2, 1, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
     }
-    if (N >= 4096) return launch_fast<F, 4, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
-    return launch_fast<F, 4, 1, NW, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
+    if (N >= 4096) return launch_fast<F, 4, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
+    return launch_fast<F, 4, 1, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
 }
 
 template <class F, typename TA, typename TC>
-hipError_t dispatch_fast(const void* A, const Seg* segs, int nseg, int M, int K, bool a_vec, hipStream_t stream) {
+hipError_t dispatch_fast(const void* A, const Seg* segs, int nseg, int M, int K, bool a_vec, const GemvFuse& fz,
+                         hipStream_t stream) {
     int N = 0;
     for (int j = 0; j < nseg; ++j) N += segs[j].N;
     // Resident activations above 40 KB of LDS leave room for at most three workgroups per CU:
@@ -1194,8 +1328,8 @@ hipError_t dispatch_fast(const void* A, const Seg* segs, int nseg, int M, int K,
     // tiles use the windowed kernel at such K).
     const int nwin = (K + kGemvWindow - 1) / kGemvWindow;
     const size_t res_lds = static_cast<size_t>(min(M, 4)) * nwin * kSlotBytes;
-    if (M <= 2 && res_lds > 40 * 1024) return dispatch_rows<F, 16, TA, TC>(A, segs, nseg, M, N, K, a_vec, stream);
-    return dispatch_rows<F, QMM_GEMV_NW, TA, TC>(A, segs, nseg, M, N, K, a_vec, stream);
+    if (M <= 2 && res_lds > 40 * 1024) return dispatch_rows<F, 16, TA, TC>(A, segs, nseg, M, N, K, a_vec, fz, stream);
+    return dispatch_rows<F, QMM_GEMV_NW, TA, TC>(A, segs, nseg, M, N, K, a_vec, fz, stream);
 }
 
 template <int T, typename TA, typename TC>
@@ -1214,13 +1348,14 @@ bool fast_weights(int t, const void* W) {
 }
 
 template <typename TA, typename TC>
-hipError_t dispatch_types(int t, const void* A, const Seg* segs, int nseg, int M, int K, hipStream_t stream) {
+hipError_t dispatch_types(int t, const void* A, const Seg* segs, int nseg, int M, int K, const GemvFuse& fz,
+                          hipStream_t stream) {
     const bool a_ok = (reinterpret_cast<uintptr_t>(A) & (sizeof(TA) - 1)) == 0;
     const bool a_vec = (reinterpret_cast<uintptr_t>(A) & 15u) == 0;
     bool fast = a_ok && (t != QMM_TYPE_F16 || K % 16 == 0);
     for (int j = 0; j < nseg; ++j) fast = fast && fast_weights(t, segs[j].W);
     if (!fast) {
-        if (nseg != 1) return hipErrorNotSupported;
+        if (nseg != 1 || fz.kind != 0 || fz.ea != nullptr) return hipErrorNotSupported;
         const void* W = segs[0].W;
         void* C = segs[0].C;
         const int N = segs[0].N;
@@ -1234,23 +1369,27 @@ hipError_t dispatch_types(int t, const void* A, const Seg* segs, int nseg, int M
         }
     }
     switch (t) {
-        case QMM_TYPE_Q4_K: return dispatch_fast<GQ4K, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
-        case QMM_TYPE_Q6_K: return dispatch_fast<GQ6K, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
-        case QMM_TYPE_Q8_0: return dispatch_fast<GQ80, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
-        case QMM_TYPE_Q4_0: return dispatch_fast<GQ40, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
-        case QMM_TYPE_F16: return dispatch_fast<GF16, TA, TC>(A, segs, nseg, M, K, a_vec, stream);
+        case QMM_TYPE_Q4_K: return dispatch_fast<GQ4K, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
+        case QMM_TYPE_Q6_K: return dispatch_fast<GQ6K, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
+        case QMM_TYPE_Q8_0: return dispatch_fast<GQ80, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
+        case QMM_TYPE_Q4_0: return dispatch_fast<GQ40, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
+        case QMM_TYPE_F16: return dispatch_fast<GF16, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t dispatch_dtypes(int t, const void* A, int a_dtype, int c_dtype, const Seg* segs, int nseg, int M, int K,
-                           hipStream_t stream) {
+                           hipStream_t stream, const GemvFuse& fz = GemvFuse{}) {
     if (a_dtype == QMM_DTYPE_F32) {
-        if (c_dtype == QMM_DTYPE_F32) return dispatch_types<float, float>(t, A, segs, nseg, M, K, stream);
-        return dispatch_types<float, __half>(t, A, segs, nseg, M, K, stream);
+        if (fz.kind != 0 || fz.ea != nullptr) return hipErrorNotSupported;
+        if (c_dtype == QMM_DTYPE_F32) return dispatch_types<float, float>(t, A, segs, nseg, M, K, fz, stream);
+        return dispatch_types<float, __half>(t, A, segs, nseg, M, K, fz, stream);
     }
-    if (c_dtype == QMM_DTYPE_F32) return dispatch_types<__half, float>(t, A, segs, nseg, M, K, stream);
-    return dispatch_types<__half, __half>(t, A, segs, nseg, M, K, stream);
+    if (c_dtype == QMM_DTYPE_F32) {
+        if (fz.ea != nullptr) return hipErrorNotSupported;
+        return dispatch_types<__half, float>(t, A, segs, nseg, M, K, fz, stream);
+    }
+    return dispatch_types<__half, __half>(t, A, segs, nseg, M, K, fz, stream);
 }
 
 }  // namespace
@@ -1270,5 +1409,17 @@ hipError_t launch_gemv_fused(int ggml_type, const void* A, int a_dtype, int c_dt
 }
 
 int gemv_max_fused() { return kMaxSegs; }
+
+hipError_t launch_gemv_ex(int ggml_type, const void* A, int c_dtype, int M, int K, const void* const* W, void* const* C,
+                          const int* N, int count, const GemvFuse& fz, hipStream_t stream) {
+    if (count < 1 || count > kMaxSegs || M != 1) return hipErrorNotSupported;
+    // the folded staging reads 16-value pieces (and the norm weights) as 16-byte vectors
+    const uintptr_t align = reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(fz.R) | reinterpret_cast<uintptr_t>(fz.w);
+    if (fz.kind < 0 || fz.kind > 2) return hipErrorInvalidValue;
+    if (fz.kind != 0 && (K % 16 != 0 || (align & 15u) != 0)) return hipErrorNotSupported;
+    Seg segs[kMaxSegs];
+    for (int j = 0; j < count; ++j) segs[j] = Seg{W[j], C[j], N[j]};
+    return dispatch_dtypes(ggml_type, A, QMM_DTYPE_F16, c_dtype, segs, count, M, K, stream, fz);
+}
 
 }  // namespace qmm

@@ -50,6 +50,23 @@ inline int block_bytes(int t) {
     }
 }
 
+// Work folded into a GEMV launch with fp16 activations (the decode layer's neighbours of its
+// projections).  Activation prologue, applied while the activations are staged:
+//   kind 0: A as given;
+//   kind 1: half(A * rsqrt(mean(A^2) + eps) * w), w F16 or F32 (w_f32) of length K;
+//   kind 2: the same on v = half(A + R).
+// Output epilogue (ea != nullptr, fp16 output): C = half(half(ea + eb) + half(acc)), ea / eb of
+// C's shape.
+struct GemvFuse {
+    int kind = 0;
+    const void* R = nullptr;
+    const void* w = nullptr;
+    int w_f32 = 0;
+    float eps = 0.0f;
+    const void* ea = nullptr;
+    const void* eb = nullptr;
+};
+
 // Kernel launchers (validated arguments; return a hipError_t from the launch).
 hipError_t launch_gemv(int ggml_type, const void* A, int a_dtype, const void* W, void* C,
                        int c_dtype, int M, int N, int K, hipStream_t stream);
@@ -57,6 +74,11 @@ hipError_t launch_gemv(int ggml_type, const void* A, int a_dtype, const void* W,
 // hipErrorNotSupported when the fused path does not apply (the caller then launches each).
 hipError_t launch_gemv_fused(int ggml_type, const void* A, int a_dtype, int c_dtype, int M, int K,
                              const void* const* W, void* const* C, const int* N, int count, hipStream_t stream);
+// GEMV of up to gemv_max_fused() matrices sharing fp16 activations A [M, K] (M < kGemvMaxM), with
+// work folded in (`fz`); hipErrorNotSupported when the shapes or alignments need a kernel without
+// the folding (the caller then runs the separate kernels).
+hipError_t launch_gemv_ex(int ggml_type, const void* A, int c_dtype, int M, int K, const void* const* W, void* const* C,
+                          const int* N, int count, const GemvFuse& fz, hipStream_t stream);
 int gemv_max_fused();
 hipError_t launch_gemm_prefill(int ggml_type, const void* A, int a_dtype, const void* W, void* C,
                                int c_dtype, int M, int N, int K, hipStream_t stream);

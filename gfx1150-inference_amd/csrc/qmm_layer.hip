@@ -415,15 +415,35 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const float* __r
     const int m = static_cast<int>(mh / heads);
     const size_t stride = static_cast<size_t>(head_dim) + 2;
     auto at = [&](int c) { return part + ((static_cast<size_t>(m) * chunks + c) * heads + h) * stride; };
+    // chunks are taken 8 at a time with all their loads issued first; the arithmetic runs in chunk
+    // order
+    constexpr int kG = 8;
     float mx = -INFINITY;
-    for (int c = 0; c < chunks; ++c) mx = fmaxf(mx, at(c)[0]);
+    for (int c0 = 0; c0 < chunks; c0 += kG) {
+        float v[kG];
+#pragma unroll
+        for (int i = 0; i < kG; ++i) v[i] = c0 + i < chunks ? at(c0 + i)[0] : -INFINITY;
+#pragma unroll
+        for (int i = 0; i < kG; ++i) mx = fmaxf(mx, v[i]);
+    }
     float sum = 0.0f, acc = 0.0f;
-    for (int c = 0; c < chunks; ++c) {
-        const float* p = at(c);
-        if (p[1] > 0.0f) {
-            const float a = expf(p[0] - mx);
-            sum += p[1] * a;
-            acc += p[2 + d] * a;
+    for (int c0 = 0; c0 < chunks; c0 += kG) {
+        float pm[kG], ps[kG], po[kG];
+#pragma unroll
+        for (int i = 0; i < kG; ++i) {
+            const bool ok = c0 + i < chunks;
+            const float* p = at(ok ? c0 + i : 0);
+            pm[i] = p[0];
+            ps[i] = ok ? p[1] : 0.0f;
+            po[i] = p[2 + d];
+        }
+#pragma unroll
+        for (int i = 0; i < kG; ++i) {
+            if (ps[i] > 0.0f) {
+                const float a = expf(pm[i] - mx);
+                sum += ps[i] * a;
+                acc += po[i] * a;
+            }
         }
     }
     out[idx] = static_cast<_Float16>(sum > 0.0f ? acc / sum : 0.0f);
@@ -922,16 +942,56 @@ LayerStatus forward_layer(const qmm_layer_config& cfg, const qmm_layer_weights& 
         return d;
     };
     const int nw_f32 = w.attn_norm_dtype == QMM_DTYPE_F32 ? 1 : 0, fw_f32 = w.ffn_norm_dtype == QMM_DTYPE_F32 ? 1 : 0;
+    // Decode (one row): the norms, SwiGLU and the last residual add are folded into the GEMV
+    // launches (their activation staging and output epilogue); a step whose shapes the folded
+    // kernels do not take runs the separate kernels instead.
+    const bool fold = seq_len == 1;
+    // Runs descriptors of `d` with fold `fz` on their common activations, consecutive descriptors
+    // of one weight type as one launch, until one is not supported folded; `done` = how many ran.
+    auto folded = [&](const qmm_gemm_desc* d, int n, const GemvFuse& fz, int& done) -> LayerStatus {
+        done = 0;
+        if (!fold) return {QMM_OK, ""};
+        for (int i = 0; i < n;) {
+            int j = i + 1;
+            while (j < n && d[j].ggml_type == d[i].ggml_type) ++j;
+            const void* W[3];
+            void* C[3];
+            int N[3];
+            for (int t = i; t < j; ++t) {
+                W[t - i] = d[t].W;
+                C[t - i] = d[t].C;
+                N[t - i] = d[t].N;
+            }
+            const hipError_t fe = launch_gemv_ex(d[i].ggml_type, d[i].A, QMM_DTYPE_F16, 1, d[i].K, W, C, N, j - i, fz, stream);
+            if (fe == hipErrorNotSupported) return {QMM_OK, ""};  // the caller runs the rest unfolded
+            if (fe != hipSuccess) return {QMM_ERR_HIP, std::string("folded GEMV: ") + hipGetErrorString(fe)};
+            i = j;
+            done = j;
+        }
+        return {QMM_OK, ""};
+    };
+    int done = 0;
 
-    // 1. pre-attention RMSNorm
-    if ((e = launch_rmsnorm(x_in, nullptr, w.attn_norm, nw_f32, nullptr, ws + o_norm, seq_len, hid, cfg.rms_norm_eps,
-                            stream)) != hipSuccess)
-        return fail(e, "rmsnorm");
-    // 2. q, k, v (one fused launch)
+    // 1.-2. pre-attention RMSNorm, q, k, v (one launch per weight type)
     const qmm_gemm_desc qkv[3] = {desc(w.wq_type, ws + o_norm, w.wq, ws + o_q, seq_len, qd, hid),
                                   desc(w.wk_type, ws + o_norm, w.wk, ws + o_k, seq_len, kvd, hid),
                                   desc(w.wv_type, ws + o_norm, w.wv, ws + o_v, seq_len, kvd, hid)};
-    if ((st = gemms(qkv, 3)).code != QMM_OK) return st;
+    {
+        GemvFuse fz;
+        fz.kind = 1;
+        fz.w = w.attn_norm;
+        fz.w_f32 = nw_f32;
+        fz.eps = cfg.rms_norm_eps;
+        qmm_gemm_desc dq[3] = {qkv[0], qkv[1], qkv[2]};
+        for (auto& d : dq) d.A = x_in;
+        if ((st = folded(dq, 3, fz, done)).code != QMM_OK) return st;
+    }
+    if (done < 3) {
+        if ((e = launch_rmsnorm(x_in, nullptr, w.attn_norm, nw_f32, nullptr, ws + o_norm, seq_len, hid, cfg.rms_norm_eps,
+                                stream)) != hipSuccess)
+            return fail(e, "rmsnorm");
+        if ((st = gemms(qkv + done, 3 - done)).code != QMM_OK) return st;
+    }
     // 3. RoPE on q and k; k and v land in the cache at their positions
     const size_t cache_off = static_cast<size_t>(pos_offset) * kvd;
     if ((e = launch_rope(ws + o_q, ws + o_qr, H, ws + o_k, kc + cache_off, ws + o_v, vc + cache_off, KVH, seq_len, D,
@@ -945,21 +1005,49 @@ LayerStatus forward_layer(const qmm_layer_config& cfg, const qmm_layer_weights& 
     // 5. output projection
     const qmm_gemm_desc o = desc(w.wo_type, ws + o_att, w.wo, ws + o_proj, seq_len, hid, qd);
     if ((st = gemms(&o, 1)).code != QMM_OK) return st;
-    // 6. residual + pre-FFN RMSNorm
-    if ((e = launch_rmsnorm(x_in, ws + o_proj, w.ffn_norm, fw_f32, ws + o_h, ws + o_norm, seq_len, hid, cfg.rms_norm_eps,
-                            stream)) != hipSuccess)
-        return fail(e, "rmsnorm_residual");
-    // 7. gate, up (one fused launch), SwiGLU, down
+    // 6.-7. residual + pre-FFN RMSNorm, gate, up (one launch per weight type)
     const qmm_gemm_desc gu[2] = {desc(w.wgate_type, ws + o_norm, w.wgate, ws + o_g, seq_len, inter, hid),
                                  desc(w.wup_type, ws + o_norm, w.wup, ws + o_u, seq_len, inter, hid)};
-    if ((st = gemms(gu, 2)).code != QMM_OK) return st;
+    bool h_ready = false;  // h = half(x_in + o) materialised at ws + o_h
+    {
+        GemvFuse fz;
+        fz.kind = 2;
+        fz.R = ws + o_proj;
+        fz.w = w.ffn_norm;
+        fz.w_f32 = fw_f32;
+        fz.eps = cfg.rms_norm_eps;
+        qmm_gemm_desc dg[2] = {gu[0], gu[1]};
+        for (auto& d : dg) d.A = x_in;
+        if ((st = folded(dg, 2, fz, done)).code != QMM_OK) return st;
+    }
+    if (done < 2) {
+        if ((e = launch_rmsnorm(x_in, ws + o_proj, w.ffn_norm, fw_f32, ws + o_h, ws + o_norm, seq_len, hid,
+                                cfg.rms_norm_eps, stream)) != hipSuccess)
+            return fail(e, "rmsnorm_residual");
+        h_ready = true;
+        if ((st = gemms(gu + done, 2 - done)).code != QMM_OK) return st;
+    }
+    // 8.-9. SwiGLU, down and the second residual (folded into down's output).  SwiGLU stays a
+    // kernel of its own: folded into down's staging, every down workgroup would read both
+    // intermediate vectors and evaluate every exp (measured slower than the separate kernel).
     if ((e = launch_swiglu(ws + o_g, ws + o_u, ws + o_act, static_cast<int64_t>(S) * inter, stream)) != hipSuccess)
         return fail(e, "swiglu");
-    const qmm_gemm_desc dn = desc(w.wdown_type, ws + o_act, w.wdown, ws + o_down, seq_len, hid, inter);
-    if ((st = gemms(&dn, 1)).code != QMM_OK) return st;
-    // 8. second residual
-    if ((e = launch_residual_add(ws + o_h, ws + o_down, x_out, static_cast<int64_t>(S) * hid, stream)) != hipSuccess)
-        return fail(e, "residual_add");
+    {
+        GemvFuse fz;
+        fz.ea = x_in;
+        fz.eb = ws + o_proj;
+        const qmm_gemm_desc dd = desc(w.wdown_type, ws + o_act, w.wdown, x_out, seq_len, hid, inter);
+        if ((st = folded(&dd, 1, fz, done)).code != QMM_OK) return st;
+    }
+    if (done < 1) {
+        const qmm_gemm_desc dn = desc(w.wdown_type, ws + o_act, w.wdown, ws + o_down, seq_len, hid, inter);
+        if ((st = gemms(&dn, 1)).code != QMM_OK) return st;
+        if (!h_ready &&
+            (e = launch_residual_add(x_in, ws + o_proj, ws + o_h, static_cast<int64_t>(S) * hid, stream)) != hipSuccess)
+            return fail(e, "residual_add");
+        if ((e = launch_residual_add(ws + o_h, ws + o_down, x_out, static_cast<int64_t>(S) * hid, stream)) != hipSuccess)
+            return fail(e, "residual_add");
+    }
     return {QMM_OK, ""};
 }
 

@@ -111,9 +111,10 @@ def test_batch_overlapping_outputs_keep_sequential_order(dev):
     assert torch.equal(C.cpu(), single(t, A, W2, N, K, torch.float32))
 
 
-def test_batch_output_overwriting_shared_input(dev):
-    # The first descriptor writes its output over the activations the second one reads (fp32
-    # [1, K] activations, N = K): sequentially, the second sees the first one's output.
+def test_batch_output_feeding_the_next_descriptor(dev):
+    # The first descriptor's output is the second one's activations: run in order, the second sees
+    # the first one's result.  An output over the descriptor's own input is rejected (every
+    # workgroup reads all of A while others write C).
     import torch
     import qmm
     t = O.GGML_Q8_0
@@ -123,12 +124,15 @@ def test_batch_output_overwriting_shared_input(dev):
     raw1, raw2 = O.synth_weights(t, K, K, rng), O.synth_weights(t, 64, K, rng)
     W1, W2 = to_dev(raw1, dev), to_dev(raw2, dev)
     A = to_dev(x, dev)
+    B = torch.empty((1, K), device=dev)
     C2 = torch.empty((1, 64), device=dev)
-    qmm.gemm_batch(descs_of([(t, A, W1, A, K, K), (t, A, W2, C2, 64, K)]))
+    qmm.gemm_batch(descs_of([(t, A, W1, B, K, K), (t, B, W2, C2, 64, K)]))
     torch.cuda.synchronize()
     y1 = single(t, to_dev(x, dev), W1, K, K, torch.float32)
-    assert torch.equal(A.cpu(), y1)
+    assert torch.equal(B.cpu(), y1)
     assert torch.equal(C2.cpu(), single(t, y1.to(dev), W2, 64, K, torch.float32))
+    with pytest.raises(ValueError, match="must not overlap A"):
+        qmm.gemm_batch(descs_of([(t, A, W1, A, K, K)]))
 
 
 def test_batch_events_between_descriptors(dev):
