@@ -692,7 +692,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32 activations, Q4_K/Q6_K weights, fp32 accumulate",
+        "dtype": "f16",
+        "dtype_detail": "fp32 activations rounded to f16 when staged; Q4_K/Q6_K codes as exact f16; "
+                        "f16 x f16 products (v_dot2_f32_f16) accumulated in fp32",
         "data": "synthetic: random packed blocks (fp16 scales |N(0,1)|*0.01), x ~ N(0,1)",
         "config": {"workload": "llama3-70b-q4_k_m-decode-m1-80-layers", "layers": args.layers, "M": 1,
                    "hidden": 8192, "intermediate": 28672, "kv_dim": 1024,
