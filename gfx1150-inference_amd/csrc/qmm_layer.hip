@@ -349,6 +349,14 @@ __global__ __launch_bounds__(256) void attention_keys_kernel(const _Float16* __r
 #pragma unroll
     for (int i = 0; i < kMaxPairs / 4; ++i)
         if (4 * i < pairs) kv[i] = kr[i];
+    // the chunk's V rows are requested together with the K rows (they do not depend on the scores):
+    // lane l <-> dims 2l, 2l + 1 of every row; rows past the chunk re-read its last key
+    const bool own = 2 * lane < head_dim;
+    const uint32_t* vbase = reinterpret_cast<const uint32_t*>(Vc + static_cast<size_t>(kvh) * head_dim) + (own ? lane : 0);
+    const size_t vrow = row / 2;  // in f16 pairs
+    uint32_t vv[kAttnChunk];
+#pragma unroll
+    for (int j = 0; j < kAttnChunk; ++j) vv[j] = vbase[static_cast<size_t>(s0 + min(j, max(n - 1, 0))) * vrow];
     float dot = 0.0f;
 #pragma unroll
     for (int i = 0; i < kMaxPairs / 4; ++i) {
@@ -367,21 +375,13 @@ __global__ __launch_bounds__(256) void attention_keys_kernel(const _Float16* __r
 
     // output: lane l <-> dims 2l, 2l + 1
     float acc0 = 0.0f, acc1 = 0.0f;
-    const bool own = 2 * lane < head_dim;
-    const uint32_t* vbase = reinterpret_cast<const uint32_t*>(Vc + static_cast<size_t>(kvh) * head_dim) + (own ? lane : 0);
-    const size_t vrow = row / 2;  // in f16 pairs
-    for (int j0 = 0; j0 < n; j0 += 16) {
-        uint32_t vv[16];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) vv[j] = vbase[static_cast<size_t>(s0 + min(j0 + j, n - 1)) * vrow];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const float pj = __shfl(e, j0 + j, 64);  // 0 beyond the chunk's keys
-            h2v v;
-            __builtin_memcpy(&v, &vv[j], 4);
-            acc0 += pj * static_cast<float>(v[0]);
-            acc1 += pj * static_cast<float>(v[1]);
-        }
+    for (int j = 0; j < kAttnChunk; ++j) {
+        const float pj = __shfl(e, j, 64);  // 0 beyond the chunk's keys
+        h2v v;
+        __builtin_memcpy(&v, &vv[j], 4);
+        acc0 += pj * static_cast<float>(v[0]);
+        acc1 += pj * static_cast<float>(v[1]);
     }
     if (chunks == 1) {
         if (own) {
