@@ -320,11 +320,25 @@ __global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restri
 //     once and accumulates p_j v_j with p_j broadcast from lane j.
 // Output: partial results (max, sum, unnormalised output) as attention_kernel, or fp16 output
 // when there is one chunk.
+// With kRope (one query row, the decode step): Q, k_new and v_new are the projections before
+// RoPE; each wave rotates its query into LDS, the new key (position start_pos) is rotated into LDS
+// and stands in for its cache row, and the first query head of each KV head's group writes the
+// rotated key and the value into the cache row (which no wave of this launch reads).
+struct DecodeRope {
+    const _Float16* k_new;  // [kv_heads][head_dim]
+    const _Float16* v_new;
+    _Float16* kc;           // the layer's K / V cache (rows of kv_heads * head_dim)
+    _Float16* vc;
+    int neox;
+    float cs[kMaxRopePairs / 2], sn[kMaxRopePairs / 2];  // cos / sin of pair p's angle at the new position
+};
+
+template <bool kRope>
 __global__ __launch_bounds__(256) void attention_keys_kernel(const _Float16* __restrict__ Q, const _Float16* __restrict__ Kc,
                                                             const _Float16* __restrict__ Vc, _Float16* __restrict__ out,
                                                             float* __restrict__ part, int q_len, int kv_len, int heads,
                                                             int kv_heads, int head_dim, int start_pos, float scale,
-                                                            int causal, int chunks) {
+                                                            int causal, int chunks, DecodeRope dr) {
     constexpr int kMaxPairs = 64;  // head_dim <= 128
     const int lane = threadIdx.x & 63;
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
@@ -343,20 +357,72 @@ __global__ __launch_bounds__(256) void attention_keys_kernel(const _Float16* __r
 
     // scores: lane j <-> key s0 + j (lanes past the chunk re-read its first key and are masked)
     const uint32_t* qp = reinterpret_cast<const uint32_t*>(Q + (static_cast<size_t>(m) * heads + h) * head_dim);
-    const int sj = s0 + (lane < n ? lane : 0);
+    const int pos = start_pos + m;                       // the new key (kRope: m == 0)
+    const int j_new = kRope && pos >= s0 && pos < s0 + kAttnChunk ? pos - s0 : -1;
+    __shared__ __align__(16) _Float16 rot[4][2][2 * kMaxPairs];  // [wave][q, k_new][dim]
+    if constexpr (kRope) {
+        // lane p rotates pair p (dims 2p, 2p + 1, or p, p + head_dim / 2) of the query and of the
+        // new key, as rope_kernel does
+        const int wl = threadIdx.x >> 6;
+        if (lane < pairs) {
+            const float cs = dr.cs[lane], sn = dr.sn[lane];
+            const int i0 = dr.neox ? lane : 2 * lane, i1 = dr.neox ? lane + pairs : 2 * lane + 1;
+            const _Float16* qs = Q + (static_cast<size_t>(m) * heads + h) * head_dim;
+            const _Float16* ks = dr.k_new + static_cast<size_t>(kvh) * head_dim;
+            float a = static_cast<float>(qs[i0]), b = static_cast<float>(qs[i1]);
+            rot[wl][0][i0] = static_cast<_Float16>(a * cs - b * sn);
+            rot[wl][0][i1] = static_cast<_Float16>(a * sn + b * cs);
+            a = static_cast<float>(ks[i0]);
+            b = static_cast<float>(ks[i1]);
+            const _Float16 k0 = static_cast<_Float16>(a * cs - b * sn), k1 = static_cast<_Float16>(a * sn + b * cs);
+            rot[wl][1][i0] = k0;
+            rot[wl][1][i1] = k1;
+            if (j_new >= 0 && h % (heads / kv_heads) == 0) {  // one writer per KV head
+                const size_t crow = static_cast<size_t>(pos) * row + static_cast<size_t>(kvh) * head_dim;
+                dr.kc[crow + i0] = k0;
+                dr.kc[crow + i1] = k1;
+                const _Float16* vs = dr.v_new + static_cast<size_t>(kvh) * head_dim;
+                dr.vc[crow + i0] = vs[i0];
+                dr.vc[crow + i1] = vs[i1];
+            }
+        }
+        // only this wave reads its LDS rows, and a wave's LDS operations complete in order
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        qp = reinterpret_cast<const uint32_t*>(rot[wl][0]);
+    }
+    // a dummy lane (and the new key's lane, which takes its key from LDS) reads a row below the
+    // new key: s0 when the new key is not the chunk's first, else row 0 (pos > 0), else it is masked
+    const int dummy = j_new == 0 ? 0 : s0;
+    const int sj = lane < n && lane != j_new ? s0 + lane : (kRope ? min(dummy, max(pos - 1, 0)) : s0);
     const u32x4* kr = reinterpret_cast<const u32x4*>(Kc + static_cast<size_t>(sj) * row + static_cast<size_t>(kvh) * head_dim);
     u32x4 kv[kMaxPairs / 4];
 #pragma unroll
     for (int i = 0; i < kMaxPairs / 4; ++i)
         if (4 * i < pairs) kv[i] = kr[i];
+    if constexpr (kRope) {
+        if (lane == j_new) {
+            const u32x4* kn = reinterpret_cast<const u32x4*>(rot[threadIdx.x >> 6][1]);
+#pragma unroll
+            for (int i = 0; i < kMaxPairs / 4; ++i)
+                if (4 * i < pairs) kv[i] = kn[i];
+        }
+    }
     // the chunk's V rows are requested together with the K rows (they do not depend on the scores):
     // lane l <-> dims 2l, 2l + 1 of every row; rows past the chunk re-read its last key
     const bool own = 2 * lane < head_dim;
     const uint32_t* vbase = reinterpret_cast<const uint32_t*>(Vc + static_cast<size_t>(kvh) * head_dim) + (own ? lane : 0);
     const size_t vrow = row / 2;  // in f16 pairs
     uint32_t vv[kAttnChunk];
+    // in the kRope launch the new key's value comes from v_new and rows past the chunk's keys are
+    // replaced by zeros below, so the loads stay below the new key's row where it is in this chunk
+    const int vlast = j_new > 0 ? j_new - 1 : max(n - 1, 0);
 #pragma unroll
-    for (int j = 0; j < kAttnChunk; ++j) vv[j] = vbase[static_cast<size_t>(s0 + min(j, max(n - 1, 0))) * vrow];
+    for (int j = 0; j < kAttnChunk; ++j) vv[j] = vbase[static_cast<size_t>(s0 + min(j, vlast)) * vrow];
+    if constexpr (kRope) {
+        const uint32_t vn = own ? reinterpret_cast<const uint32_t*>(dr.v_new + static_cast<size_t>(kvh) * head_dim)[lane] : 0u;
+#pragma unroll
+        for (int j = 0; j < kAttnChunk; ++j) vv[j] = j == j_new ? vn : (j < n ? vv[j] : 0u);
+    }
     float dot = 0.0f;
 #pragma unroll
     for (int i = 0; i < kMaxPairs / 4; ++i) {
@@ -801,10 +867,10 @@ hipError_t launch_attention(const void* Q, const void* K, const void* V, void* o
     };
     const bool aligned = (reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(K) | reinterpret_cast<uintptr_t>(V)) % 16 == 0;
     if (head_dim % 8 == 0 && head_dim <= 128 && aligned)
-        hipLaunchKernelGGL(attention_keys_kernel, grid, dim3(256), 0, stream, static_cast<const _Float16*>(Q),
+        hipLaunchKernelGGL((attention_keys_kernel<false>), grid, dim3(256), 0, stream, static_cast<const _Float16*>(Q),
                            static_cast<const _Float16*>(K), static_cast<const _Float16*>(V), static_cast<_Float16*>(out),
                            static_cast<float*>(part), q_len, kv_len, heads, kv_heads, head_dim, start_pos, scale,
-                           causal ? 1 : 0, chunks);
+                           causal ? 1 : 0, chunks, DecodeRope{});
     else if (head_dim <= 64) go(std::integral_constant<int, 1>{});
     else if (head_dim <= 128) go(std::integral_constant<int, 2>{});
     else go(std::integral_constant<int, 4>{});
@@ -813,6 +879,40 @@ hipError_t launch_attention(const void* Q, const void* K, const void* V, void* o
     const int64_t n = static_cast<int64_t>(q_len) * heads * head_dim;
     hipLaunchKernelGGL(attention_combine_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream,
                        static_cast<const float*>(part), static_cast<_Float16*>(out), q_len, heads, head_dim, chunks);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_decode_rope(const void* q, const void* k_new, const void* v_new, void* kc, void* vc, void* out,
+                                        void* part, int kv_len, int heads, int kv_heads, int head_dim, float scale,
+                                        float freq_base, bool neox, hipStream_t stream) {
+    const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_new) |
+                         reinterpret_cast<uintptr_t>(v_new) | reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(vc);
+    if (kv_len <= 0 || heads <= 0 || head_dim % 8 != 0 || head_dim > 128 || (al & 15u) != 0) return hipErrorNotSupported;
+    DecodeRope dr{};
+    dr.k_new = static_cast<const _Float16*>(k_new);
+    dr.v_new = static_cast<const _Float16*>(v_new);
+    dr.kc = static_cast<_Float16*>(kc);
+    dr.vc = static_cast<_Float16*>(vc);
+    dr.neox = neox ? 1 : 0;
+    // the angle as the RoPE kernel forms it (fp32 position x fp32 inverse frequency); its cosine
+    // and sine evaluated here once for the step
+    for (int i = 0; i < head_dim / 2; ++i) {
+        const float inv = 1.0f / std::pow(freq_base, static_cast<float>(2 * i) / static_cast<float>(head_dim));
+        const float ang = static_cast<float>(kv_len - 1) * inv;
+        dr.cs[i] = static_cast<float>(std::cos(static_cast<double>(ang)));
+        dr.sn[i] = static_cast<float>(std::sin(static_cast<double>(ang)));
+    }
+    const int chunks = attn_chunks(kv_len);
+    const int64_t waves = static_cast<int64_t>(heads) * chunks;
+    hipLaunchKernelGGL((attention_keys_kernel<true>), dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0, stream,
+                       static_cast<const _Float16*>(q), static_cast<const _Float16*>(kc), static_cast<const _Float16*>(vc),
+                       static_cast<_Float16*>(out), static_cast<float*>(part), 1, kv_len, heads, kv_heads, head_dim,
+                       kv_len - 1, scale, 1, chunks, dr);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || chunks == 1) return e;
+    const int64_t n = static_cast<int64_t>(heads) * head_dim;
+    hipLaunchKernelGGL(attention_combine_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream,
+                       static_cast<const float*>(part), static_cast<_Float16*>(out), 1, heads, head_dim, chunks);
     return hipGetLastError();
 }
 
@@ -992,16 +1092,21 @@ LayerStatus forward_layer(const qmm_layer_config& cfg, const qmm_layer_weights& 
             return fail(e, "rmsnorm");
         if ((st = gemms(qkv + done, 3 - done)).code != QMM_OK) return st;
     }
-    // 3. RoPE on q and k; k and v land in the cache at their positions
-    const size_t cache_off = static_cast<size_t>(pos_offset) * kvd;
-    if ((e = launch_rope(ws + o_q, ws + o_qr, H, ws + o_k, kc + cache_off, ws + o_v, vc + cache_off, KVH, seq_len, D,
-                         pos_offset, cfg.rope_freq_base, cfg.rope_neox != 0, stream)) != hipSuccess)
-        return fail(e, "rope");
-    // 4. attention over the cache
+    // 3.-4. RoPE on q and k (k and v land in the cache at their positions), attention over the
+    // cache; in decode the rotation and the cache write run inside the attention kernel
     const float scale = cfg.scale != 0.0f ? cfg.scale : 1.0f / std::sqrt(static_cast<float>(D));
-    if ((e = launch_attention(ws + o_qr, kc, vc, ws + o_att, ws + o_part, seq_len, kv_len, H, KVH, D, pos_offset, scale,
-                              true, stream)) != hipSuccess)
-        return fail(e, "attention");
+    e = fold ? launch_attention_decode_rope(ws + o_q, ws + o_k, ws + o_v, kc, vc, ws + o_att, ws + o_part, kv_len, H, KVH, D,
+                                            scale, cfg.rope_freq_base, cfg.rope_neox != 0, stream)
+             : hipErrorNotSupported;
+    if (e == hipErrorNotSupported) {
+        const size_t cache_off = static_cast<size_t>(pos_offset) * kvd;
+        if ((e = launch_rope(ws + o_q, ws + o_qr, H, ws + o_k, kc + cache_off, ws + o_v, vc + cache_off, KVH, seq_len, D,
+                             pos_offset, cfg.rope_freq_base, cfg.rope_neox != 0, stream)) != hipSuccess)
+            return fail(e, "rope");
+        e = launch_attention(ws + o_qr, kc, vc, ws + o_att, ws + o_part, seq_len, kv_len, H, KVH, D, pos_offset, scale, true,
+                             stream);
+    }
+    if (e != hipSuccess) return fail(e, "attention");
     // 5. output projection
     const qmm_gemm_desc o = desc(w.wo_type, ws + o_att, w.wo, ws + o_proj, seq_len, hid, qd);
     if ((st = gemms(&o, 1)).code != QMM_OK) return st;

@@ -236,8 +236,10 @@ def make_layer(r, hidden, inter, heads, kvh, d, types):
     return packed, deq
 
 
-@pytest.mark.parametrize("prefill", [4, 40])
-def test_forward_layer_prefill_then_decode(dev, prefill):
+# Decode positions cover the new key as the first of a 64-key chunk (64) and position 0 (no
+# prefill); NeoX pairs are rotated in the decode attention kernel too.
+@pytest.mark.parametrize("prefill,neox", [(4, False), (40, False), (64, False), (0, False), (40, True)])
+def test_forward_layer_prefill_then_decode(dev, prefill, neox):
     import torch
     import qmm
     r = np.random.default_rng(50 + prefill)
@@ -255,24 +257,31 @@ def test_forward_layer_prefill_then_decode(dev, prefill):
         setattr(w, f + "_type", packed[n][0])
     c = qmm.LayerConfig()
     c.hidden_size, c.intermediate_size, c.num_heads, c.num_kv_heads, c.head_dim = hidden, inter, heads, kvh, d
-    c.rms_norm_eps, c.rope_freq_base, c.rope_neox, c.scale = 1e-5, 10000.0, 0, 0.0
+    c.rms_norm_eps, c.rope_freq_base, c.rope_neox, c.scale = 1e-5, 10000.0, int(neox), 0.0
     cfg = {"num_heads": heads, "num_kv_heads": kvh, "head_dim": d, "rms_norm_eps": 1e-5, "rope_freq_base": 10000.0,
-           "rope_neox": False}
-    total = prefill + 1
+           "rope_neox": neox}
+    total = prefill + 2
     x = (r.standard_normal((total, hidden)) * 0.5).astype(np.float16)
-    kc, vc = np.zeros((64, kvh, d), np.float16), np.zeros((64, kvh, d), np.float16)
-    want_pre = L.layer_forward(x[:prefill], deq, cfg, kc, vc, 0)
-    want_dec = L.layer_forward(x[prefill:], deq, cfg, kc, vc, prefill)
+    kc, vc = np.zeros((80, kvh, d), np.float16), np.zeros((80, kvh, d), np.float16)
+    want_pre = L.layer_forward(x[:prefill], deq, cfg, kc, vc, 0) if prefill else None
+    want_dec = L.layer_forward(x[prefill:prefill + 1], deq, cfg, kc, vc, prefill)
+    want_dec2 = L.layer_forward(x[prefill + 1:], deq, cfg, kc, vc, prefill + 1)
     lib = qmm.lib()
-    qmm.check(lib.qmm_kv_cache_init(3, 64, kvh, d))
+    qmm.check(lib.qmm_kv_cache_init(3, 80, kvh, d))
     try:
         X = t16(x, dev)
         Y = torch.empty_like(X)
-        qmm.check(lib.qmm_forward_layer(c, w, X.data_ptr(), Y.data_ptr(), 2, prefill, 0, stream()))
+        if prefill:
+            qmm.check(lib.qmm_forward_layer(c, w, X.data_ptr(), Y.data_ptr(), 2, prefill, 0, stream()))
         qmm.check(lib.qmm_forward_layer(c, w, X[prefill:].data_ptr(), Y[prefill:].data_ptr(), 2, 1, prefill, stream()))
         y = host(Y)
-        assert maxerr(y[:prefill], want_pre) < 5e-3
-        assert maxerr(y[prefill:], want_dec) < 5e-3
+        if prefill:
+            assert maxerr(y[:prefill], want_pre) < 5e-3
+        assert maxerr(y[prefill:prefill + 1], want_dec) < 5e-3
+        # a second decode step attends over the key and value the first one wrote into the cache
+        qmm.check(lib.qmm_forward_layer(c, w, X[prefill + 1:].data_ptr(), Y[prefill + 1:].data_ptr(), 2, 1, prefill + 1,
+                                        stream()))
+        assert maxerr(host(Y)[prefill + 1:], want_dec2) < 5e-3
         with pytest.raises(IndexError):
             qmm.check(lib.qmm_forward_layer(c, w, X.data_ptr(), Y.data_ptr(), 3, 1, 0, stream()))
     finally:
