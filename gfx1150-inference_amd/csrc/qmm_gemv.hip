@@ -699,6 +699,20 @@ __device__ __forceinline__ void reduce_store(float (&acc)[MR][YT], TC* __restric
     for (int m = 0; m < MR; ++m)
 #pragma unroll
         for (int y = 0; y < YT; ++y) v[m][y] = wave_sum_to_lane63(acc[m][y]);
+    if constexpr (YT == 2 && sizeof(TC) == 2) {
+        if (fz.pair) {  // row0 is the row of both matrices: C[row0] = half(silu(half(gate)) * half(up))
+            if (lane == 63) {
+#pragma unroll
+                for (int m = 0; m < MR; ++m)
+                    if (m0 + m < M && row0 < N) {
+                        const float g = static_cast<float>(static_cast<_Float16>(v[m][0]));
+                        const float u = static_cast<float>(static_cast<_Float16>(v[m][1]));
+                        store_out<TC>(C + static_cast<size_t>(m0 + m) * N + row0, g / (1.0f + expf(-g)) * u);
+                    }
+            }
+            return;
+        }
+    }
     if (lane == 63) {
 #pragma unroll
         for (int m = 0; m < MR; ++m)
@@ -775,7 +789,10 @@ void gemv_resident_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int 
         const uint8_t* base = sr.W + static_cast<size_t>(w) * F::kWinBytes;
 #pragma unroll
         for (int y = 0; y < YT; ++y) {
-            const uint8_t* rp = base + static_cast<size_t>(min((g - sr.g0) * YT + y, sr.N - 1)) * row_bytes;
+            // paired rows: y = 0 from the first matrix, y = 1 from the second, both row g
+            const uint8_t* rp = fz.pair ? (y == 0 ? sg.W[0] : sg.W[1]) + static_cast<size_t>(w) * F::kWinBytes +
+                                              static_cast<size_t>(min(g, sr.N - 1)) * row_bytes
+                                        : base + static_cast<size_t>(min((g - sr.g0) * YT + y, sr.N - 1)) * row_bytes;
             r[y] = F::load(rp, lane, kv);
         }
     };
@@ -847,7 +864,7 @@ void gemv_resident_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int 
         else mac_window<F, MR, YT, false>(b, nwin, wc, lane, kv, KC, acc);
         if (wc == nwin - 1) {
             const SegRef<TC> sr = seg_of(sg, gc);
-            reduce_store<MR, YT, TC>(acc, sr.C, M, sr.N, m0, (gc - sr.g0) * YT, lane, fz);
+            reduce_store<MR, YT, TC>(acc, sr.C, M, sr.N, m0, fz.pair ? gc : (gc - sr.g0) * YT, lane, fz);
 #pragma unroll
             for (int m = 0; m < MR; ++m)
 #pragma unroll
@@ -942,7 +959,8 @@ void gemv_stream_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K,
         const int valid = static_cast<int>(min(static_cast<size_t>(F::kWinBytes), row_bytes - woff));
 #pragma unroll
         for (int y = 0; y < YT; ++y) {
-            const uint8_t* rp = sr.W + static_cast<size_t>(min((g - sr.g0) * YT + y, sr.N - 1)) * row_bytes + woff;
+            const uint8_t* rp = fz.pair ? (y == 0 ? sg.W[0] : sg.W[1]) + static_cast<size_t>(min(g, sr.N - 1)) * row_bytes + woff
+                                        : sr.W + static_cast<size_t>(min((g - sr.g0) * YT + y, sr.N - 1)) * row_bytes + woff;
             uint8_t* dst = wslots + (slot * YT + y) * WS::kBytes;
 #pragma unroll
             for (int i = 0; i < WS::kInstr; ++i) {
@@ -1011,7 +1029,7 @@ void gemv_stream_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K,
         else mac_window<F, MR, YT, false>(b, nwin, wc, lane, kv, KC, acc);
         if (wc == nwin - 1) {
             const SegRef<TC> sr = seg_of(sg, gc);
-            reduce_store<MR, YT, TC>(acc, sr.C, M, sr.N, m0, (gc - sr.g0) * YT, lane, fz);
+            reduce_store<MR, YT, TC>(acc, sr.C, M, sr.N, m0, fz.pair ? gc : (gc - sr.g0) * YT, lane, fz);
 #pragma unroll
             for (int m = 0; m < MR; ++m)
 #pragma unroll
@@ -1208,6 +1226,33 @@ struct Seg {
     int N;
 };
 
+// Segment table of a launch and its row-group count.  Paired rows: one segment of N row groups
+// whose two rows come from the first and second matrix (W[0], W[1]).
+template <typename TC, int YT>
+int seg_table(const Seg* segs, int nseg, const GemvFuse& fz, GemvSegs<TC>& sg) {
+    int nrg = 0;
+    for (int j = 0; j < kMaxSegs; ++j) {
+        if (j < nseg) {
+            sg.W[j] = static_cast<const uint8_t*>(segs[j].W);
+            sg.C[j] = static_cast<TC*>(segs[j].C);
+            sg.N[j] = segs[j].N;
+            nrg += (segs[j].N + YT - 1) / YT;
+            sg.gend[j] = nrg;
+        } else {
+            sg.W[j] = sg.W[0];
+            sg.C[j] = sg.C[0];
+            sg.N[j] = sg.N[0];
+            sg.gend[j] = INT_MAX;
+        }
+    }
+    if (fz.pair) {
+        nrg = segs[0].N;
+        sg.gend[0] = nrg;
+        for (int j = 1; j < kMaxSegs; ++j) sg.gend[j] = INT_MAX;
+    }
+    return nrg;
+}
+
 template <class F, int MR, int YT, int NW, typename TA, typename TC>
 hipError_t launch_fast(const void* A, const Seg* segs, int nseg, int M, int K, bool a_vec, const GemvFuse& fz,
                        hipStream_t stream) {
@@ -1218,8 +1263,9 @@ hipError_t launch_fast(const void* A, const Seg* segs, int nseg, int M, int K, b
     const int mblocks = (M + MR - 1) / MR;
     const size_t res_lds = static_cast<size_t>(MR) * nwin * kSlotBytes;
     const int threads = 64 * NW;
-    const bool folded = fz.kind != 0 || fz.ea != nullptr;
+    const bool folded = fz.kind != 0 || fz.ea != nullptr || fz.pair != 0;
     if (folded && !kFoldable<F, MR, YT, NW, TA>) return hipErrorNotSupported;
+    if (fz.pair && (YT != 2 || MR != 1 || nseg != 2 || segs[0].N != segs[1].N || sizeof(TC) != 2)) return hipErrorNotSupported;
     if (fz.kind != 0 && static_cast<int64_t>(nwin) * MR * 256 > static_cast<int64_t>(kFuseOwn) * threads)
         return hipErrorNotSupported;
 #if QMM_GEMV_STREAM
@@ -1234,21 +1280,7 @@ hipError_t launch_fast(const void* A, const Seg* segs, int nseg, int M, int K, b
             int occ = 0;
             if ((e = occupancy(kern, threads, st_lds, occ)) != hipSuccess) return e;
             GemvSegs<TC> sg;
-            int nrg = 0;
-            for (int j = 0; j < kMaxSegs; ++j) {
-                if (j < nseg) {
-                    sg.W[j] = static_cast<const uint8_t*>(segs[j].W);
-                    sg.C[j] = static_cast<TC*>(segs[j].C);
-                    sg.N[j] = segs[j].N;
-                    nrg += (segs[j].N + YT - 1) / YT;
-                    sg.gend[j] = nrg;
-                } else {
-                    sg.W[j] = sg.W[0];
-                    sg.C[j] = sg.C[0];
-                    sg.N[j] = sg.N[0];
-                    sg.gend[j] = INT_MAX;
-                }
-            }
+            const int nrg = seg_table<TC, YT>(segs, nseg, fz, sg);
             const int need = (nrg + NW - 1) / NW;
             const int fill = max(1, occ * di.cus / mblocks);
             const dim3 grid(min(need, fill), mblocks);
@@ -1263,21 +1295,7 @@ hipError_t launch_fast(const void* A, const Seg* segs, int nseg, int M, int K, b
         int occ = 0;
         if ((e = occupancy(kern, threads, res_lds, occ)) != hipSuccess) return e;
         GemvSegs<TC> sg;
-        int nrg = 0;
-        for (int j = 0; j < kMaxSegs; ++j) {
-            if (j < nseg) {
-                sg.W[j] = static_cast<const uint8_t*>(segs[j].W);
-                sg.C[j] = static_cast<TC*>(segs[j].C);
-                sg.N[j] = segs[j].N;
-                nrg += (segs[j].N + YT - 1) / YT;
-                sg.gend[j] = nrg;
-            } else {
-                sg.W[j] = sg.W[0];
-                sg.C[j] = sg.C[0];
-                sg.N[j] = sg.N[0];
-                sg.gend[j] = INT_MAX;
-            }
-        }
+        const int nrg = seg_table<TC, YT>(segs, nseg, fz, sg);
         const int need = (nrg + NW - 1) / NW;
         const int fill = max(1, occ * di.cus / mblocks);
         const dim3 grid(min(need, fill), mblocks);
@@ -1304,6 +1322,10 @@ hipError_t dispatch_rows(const void* A, const Seg* segs, int nseg, int M, int N,
                          const GemvFuse& fz, hipStream_t stream) {
     // Rows per wave item by the total row count (enough items to cover the 256 CUs several times).
     constexpr int YB = QMM_GEMV_YT_BIG;
+    if (fz.pair) {
+        if (M != 1) return hipErrorNotSupported;
+        return launch_fast<F, 1, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
+    }
     if (M == 1) {
         if (N >= 8192) return launch_fast<F, 1, YB, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
         if (N >= 2048) return launch_fast<F, 1, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
@@ -1355,7 +1377,7 @@ hipError_t dispatch_types(int t, const void* A, const Seg* segs, int nseg, int M
     bool fast = a_ok && (t != QMM_TYPE_F16 || K % 16 == 0);
     for (int j = 0; j < nseg; ++j) fast = fast && fast_weights(t, segs[j].W);
     if (!fast) {
-        if (nseg != 1 || fz.kind != 0 || fz.ea != nullptr) return hipErrorNotSupported;
+        if (nseg != 1 || fz.kind != 0 || fz.ea != nullptr || fz.pair != 0) return hipErrorNotSupported;
         const void* W = segs[0].W;
         void* C = segs[0].C;
         const int N = segs[0].N;
@@ -1381,12 +1403,12 @@ hipError_t dispatch_types(int t, const void* A, const Seg* segs, int nseg, int M
 hipError_t dispatch_dtypes(int t, const void* A, int a_dtype, int c_dtype, const Seg* segs, int nseg, int M, int K,
                            hipStream_t stream, const GemvFuse& fz = GemvFuse{}) {
     if (a_dtype == QMM_DTYPE_F32) {
-        if (fz.kind != 0 || fz.ea != nullptr) return hipErrorNotSupported;
+        if (fz.kind != 0 || fz.ea != nullptr || fz.pair != 0) return hipErrorNotSupported;
         if (c_dtype == QMM_DTYPE_F32) return dispatch_types<float, float>(t, A, segs, nseg, M, K, fz, stream);
         return dispatch_types<float, __half>(t, A, segs, nseg, M, K, fz, stream);
     }
     if (c_dtype == QMM_DTYPE_F32) {
-        if (fz.ea != nullptr) return hipErrorNotSupported;
+        if (fz.ea != nullptr || fz.pair != 0) return hipErrorNotSupported;
         return dispatch_types<__half, float>(t, A, segs, nseg, M, K, fz, stream);
     }
     return dispatch_types<__half, __half>(t, A, segs, nseg, M, K, fz, stream);

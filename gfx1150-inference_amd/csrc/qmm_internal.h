@@ -57,7 +57,11 @@ inline int block_bytes(int t) {
 //   kind 2: the same on v = half(A + R).
 // Output epilogue (ea != nullptr, fp16 output): C = half(half(ea + eb) + half(acc)), ea / eb of
 // C's shape.
+// Paired rows (pair != 0; two matrices of N rows, one fp16 row of activations): row n of the first
+// matrix (gate) and row n of the second (up) are multiplied by one wave and C[n] (the first
+// output) = half(silu(half(gate)) * half(up)), silu(g) = g / (1 + exp(-g)).
 struct GemvFuse {
+    int pair = 0;
     int kind = 0;
     const void* R = nullptr;
     const void* w = nullptr;

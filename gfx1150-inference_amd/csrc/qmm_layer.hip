@@ -1113,7 +1113,8 @@ LayerStatus forward_layer(const qmm_layer_config& cfg, const qmm_layer_weights& 
     // 6.-7. residual + pre-FFN RMSNorm, gate, up (one launch per weight type)
     const qmm_gemm_desc gu[2] = {desc(w.wgate_type, ws + o_norm, w.wgate, ws + o_g, seq_len, inter, hid),
                                  desc(w.wup_type, ws + o_norm, w.wup, ws + o_u, seq_len, inter, hid)};
-    bool h_ready = false;  // h = half(x_in + o) materialised at ws + o_h
+    bool h_ready = false;    // h = half(x_in + o) materialised at ws + o_h
+    bool act_ready = false;  // SwiGLU's output already at ws + o_act
     {
         GemvFuse fz;
         fz.kind = 2;
@@ -1123,19 +1124,29 @@ LayerStatus forward_layer(const qmm_layer_config& cfg, const qmm_layer_weights& 
         fz.eps = cfg.rms_norm_eps;
         qmm_gemm_desc dg[2] = {gu[0], gu[1]};
         for (auto& d : dg) d.A = x_in;
-        if ((st = folded(dg, 2, fz, done)).code != QMM_OK) return st;
+        if (w.wgate_type == w.wup_type) {
+            // gate row n and up row n in one wave: the launch writes SwiGLU's output directly
+            qmm_gemm_desc dp[2] = {dg[0], dg[1]};
+            dp[0].C = ws + o_act;
+            fz.pair = 1;
+            if ((st = folded(dp, 2, fz, done)).code != QMM_OK) return st;
+            act_ready = done == 2;
+            fz.pair = 0;
+        }
+        if (!act_ready && (st = folded(dg, 2, fz, done)).code != QMM_OK) return st;
     }
-    if (done < 2) {
+    if (!act_ready && done < 2) {
         if ((e = launch_rmsnorm(x_in, ws + o_proj, w.ffn_norm, fw_f32, ws + o_h, ws + o_norm, seq_len, hid,
                                 cfg.rms_norm_eps, stream)) != hipSuccess)
             return fail(e, "rmsnorm_residual");
         h_ready = true;
         if ((st = gemms(gu + done, 2 - done)).code != QMM_OK) return st;
     }
-    // 8.-9. SwiGLU, down and the second residual (folded into down's output).  SwiGLU stays a
-    // kernel of its own: folded into down's staging, every down workgroup would read both
-    // intermediate vectors and evaluate every exp (measured slower than the separate kernel).
-    if ((e = launch_swiglu(ws + o_g, ws + o_u, ws + o_act, static_cast<int64_t>(S) * inter, stream)) != hipSuccess)
+    // 8.-9. SwiGLU (unless the gate/up launch produced it), down and the second residual (folded
+    // into down's output).  SwiGLU is not folded into down's staging: every down workgroup would
+    // read both intermediate vectors and evaluate every exp (measured slower than a kernel).
+    if (!act_ready &&
+        (e = launch_swiglu(ws + o_g, ws + o_u, ws + o_act, static_cast<int64_t>(S) * inter, stream)) != hipSuccess)
         return fail(e, "swiglu");
     {
         GemvFuse fz;
