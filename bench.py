@@ -6,7 +6,8 @@ of a Llama-3-70B Q4_K_M model whose weights are distinct random tensors resident
 (q/k/v/o/gate/up in Q4_K, down in Q6_K; 43.35 GB).  A step issues the 7 projections of
 every layer (560 GEMVs) back to back on one stream through `qmm_gemm_batch`, which runs q/k/v
 and gate/up (each set reads the same activations) as one launch each: 4 launches per layer.
-`value` is algorithmic bytes (packed weights + fp32 activations read once per GEMV + fp32
+Activations and outputs are fp16, the dtype of the reference's `matmul_q4_k` interface.
+`value` is algorithmic bytes (packed weights + fp16 activations read once per GEMV + fp16
 outputs written once) per second over the timed steps.
 
 The `roofline` object covers the dominant kernel, the fused gate+up launch (two Q4_K
@@ -123,10 +124,14 @@ def make_weight(torch, t, n, k, gen, dev):
 
 
 class Workload:
-    """Weights, activations and the qmm_gemm_desc list of one step."""
+    """Weights, activations and the qmm_gemm_desc list of one step.  Activations and outputs are
+    fp16 (the reference API's dtype) unless io == "f32"."""
 
-    def __init__(self, torch, qmm, name, specs_per_layer, layers, M, dev, gen, dominant=None):
+    def __init__(self, torch, qmm, name, specs_per_layer, layers, M, dev, gen, dominant=None, io="f16"):
         self.torch, self.qmm, self.name, self.M = torch, qmm, name, M
+        self.io_dtype = torch.float16 if io == "f16" else torch.float32
+        self.io_code = qmm.DTYPE_F16 if io == "f16" else qmm.DTYPE_F32
+        self.eb = 2 if io == "f16" else 4  # bytes per activation / output element
         self.weights, self.descs_py = [], []
         self.inputs, self.outputs = {}, {}
         widths = {}
@@ -134,7 +139,7 @@ class Workload:
             for (_, _, n, k, inp) in specs:
                 widths[inp] = k
         for inp, k in widths.items():
-            self.inputs[inp] = torch.randn((M, k), device=dev, generator=gen, dtype=torch.float32)
+            self.inputs[inp] = torch.randn((M, k), device=dev, generator=gen, dtype=torch.float32).to(self.io_dtype)
         self.algo_bytes = 0
         self.weight_bytes = 0
         self.flops = 0
@@ -146,12 +151,12 @@ class Workload:
                 self.weights.append(w)
                 key = (pname, n)
                 if key not in self.outputs:
-                    self.outputs[key] = torch.empty((M, n), device=dev, dtype=torch.float32)
+                    self.outputs[key] = torch.empty((M, n), device=dev, dtype=self.io_dtype)
                 if dominant is not None and (t, n, k) == dominant:
                     self.dominant_idx.append(len(self.descs_py))
                 self.descs_py.append((t, self.inputs[inp], w, self.outputs[key], n, k))
                 self.weight_bytes += weight_bytes(t, n, k)
-                self.algo_bytes += weight_bytes(t, n, k) + 4 * M * k + 4 * M * n
+                self.algo_bytes += weight_bytes(t, n, k) + self.eb * M * (k + n)
                 self.flops += 2 * M * n * k
         self.dominant = dominant
 
@@ -161,8 +166,8 @@ class Workload:
         arr = (qmm.GemmDesc * len(self.descs_py))()
         for i, (t, a, w, c, n, k) in enumerate(self.descs_py):
             d = arr[i]
-            d.ggml_type, d.A, d.a_dtype, d.W, d.C, d.c_dtype = t, a.data_ptr(), qmm.DTYPE_F32, w.data_ptr(), \
-                c.data_ptr(), qmm.DTYPE_F32
+            d.ggml_type, d.A, d.a_dtype, d.W, d.C, d.c_dtype = t, a.data_ptr(), self.io_code, w.data_ptr(), \
+                c.data_ptr(), self.io_code
             d.M, d.N, d.K = self.M, n, k
             ev = events.get(i) if events else None
             d.ev_before, d.ev_after = (ev if ev else (None, None))
@@ -505,15 +510,15 @@ def pmc_workload(torch, qmm, dev, gen, reps=8):
     del src, dst
     n, k = 28672, 8192
     ws = [make_weight(torch, Q4_K, n, k, gen, dev) for _ in range(16)]
-    x = torch.randn((1, k), device=dev, generator=gen)
-    ys = [torch.empty((1, n), device=dev) for _ in range(2)]
+    x = torch.randn((1, k), device=dev, generator=gen).half()
+    ys = [torch.empty((1, n), device=dev, dtype=torch.float16) for _ in range(2)]
     pairs = []
     for j in range(0, 16, 2):
         arr = (qmm.GemmDesc * 2)()
         for e in range(2):
             d = arr[e]
-            d.ggml_type, d.A, d.a_dtype, d.W, d.C, d.c_dtype = (Q4_K, x.data_ptr(), qmm.DTYPE_F32, ws[j + e].data_ptr(),
-                                                                ys[e].data_ptr(), qmm.DTYPE_F32)
+            d.ggml_type, d.A, d.a_dtype, d.W, d.C, d.c_dtype = (Q4_K, x.data_ptr(), qmm.DTYPE_F16, ws[j + e].data_ptr(),
+                                                                ys[e].data_ptr(), qmm.DTYPE_F16)
             d.M, d.N, d.K = 1, n, k
         pairs.append(arr)
     for r in range(reps):
@@ -583,7 +588,7 @@ def main():
     gbs = wl.algo_bytes / (ms * 1e-3) / 1e9
     log(f"70B M=1: {ms:.3f} ms/token (median {p50:.3f}, p95 {p95:.3f}), {gbs:.1f} GB/s "
         f"({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM peak), wall {wall:.3f} s for {args.steps} steps")
-    dom_bytes = 2 * weight_bytes(Q4_K, 28672, 8192) + 4 * 8192 + 2 * 4 * 28672
+    dom_bytes = 2 * weight_bytes(Q4_K, 28672, 8192) + wl.eb * (8192 + 2 * 28672)
     dom_us, dom_launches = run_dominant(torch, qmm, hip, wl, max(2, args.steps // 4))
     dom_gbs = dom_bytes / (dom_us * 1e-6) / 1e9
     log(f"dominant kernel (fused gate+up, 2 x Q4_K 28672x8192 GEMV, M=1): {dom_us:.2f} us avg over "
@@ -597,12 +602,13 @@ def main():
         wl4 = Workload.__new__(Workload)
         wl4.__dict__.update(wl.__dict__)
         wl4.M = 4
-        wl4.inputs = {k: torch.randn((4, v.shape[1]), device=dev, generator=gen) for k, v in wl.inputs.items()}
-        wl4.outputs = {k: torch.empty((4, v.shape[1]), device=dev) for k, v in wl.outputs.items()}
+        wl4.inputs = {k: torch.randn((4, v.shape[1]), device=dev, generator=gen).to(wl.io_dtype)
+                      for k, v in wl.inputs.items()}
+        wl4.outputs = {k: torch.empty((4, v.shape[1]), device=dev, dtype=wl.io_dtype) for k, v in wl.outputs.items()}
         remap_in = {id(wl.inputs[k]): wl4.inputs[k] for k in wl.inputs}
         remap_out = {id(wl.outputs[k]): wl4.outputs[k] for k in wl.outputs}
         wl4.descs_py = [(t, remap_in[id(a)], w, remap_out[id(c)], n, k) for (t, a, w, c, n, k) in wl.descs_py]
-        wl4.algo_bytes = sum(weight_bytes(t, n, k) + 16 * k + 16 * n for (t, _, _, _, n, k) in wl4.descs_py)
+        wl4.algo_bytes = sum(weight_bytes(t, n, k) + 4 * wl.eb * (k + n) for (t, _, _, _, n, k) in wl4.descs_py)
         ms4, _ = run_workload(torch, qmm, hip, wl4, max(3, args.steps // 2), 2)
         extra["70b_q4_k_m_m4"] = {"GB/s": round(wl4.algo_bytes / (ms4 * 1e-3) / 1e9, 1), "ms_per_token": round(ms4, 3),
                                   "frac_hbm": round(wl4.algo_bytes / (ms4 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
@@ -664,7 +670,7 @@ def main():
             log(f"embed {label}: {extra[f'8b_q6_k_embed_{label}']}")
         lm.free()
         del lm
-        q40 = Workload(torch, qmm, "q4_0", [[("w", Q4_0, 4096, 4096, "h")]], 128, 1, dev, gen)
+        q40 = Workload(torch, qmm, "q4_0", [[("w", Q4_0, 4096, 4096, "h")]], 128, 1, dev, gen, io="f32")
         msq, _ = run_workload(torch, qmm, hip, q40, args.steps, args.warmup)
         g = q40.algo_bytes / (msq * 1e-3) / 1e9
         extra["q4_0_4096x4096_m1"] = {"GB/s": round(g, 1), "us": round(msq * 1e3 / 128, 2),
@@ -693,8 +699,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
-        "dtype_detail": "fp32 activations rounded to f16 when staged; Q4_K/Q6_K codes as exact f16; "
-                        "f16 x f16 products (v_dot2_f32_f16) accumulated in fp32",
+        "dtype_detail": "fp16 activations and outputs (the reference API's dtype); Q4_K/Q6_K codes as exact "
+                        "f16; f16 x f16 products (v_dot2_f32_f16) accumulated in fp32",
         "data": "synthetic: random packed blocks (fp16 scales |N(0,1)|*0.01), x ~ N(0,1)",
         "config": {"workload": "llama3-70b-q4_k_m-decode-m1-80-layers", "layers": args.layers, "M": 1,
                    "hidden": 8192, "intermediate": 28672, "kv_dim": 1024,
