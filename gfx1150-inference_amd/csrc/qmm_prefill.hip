@@ -361,13 +361,16 @@ struct PF16 {
 // Output segments of one launch: consecutive weight matrices that multiply the same activations
 // (q/k/v, gate/up).  Their n-tiles are concatenated; tile_end[s] is the cumulative n-tile count
 // through segment s (INT_MAX for unused entries), part_off[s] the offset of segment s's split-K
-// partial block ([ksplit][M][N_s] fp32) in the partial workspace.
+// partial block ([ksplit][M][N_s] fp32) in the partial workspace.  Segment s computes columns
+// [0, N_s) of a C block whose rows are ldc[s] elements apart (a column range of a wider C when
+// a launch covers only some of a matrix's rows).
 constexpr int kPfMaxSegs = 4;
 template <typename TC>
 struct PfSegs {
     const uint8_t* W[kPfMaxSegs];
     TC* C[kPfMaxSegs];
     int N[kPfMaxSegs];
+    int ldc[kPfMaxSegs];
     int tile_end[kPfMaxSegs];
     size_t part_off[kPfMaxSegs];
 };
@@ -436,6 +439,7 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
     const uint8_t* __restrict__ W = sg.W[sgi];
     TC* __restrict__ C = sg.C[sgi];
     const int N = sg.N[sgi];
+    const int ldc = sg.ldc[sgi];
     float* __restrict__ part = part_base + sg.part_off[sgi];
     const int m0 = tm * kBM, n0 = tn * kBN;
     const int kb = kz * klen;
@@ -580,8 +584,8 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     if (n + e < N) {
-                        if constexpr (sizeof(TC) == 4) reinterpret_cast<float*>(C)[static_cast<size_t>(m) * N + n + e] = vs[e];
-                        else reinterpret_cast<uint16_t*>(C)[static_cast<size_t>(m) * N + n + e] = float_to_half_bits(vs[e]);
+                        if constexpr (sizeof(TC) == 4) reinterpret_cast<float*>(C)[static_cast<size_t>(m) * ldc + n + e] = vs[e];
+                        else reinterpret_cast<uint16_t*>(C)[static_cast<size_t>(m) * ldc + n + e] = float_to_half_bits(vs[e]);
                     }
                 }
             }
@@ -652,6 +656,7 @@ void prefill_wide_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> s
     const uint8_t* __restrict__ W = sg.W[sgi];
     TC* __restrict__ C = sg.C[sgi];
     const int N = sg.N[sgi];
+    const int ldc = sg.ldc[sgi];
     float* __restrict__ part = part_base + sg.part_off[sgi];
     const int m0 = tm * kWBM, n0 = tn * kWBN;
     const int kb = kz * klen;
@@ -814,8 +819,8 @@ void prefill_wide_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> s
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         if (n + e < N) {
-                            if constexpr (sizeof(TC) == 4) reinterpret_cast<float*>(C)[static_cast<size_t>(m) * N + n + e] = vs[e];
-                            else reinterpret_cast<uint16_t*>(C)[static_cast<size_t>(m) * N + n + e] = float_to_half_bits(vs[e]);
+                            if constexpr (sizeof(TC) == 4) reinterpret_cast<float*>(C)[static_cast<size_t>(m) * ldc + n + e] = vs[e];
+                            else reinterpret_cast<uint16_t*>(C)[static_cast<size_t>(m) * ldc + n + e] = float_to_half_bits(vs[e]);
                         }
                     }
                 }
@@ -846,16 +851,19 @@ __global__ __launch_bounds__(256) void to_f16_kernel(const TA* __restrict__ A, _
     __builtin_memcpy(out + static_cast<size_t>(m) * lda + k, v, 16);
 }
 
-// C = sum_z part[z] in a fixed order.
+// C[m, n] (rows ldc apart) = sum_z part[z][m][n] in a fixed order, for part blocks [ksplit][M][N].
 template <typename TC>
-__global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ part, TC* __restrict__ C, int64_t mn,
-                                                     int ksplit) {
+__global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ part, TC* __restrict__ C, int M, int N,
+                                                     int ldc, int ksplit) {
+    const int64_t mn = static_cast<int64_t>(M) * N;
     const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (i >= mn) return;
     float s = part[i];
     for (int z = 1; z < ksplit; ++z) s += part[static_cast<size_t>(z) * mn + i];
-    if constexpr (sizeof(TC) == 4) C[i] = s;
-    else reinterpret_cast<uint16_t*>(C)[i] = float_to_half_bits(s);
+    const int64_t m = i / N;
+    const size_t o = static_cast<size_t>(m) * ldc + static_cast<size_t>(i - m * N);
+    if constexpr (sizeof(TC) == 4) C[o] = s;
+    else reinterpret_cast<uint16_t*>(C)[o] = float_to_half_bits(s);
 }
 
 // Grow-only device workspace per (device, stream): the f16 copy of the activations and the
@@ -948,12 +956,88 @@ struct PfSeg {
     const void* W;
     void* C;
     int N;
+    int ldc;  // elements between rows of C (N for a whole matrix)
 };
+
+// One launch of the 128 x 256 (Wide = false) or 256 x 256 (Wide = true) tile kernel over `segs`
+// with K split `ksplit` ways (at most; the split length is a whole number of steps), then, for a
+// split, the pass that adds the partial tiles (at `part`) into C.
+template <class P, typename TC, bool Wide>
+hipError_t launch_grid(const _Float16* a16, int lda, const PfSeg* segs, int nseg, int M, int K, int ksplit,
+                       float* part, hipStream_t stream) {
+    constexpr int BM = Wide ? kWBM : kBM, BN = Wide ? kWBN : kBN, BK = Wide ? kWBK : kBK;
+    constexpr int threads = Wide ? kWThreads : kThreads;
+    const int tiles_m = (M + BM - 1) / BM;
+    const int steps = (K + BK - 1) / BK;
+    const int klen = ((steps + ksplit - 1) / ksplit) * BK;
+    ksplit = (steps * BK + klen - 1) / klen;
+    PfSegs<TC> sg;
+    size_t off = 0;
+    int tiles_n = 0;
+    for (int i = 0; i < kPfMaxSegs; ++i) {
+        const bool used = i < nseg;
+        sg.W[i] = used ? static_cast<const uint8_t*>(segs[i].W) : nullptr;
+        sg.C[i] = used ? static_cast<TC*>(segs[i].C) : nullptr;
+        sg.N[i] = used ? segs[i].N : 0;
+        sg.ldc[i] = used ? segs[i].ldc : 0;
+        if (used) tiles_n += (segs[i].N + BN - 1) / BN;
+        sg.tile_end[i] = used ? tiles_n : INT_MAX;
+        sg.part_off[i] = off;
+        if (used && ksplit > 1) off += static_cast<size_t>(ksplit) * M * segs[i].N;
+    }
+    const int tiles = tiles_m * tiles_n * ksplit;
+    if constexpr (Wide)
+        hipLaunchKernelGGL((prefill_wide_kernel<P, TC>), dim3(tiles), dim3(threads), 0, stream, a16, lda, sg,
+                           ksplit > 1 ? part : nullptr, M, K, klen, tiles_m, tiles_n, ksplit);
+    else
+        hipLaunchKernelGGL((prefill_kernel<P, TC>), dim3(tiles), dim3(threads), 0, stream, a16, lda, sg,
+                           ksplit > 1 ? part : nullptr, M, K, klen, tiles_m, tiles_n, ksplit);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (ksplit > 1) {
+        for (int i = 0; i < nseg; ++i) {
+            const int64_t mn = static_cast<int64_t>(M) * segs[i].N;
+            hipLaunchKernelGGL((reduce_kernel<TC>), dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, stream,
+                               part + sg.part_off[i], sg.C[i], M, segs[i].N, segs[i].ldc, ksplit);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
+    }
+    return hipSuccess;
+}
+
+// Launch plan.  While the tiles cover at most half the CUs, K is split over the whole grid
+// (doubling, keeping at least 1024 k per split).  Otherwise, when the tiles fill the CUs at
+// least once and leave a last round of at most half the CUs (e.g. 896 tiles on 256 CUs), the
+// last `tail_n` n-tiles (all m) run as a second launch with K split `tail_ks` ways, so that
+// round's work is spread over all CUs: whole rounds first, then the split tail and its
+// partial-sum pass over those columns only.  Wide tile only, for K of at least 32 steps (a
+// shorter split saves less than its partial sums cost).
+struct PfPlan {
+    int ksplit = 1;
+    int tail_n = 0;
+    int tail_ks = 1;
+};
+
+PfPlan plan_prefill(bool wide, int tiles_m, int tiles_n, int steps, int bk, int cus) {
+    PfPlan p;
+    while (tiles_m * tiles_n * p.ksplit * 2 <= cus && steps / (p.ksplit * 2) >= 1024 / bk) p.ksplit *= 2;
+    if (!wide || p.ksplit > 1 || steps < 32) return p;
+    const int64_t T = static_cast<int64_t>(tiles_m) * tiles_n;
+    const int64_t r = T % cus;
+    if (T <= cus || r == 0 || 2 * r > cus) return p;
+    const int tail_n = static_cast<int>((r + tiles_m - 1) / tiles_m);
+    if (tail_n >= tiles_n) return p;
+    int ks = static_cast<int>(cus / (static_cast<int64_t>(tiles_m) * tail_n));
+    while (ks > 1 && steps / ks < 1024 / bk) --ks;
+    if (ks < 2) return p;
+    p.tail_n = tail_n;
+    p.tail_ks = ks;
+    return p;
+}
 
 template <class P, typename TA, typename TC, bool Wide>
 hipError_t launch_p(const void* A, const PfSeg* segs, int nseg, int M, int K, hipStream_t stream) {
     constexpr int BM = Wide ? kWBM : kBM, BN = Wide ? kWBN : kBN, BK = Wide ? kWBK : kBK;
-    constexpr int threads = Wide ? kWThreads : kThreads;
     int cus = 0;
     hipError_t e = cu_count(cus);
     if (e != hipSuccess) return e;
@@ -965,17 +1049,35 @@ hipError_t launch_p(const void* A, const PfSeg* segs, int nseg, int M, int K, hi
         n_total += segs[i].N;
     }
     const int steps = (K + BK - 1) / BK;
-    // split K while the grid would still cover at most half the CUs (the partial-sum pass costs
-    // 4 * (ksplit + 1) * M * N bytes), keeping at least 1024 k per split
-    int ksplit = 1;
-    while (tiles_m * tiles_n * ksplit * 2 <= cus && steps / (ksplit * 2) >= 1024 / BK) ksplit *= 2;
-    const int klen = ((steps + ksplit - 1) / ksplit) * BK;
-    ksplit = (steps * BK + klen - 1) / klen;
+    const PfPlan plan = plan_prefill(Wide, tiles_m, tiles_n, steps, BK, cus);
+
+    // the tail launch's segments: rows from n-tile ns on, as column ranges of the callers' C
+    PfSeg main_segs[kPfMaxSegs], tail_segs[kPfMaxSegs];
+    int n_main = 0, n_tail = 0;
+    int64_t n_tail_total = 0;
+    if (plan.tail_n > 0) {
+        const int ns = tiles_n - plan.tail_n;
+        const size_t row_bytes = static_cast<size_t>(K / P::kQK) * P::kBytes;
+        int a = 0;
+        for (int i = 0; i < nseg; ++i) {
+            const int t = (segs[i].N + BN - 1) / BN;
+            if (a < ns) main_segs[n_main++] = PfSeg{segs[i].W, segs[i].C, min(segs[i].N, (ns - a) * BN), segs[i].ldc};
+            if (a + t > ns) {
+                const int r0 = max(0, ns - a) * BN;
+                tail_segs[n_tail++] = PfSeg{static_cast<const uint8_t*>(segs[i].W) + static_cast<size_t>(r0) * row_bytes,
+                                            static_cast<TC*>(segs[i].C) + r0, segs[i].N - r0, segs[i].ldc};
+                n_tail_total += segs[i].N - r0;
+            }
+            a += t;
+        }
+    }
 
     const bool direct = sizeof(TA) == 2 && K % BK == 0 && (reinterpret_cast<uintptr_t>(A) & 15u) == 0;
     const int lda = direct ? K : steps * BK;
     const size_t a_bytes = direct ? 0 : static_cast<size_t>(M) * lda * 2;
-    const size_t p_bytes = ksplit > 1 ? static_cast<size_t>(ksplit) * M * n_total * 4 : 0;
+    size_t p_bytes = 0;
+    if (plan.ksplit > 1) p_bytes = static_cast<size_t>(plan.ksplit) * M * n_total * 4;
+    if (plan.tail_n > 0) p_bytes = static_cast<size_t>(plan.tail_ks) * M * n_tail_total * 4;
     void* ws = nullptr;
     if (a_bytes + p_bytes > 0 && (e = workspace(stream, a_bytes + p_bytes + 256, &ws)) != hipSuccess) return e;
     const _Float16* a16 = static_cast<const _Float16*>(A);
@@ -987,37 +1089,10 @@ hipError_t launch_p(const void* A, const PfSeg* segs, int nseg, int M, int K, hi
         if ((e = hipGetLastError()) != hipSuccess) return e;
         a16 = dst;
     }
-    float* part = ksplit > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + ((a_bytes + 255) / 256) * 256) : nullptr;
-    PfSegs<TC> sg;
-    size_t off = 0;
-    int tiles_acc = 0;
-    for (int i = 0; i < kPfMaxSegs; ++i) {
-        const bool used = i < nseg;
-        sg.W[i] = used ? static_cast<const uint8_t*>(segs[i].W) : nullptr;
-        sg.C[i] = used ? static_cast<TC*>(segs[i].C) : nullptr;
-        sg.N[i] = used ? segs[i].N : 0;
-        if (used) tiles_acc += (segs[i].N + BN - 1) / BN;
-        sg.tile_end[i] = used ? tiles_acc : INT_MAX;
-        sg.part_off[i] = off;
-        if (used && ksplit > 1) off += static_cast<size_t>(ksplit) * M * segs[i].N;
-    }
-    const int tiles = tiles_m * tiles_n * ksplit;
-    if constexpr (Wide)
-        hipLaunchKernelGGL((prefill_wide_kernel<P, TC>), dim3(tiles), dim3(threads), 0, stream, a16, lda, sg, part, M, K,
-                           klen, tiles_m, tiles_n, ksplit);
-    else
-        hipLaunchKernelGGL((prefill_kernel<P, TC>), dim3(tiles), dim3(threads), 0, stream, a16, lda, sg, part, M, K, klen,
-                           tiles_m, tiles_n, ksplit);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    if (ksplit > 1) {
-        for (int i = 0; i < nseg; ++i) {
-            const int64_t mn = static_cast<int64_t>(M) * segs[i].N;
-            hipLaunchKernelGGL((reduce_kernel<TC>), dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, stream,
-                               part + sg.part_off[i], sg.C[i], mn, ksplit);
-            if ((e = hipGetLastError()) != hipSuccess) return e;
-        }
-    }
-    return hipSuccess;
+    float* part = p_bytes > 0 ? reinterpret_cast<float*>(static_cast<char*>(ws) + ((a_bytes + 255) / 256) * 256) : nullptr;
+    if (plan.tail_n == 0) return launch_grid<P, TC, Wide>(a16, lda, segs, nseg, M, K, plan.ksplit, part, stream);
+    if ((e = launch_grid<P, TC, Wide>(a16, lda, main_segs, n_main, M, K, 1, nullptr, stream)) != hipSuccess) return e;
+    return launch_grid<P, TC, Wide>(a16, lda, tail_segs, n_tail, M, K, plan.tail_ks, part, stream);
 }
 
 template <template <int> class PF, typename TA, typename TC>
@@ -1069,7 +1144,7 @@ bool gemm_prefill_supported(int ggml_type, int a_dtype, int c_dtype, int M, int 
 
 hipError_t launch_gemm_prefill(int ggml_type, const void* A, int a_dtype, const void* W, void* C, int c_dtype, int M,
                                int N, int K, hipStream_t stream) {
-    const PfSeg seg{W, C, N};
+    const PfSeg seg{W, C, N, N};
     return dispatch_dtypes(ggml_type, A, a_dtype, c_dtype, &seg, 1, M, K, stream);
 }
 
@@ -1079,7 +1154,7 @@ hipError_t launch_gemm_prefill_fused(int ggml_type, const void* A, int a_dtype, 
                                      const void* const* W, void* const* C, const int* N, int count, hipStream_t stream) {
     if (count < 1 || count > kPfMaxSegs) return hipErrorInvalidValue;
     PfSeg segs[kPfMaxSegs];
-    for (int i = 0; i < count; ++i) segs[i] = PfSeg{W[i], C[i], N[i]};
+    for (int i = 0; i < count; ++i) segs[i] = PfSeg{W[i], C[i], N[i], N[i]};
     return dispatch_dtypes(ggml_type, A, a_dtype, c_dtype, segs, count, M, K, stream);
 }
 

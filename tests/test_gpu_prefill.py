@@ -7,7 +7,10 @@ Bars (written into each check):
   accumulation differs), which pins dequantization, scale rounding and the k ordering;
 * edge shapes: M, N not multiples of the 128 x 256 tile (M < 256) or of the 256 x 256 wide tile
   (M >= 256), K tails of 32 for Q4_0 / Q8_0, split K, fp16 and fp32 activations and outputs; the
-  Llama-3-8B prefill shapes (M = 512) on sampled rows.
+  Llama-3-8B prefill shapes (M = 512) on sampled rows;
+* a wide grid whose last round is split over K in a second launch (single matrices and fused
+  pairs with the split inside either matrix): fp16 outputs within 1e-3 of the f16-operand
+  product (one more rounding of each result) and of single calls.
 """
 
 import zlib
@@ -150,6 +153,87 @@ def test_prefill_full_size_m512(dev, name, t, N, K):
     sub = np.concatenate([raw[r * rb:(r + 1) * rb] for r in rows])
     assert O.max_rel_err(y[:, rows], O.matmul_f64(t, x, sub, rows.size, K)) <= TOL_F64
     assert O.max_rel_err(y[:, rows], O.matmul_f16_operands(t, x, sub, rows.size, K)) <= TOL_F16
+
+
+def tail_cols(rng, N, split):
+    # sampled columns plus those around the n-tile where the tail launch starts
+    cols = set(sampled_cols(rng, N).tolist()) | {split - 2, split - 1, split, split + 1, split + 255, split + 256}
+    return np.array(sorted(c for c in cols if 0 <= c < N))
+
+
+def check_cols(t, x, raw, y, cols, K, tol_b, what):
+    rb = O.weight_bytes(t, 1, K)
+    sub = np.concatenate([raw[r * rb:(r + 1) * rb] for r in cols])
+    ys = y[:, cols]
+    assert np.all(np.isfinite(y)), what
+    assert O.max_rel_err(ys, O.matmul_f64(t, x, sub, cols.size, K)) <= TOL_F64, what
+    assert O.max_rel_err(ys, O.matmul_f16_operands(t, x, sub, cols.size, K)) <= tol_b, what
+
+
+@pytest.mark.parametrize("t", [O.GGML_Q4_K, O.GGML_Q6_K, O.GGML_Q8_0])
+def test_prefill_wide_tail_split(dev, t):
+    # cus + 40 wide tiles (M = 256, a ragged last tile, K = 4096: 32 steps of 128) fill the CUs
+    # once and leave a last round of 40 tiles.  Those n-tiles run as a second launch with K split
+    # over the CUs; its partial tiles are summed into that column range of C.  Checked on
+    # columns of the first, the split-adjacent and the last tiles, with fp16 in and out (f16
+    # activations read in place) and fp32 in and out (an f16 copy in the same workspace as the
+    # partial tiles).
+    import torch
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    rng = np.random.default_rng(4400 + t)
+    M, K = 256, 4096
+    N = (cus + 40) * 256 - 100
+    raw = O.synth_weights(t, N, K, rng)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    for a16, c16 in ((True, True), (False, False)):
+        y = run(t, x, raw, N, K, dev, a16=a16, c16=c16)
+        xa = x.astype(np.float16).astype(np.float32) if a16 else x
+        check_cols(t, xa, raw, y, tail_cols(rng, N, cus * 256), K, 1e-3 if c16 else TOL_F16,
+                   (O.TYPE_NAMES[t], a16, c16))
+
+
+@pytest.mark.parametrize("tiles", ["tail_inside_first", "tail_inside_second"])
+def test_prefill_wide_tail_split_fused_segments(dev, tiles):
+    # Two matrices on one input through qmm_gemm_batch (one fused launch of cus + 40 wide
+    # tiles): the tail starts inside the first matrix (its last 14 n-tiles and all of the
+    # second are split), or inside the second (whose first tiles run unsplit).  The first
+    # matrix of the second case ends in a ragged tile.  fp16 outputs match single calls (which
+    # plan their own splits, so the fp32 sums may round differently) and the f16-operand product
+    # on sampled columns within 1e-3: one more rounding of each result.
+    import torch
+    import qmm
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    t = O.GGML_Q4_K
+    rng = np.random.default_rng(4500 + len(tiles))
+    M, K = 256, 4096
+    if tiles == "tail_inside_first":
+        ns = [(cus + 14) * 256, 26 * 256 - 50]
+    else:
+        ns = [150 * 256 - 10, (cus + 40 - 150) * 256]
+    split = cus * 256  # first column (in the concatenated rows) of the tail launch
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    A = to_dev(x, dev)
+    raws = [O.synth_weights(t, n, K, rng) for n in ns]
+    Ws = [to_dev(r, dev) for r in raws]
+    Cs = [torch.empty((M, n), device=dev, dtype=torch.float16) for n in ns]
+    arr = (qmm.GemmDesc * 2)()
+    for d, w, c, n in zip(arr, Ws, Cs, ns):
+        d.ggml_type, d.A, d.a_dtype, d.W, d.C, d.c_dtype = t, A.data_ptr(), qmm.DTYPE_F16, w.data_ptr(), \
+            c.data_ptr(), qmm.DTYPE_F16
+        d.M, d.N, d.K = M, n, K
+        d.ev_before = d.ev_after = None
+    qmm.gemm_batch(arr)
+    torch.cuda.synchronize()
+    off = 0
+    for raw, w, c, n in zip(raws, Ws, Cs, ns):
+        y = c.float().cpu().numpy().astype(np.float64)
+        ref = qmm.gemm(t, A, w, n, K, out_dtype=torch.float16)
+        torch.cuda.synchronize()
+        assert O.max_rel_err(y, ref.float().cpu().numpy().astype(np.float64)) <= 1e-3, (tiles, n)
+        local = split - off  # the tail's first column inside this matrix (may lie outside it)
+        check_cols(t, x.astype(np.float32), raw, y, tail_cols(rng, n, min(max(local, 2), n - 2)), K, 1e-3,
+                   (tiles, n))
+        off += n
 
 
 def test_prefill_workspace_release_and_regrow(dev):
