@@ -47,8 +47,8 @@ namespace {
 
 constexpr int kBM = 128;        // activation rows per workgroup tile
 constexpr int kBN = 256;        // weight rows per workgroup tile (32 per wave)
-constexpr int kHalves = 4;      // 64-k halves per step
-constexpr int kBK = 64 * kHalves;  // k per step (one Q4_K / Q6_K super-block)
+constexpr int kHalves = 4;      // 64-k halves per step of the quantized producers (one Q4_K / Q6_K
+                                // super-block); F16 steps take 2 (its raw rows are 3.6x larger)
 constexpr int kThreads = 512;   // 8 waves: two per SIMD, so one wave's load stalls are covered
 constexpr int kChunksPerHalf = kBM * 64 / 8;  // 16-byte chunks (8 f16) per 64-k half stage = 1024
 
@@ -112,6 +112,7 @@ __device__ __forceinline__ uint32_t affine(h2 c, h2 a, h2 b) { return as_u32(__b
 // ---------------------------------------------------------------------------------------------
 template <int H>
 struct PQ4K {
+    static constexpr int kH = H;
     static_assert(H == 2 || H == 4, "steps of 128 or 256 k");
     static constexpr int kQK = kQK_K, kBytes = kBytesQ4_K;
     struct Raw { u32x4p hd, q[H]; };
@@ -174,6 +175,7 @@ struct PQ4K {
 
 template <int H>
 struct PQ6K {
+    static constexpr int kH = H;
     static_assert(H == 2 || H == 4, "steps of 128 or 256 k");
     static constexpr int kQK = kQK_K, kBytes = kBytesQ6_K;
     struct Raw { u32x4p la[H / 2], lb[H / 2], qh[H / 2]; uint32_t sc[H], d; };
@@ -241,6 +243,7 @@ struct PQ6K {
 // holds blocks 2U (S = 0, 1) and 2U + 1 (S = 2, 3).
 template <int H>
 struct PQ80 {
+    static constexpr int kH = H;
     static constexpr int kQK = kQK8_0, kBytes = kBytesQ8_0;
     struct Raw { u32x4p q[2 * H]; uint32_t d[2 * H]; };
     struct Sc { h2 a0, a1; };
@@ -281,6 +284,7 @@ struct PQ80 {
 
 template <int H>
 struct PQ40 {
+    static constexpr int kH = H;
     static constexpr int kQK = kQK4_0, kBytes = kBytesQ4_0;
     struct Raw { u32x4p q[2 * H]; uint32_t d[2 * H]; };
     struct Sc { h2 a0, a1; };
@@ -326,6 +330,7 @@ struct PQ40 {
 // bytes (a valid address) and is zeroed in scales(), when its sub-step comes.
 template <int H>
 struct PF16 {
+    static constexpr int kH = H;
     static constexpr int kQK = 8, kBytes = 16;  // row bytes = K / 8 * 16 = 2K
     struct Raw { u32x4p w[H][4]; };
     struct Sc { uint32_t keep[4]; };
@@ -425,7 +430,9 @@ template <class P, typename TC>
 __global__ __launch_bounds__(kThreads, 1)
 void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, float* __restrict__ part_base, int M, int K,
                     int klen, int tiles_m, int tiles_n, int ksplit) {
-    __shared__ __align__(16) u32x4p sA[2][kHalves * kChunksPerHalf];
+    constexpr int kH = P::kH;      // 64-k halves per step
+    constexpr int kBK = 64 * kH;   // k per step
+    __shared__ __align__(16) u32x4p sA[2][kH * kChunksPerHalf];
 
     // Tile order: m fastest, then n-tile, then k split; blocks sharing a weight slice (same
     // n-tile and k range, different m) are consecutive and dealt to one XCD.
@@ -468,16 +475,16 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
         arow[j] = A16 + static_cast<size_t>(min(m0 + r, M - 1)) * lda + kb + 8 * c;
         apos[j] = p;
     }
-    auto load_a = [&](int t, u32x4p (&ar)[2 * kHalves]) {
+    auto load_a = [&](int t, u32x4p (&ar)[2 * kH]) {
         const int kk = min(t, nsteps - 1) * kBK;  // past the end: re-read the last step
 #pragma unroll
-        for (int u = 0; u < kHalves; ++u)
+        for (int u = 0; u < kH; ++u)
 #pragma unroll
             for (int j = 0; j < 2; ++j) ar[2 * u + j] = *reinterpret_cast<const u32x4p*>(arow[j] + kk + 64 * u);
     };
-    auto store_a = [&](int slot, const u32x4p (&ar)[2 * kHalves]) {
+    auto store_a = [&](int slot, const u32x4p (&ar)[2 * kH]) {
 #pragma unroll
-        for (int u = 0; u < kHalves; ++u)
+        for (int u = 0; u < kH; ++u)
 #pragma unroll
             for (int j = 0; j < 2; ++j) sA[slot][kChunksPerHalf * u + apos[j]] = ar[2 * u + j];
     };
@@ -501,20 +508,22 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
 
-    // Software pipeline.  Step t (k0 = kb + 256t) runs sub-steps q = 0..15 (U = q/4, S = q%4).
-    // While the 4 MFMAs of sub-step q run on wf[q&1] / af[q&1], the wave reads the activation
-    // fragments of q+1 from LDS and dequantizes its weight fragment into the other buffers.
+    // Software pipeline.  Step t (k0 = kb + kBK t) runs sub-steps q = 0..Q-1 (Q = 4 kH: 16 for
+    // the quantized formats, 8 for F16; U = q/4, S = q%4).  While the 4 MFMAs of sub-step q run
+    // on wf[q&1] / af[q&1], the wave reads the activation fragments of q+1 from LDS and
+    // dequantizes its weight fragment into the other buffers.
     //   q = 0: the raw bytes of step t+1 (into `nxt`) and A(t+1) (into `an`) are requested;
-    //   q = 4U+1 (U < 3): scales of half U+1 (from `cur`) into sc[(U+1)&1];
-    //   q = 13: scales of the next step's half 0 (from `nxt`) into sc[0];
-    //   q = 14: after the reads for q = 15, A(t+1) goes to the free LDS slot, then the barrier
-    //           (after it, q = 15 reads the next step's first fragments from that slot);
-    //   q = 15: fragment of the next step's (0, 0) from `nxt`; at the end `cur` takes `nxt`.
+    //   q = 4U+1 (U < kH-1): scales of half U+1 (from `cur`) into sc[(U+1)&1];
+    //   q = Q-3: scales of the next step's half 0 (from `nxt`) into sc[0] (its last use in this
+    //           step, by half kH-2's fragments, is at q = Q-6);
+    //   q = Q-2: after the reads for q = Q-1, A(t+1) goes to the free LDS slot, then the barrier
+    //           (after it, q = Q-1 reads the next step's first fragments from that slot);
+    //   q = Q-1: fragment of the next step's (0, 0) from `nxt`; at the end `cur` takes `nxt`.
     // The LDS slot (t+1)%2 last served step t-1, whose reads all precede step t-1's barrier, so
     // one barrier per step covers both the write-after-read and the read-after-write order.
     using Raw = typename P::Raw;
     using Sc = typename P::Sc;
-    u32x4p an[2 * kHalves];
+    u32x4p an[2 * kH];
     Raw cur, nxt;
     Sc sc[2];          // [half]
     uint32_t wf[2][4]; // [buffer][dword]
@@ -536,7 +545,7 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
         load_a(t + 1, an);
         __builtin_amdgcn_sched_barrier(0);
 
-        constexpr int kQ = 4 * kHalves;  // sub-steps per step
+        constexpr int kQ = 4 * kH;  // sub-steps per step
         auto sub = [&](auto qc) {
             constexpr int q = decltype(qc)::value;
             constexpr int U = q >> 2, B = q & 1;
@@ -549,10 +558,10 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
                 lds_barrier();
             }
             if constexpr (qn == kQ) read_a(slot ^ 1, 0, 0, af[B ^ 1]);
-            if constexpr ((q & 3) == 1 && U + 1 < kHalves)
-                sc[(U + 1) & 1] = P::template scales<(U + 1) % kHalves>(cur, k0, h, kend - k0);
+            if constexpr ((q & 3) == 1 && U + 1 < kH)
+                sc[(U + 1) & 1] = P::template scales<(U + 1) % kH>(cur, k0, h, kend - k0);
             if constexpr (q == kQ - 3) sc[0] = P::template scales<0>(nxt, k0 + kBK, h, kend - k0 - kBK);
-            if constexpr (qn < kQ) P::template frag<Un % kHalves, Sn>(cur, sc[Un & 1], h, wf[B ^ 1]);
+            if constexpr (qn < kQ) P::template frag<Un % kH, Sn>(cur, sc[Un & 1], h, wf[B ^ 1]);
             else P::template frag<0, 0>(nxt, sc[0], h, wf[B ^ 1]);
             f16x8 bw;
             __builtin_memcpy(&bw, wf[B], 16);
@@ -965,7 +974,7 @@ struct PfSeg {
 template <class P, typename TC, bool Wide>
 hipError_t launch_grid(const _Float16* a16, int lda, const PfSeg* segs, int nseg, int M, int K, int ksplit,
                        float* part, hipStream_t stream) {
-    constexpr int BM = Wide ? kWBM : kBM, BN = Wide ? kWBN : kBN, BK = Wide ? kWBK : kBK;
+    constexpr int BM = Wide ? kWBM : kBM, BN = Wide ? kWBN : kBN, BK = Wide ? kWBK : 64 * P::kH;
     constexpr int threads = Wide ? kWThreads : kThreads;
     const int tiles_m = (M + BM - 1) / BM;
     const int steps = (K + BK - 1) / BK;
@@ -1037,7 +1046,7 @@ PfPlan plan_prefill(bool wide, int tiles_m, int tiles_n, int steps, int bk, int 
 
 template <class P, typename TA, typename TC, bool Wide>
 hipError_t launch_p(const void* A, const PfSeg* segs, int nseg, int M, int K, hipStream_t stream) {
-    constexpr int BM = Wide ? kWBM : kBM, BN = Wide ? kWBN : kBN, BK = Wide ? kWBK : kBK;
+    constexpr int BM = Wide ? kWBM : kBM, BN = Wide ? kWBN : kBN, BK = Wide ? kWBK : 64 * P::kH;
     int cus = 0;
     hipError_t e = cu_count(cus);
     if (e != hipSuccess) return e;
@@ -1095,7 +1104,8 @@ hipError_t launch_p(const void* A, const PfSeg* segs, int nseg, int M, int K, hi
     return launch_grid<P, TC, Wide>(a16, lda, tail_segs, n_tail, M, K, plan.tail_ks, part, stream);
 }
 
-template <template <int> class PF, typename TA, typename TC>
+// HN: 64-k halves per step of the 128 x 256 kernel for this format.
+template <template <int> class PF, int HN, typename TA, typename TC>
 hipError_t launch_family(const void* A, const PfSeg* segs, int nseg, int M, int K, hipStream_t stream) {
     int cus = 0;
     hipError_t e = cu_count(cus);
@@ -1103,17 +1113,17 @@ hipError_t launch_family(const void* A, const PfSeg* segs, int nseg, int M, int 
     int64_t wide_tiles_n = 0;
     for (int i = 0; i < nseg; ++i) wide_tiles_n += (segs[i].N + kWBN - 1) / kWBN;
     if (use_wide(M, wide_tiles_n, K, cus)) return launch_p<PF<kWH>, TA, TC, true>(A, segs, nseg, M, K, stream);
-    return launch_p<PF<kHalves>, TA, TC, false>(A, segs, nseg, M, K, stream);
+    return launch_p<PF<HN>, TA, TC, false>(A, segs, nseg, M, K, stream);
 }
 
 template <typename TA, typename TC>
 hipError_t dispatch_p(int t, const void* A, const PfSeg* segs, int nseg, int M, int K, hipStream_t stream) {
     switch (t) {
-        case QMM_TYPE_Q4_K: return launch_family<PQ4K, TA, TC>(A, segs, nseg, M, K, stream);
-        case QMM_TYPE_Q6_K: return launch_family<PQ6K, TA, TC>(A, segs, nseg, M, K, stream);
-        case QMM_TYPE_Q8_0: return launch_family<PQ80, TA, TC>(A, segs, nseg, M, K, stream);
-        case QMM_TYPE_Q4_0: return launch_family<PQ40, TA, TC>(A, segs, nseg, M, K, stream);
-        case QMM_TYPE_F16: return launch_family<PF16, TA, TC>(A, segs, nseg, M, K, stream);
+        case QMM_TYPE_Q4_K: return launch_family<PQ4K, kHalves, TA, TC>(A, segs, nseg, M, K, stream);
+        case QMM_TYPE_Q6_K: return launch_family<PQ6K, kHalves, TA, TC>(A, segs, nseg, M, K, stream);
+        case QMM_TYPE_Q8_0: return launch_family<PQ80, kHalves, TA, TC>(A, segs, nseg, M, K, stream);
+        case QMM_TYPE_Q4_0: return launch_family<PQ40, kHalves, TA, TC>(A, segs, nseg, M, K, stream);
+        case QMM_TYPE_F16: return launch_family<PF16, 2, TA, TC>(A, segs, nseg, M, K, stream);
         default: return hipErrorInvalidValue;
     }
 }
