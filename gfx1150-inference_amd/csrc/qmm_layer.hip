@@ -1199,15 +1199,22 @@ hipError_t release_layer_workspaces() {
     int cur = 0;
     hipError_t e = hipGetDevice(&cur);
     if (e != hipSuccess) return e;
+    // An entry is erased as soon as its buffer is freed, so an error part-way leaves no freed
+    // pointer behind for the next layer_workspace() / layer_scratch() call to hand out.
     for (auto* m : {&g_lws, &g_scratch}) {
-        for (auto& kv : *m) {
-            if (!kv.second.buf) continue;
-            const int dev = std::stoi(kv.first.substr(0, kv.first.find(':')));
-            if ((e = hipSetDevice(dev)) != hipSuccess) return e;
-            if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
-            if ((e = hipFree(kv.second.buf)) != hipSuccess) return e;
+        for (auto it = m->begin(); it != m->end();) {
+            if (it->second.buf) {
+                const int dev = std::stoi(it->first.substr(0, it->first.find(':')));
+                if ((e = hipSetDevice(dev)) != hipSuccess) return e;
+                if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+                if ((e = hipFree(it->second.buf)) != hipSuccess) {
+                    it = m->erase(it);  // the runtime owns the pointer now, whatever it reported
+                    hipSetDevice(cur);
+                    return e;
+                }
+            }
+            it = m->erase(it);
         }
-        m->clear();
     }
     return hipSetDevice(cur);
 }

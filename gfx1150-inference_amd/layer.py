@@ -103,16 +103,62 @@ def _norm_arg(view) -> Tuple[int, int]:
     raise ValueError(f"Unsupported norm weight dtype: {view.dtype}")
 
 
-def layer_weights_struct(layer_weights: Dict[str, Tuple[object, object]], prefix: str) -> "qmm.LayerWeights":
-    """qmm_layer_weights from {name: (GGUFTensorInfo, device view)} of one block."""
+_PROJECTIONS = (("wq", "attn_q"), ("wk", "attn_k"), ("wv", "attn_v"), ("wo", "attn_output"),
+                ("wgate", "ffn_gate"), ("wup", "ffn_up"), ("wdown", "ffn_down"))
+
+
+def projection_dims(config: LlamaLayerConfig) -> Dict[str, Tuple[int, int]]:
+    """(N, K) of each projection: N output rows of K weights (GGUF dims are (K, N))."""
+    h, f = config.hidden_size, config.intermediate_size
+    q, kv = config.num_heads * config.head_dim, config.num_kv_heads * config.head_dim
+    return {"attn_q": (q, h), "attn_k": (kv, h), "attn_v": (kv, h), "attn_output": (h, q),
+            "ffn_gate": (f, h), "ffn_up": (f, h), "ffn_down": (h, f)}
+
+
+def _nbytes(view) -> int:
+    return view.numel() * view.element_size()
+
+
+def layer_weights_struct(layer_weights: Dict[str, Tuple[object, object]], prefix: str,
+                         config: Optional[LlamaLayerConfig] = None, device=None) -> "qmm.LayerWeights":
+    """qmm_layer_weights from {name: (GGUFTensorInfo, device view)} of one block.
+
+    With `config`, every tensor is checked against the layer's dimensions before its pointer is
+    taken (the kernels read exactly N * (K / block) * block_bytes bytes of each projection and
+    hidden_size values of each norm): GGUF dims (K, N), a contiguous view of at least that many
+    bytes, and, with `device`, residence on that device.  A mismatch raises ValueError, as the
+    reference's forward_layer_cached rejects undersized buffers (src/python_bindings/bindings.cpp
+    :562-627)."""
+
+    def on_device(name, view):
+        if not view.is_contiguous():
+            raise ValueError(f"{name}: weight view must be contiguous")
+        if device is not None and view.device != device:
+            raise ValueError(f"{name}: weight view is on {view.device}, the activations on {device}")
+
     w = qmm.LayerWeights()
-    w.attn_norm, w.attn_norm_dtype = _norm_arg(layer_weights[prefix + "attn_norm.weight"][1])
-    w.ffn_norm, w.ffn_norm_dtype = _norm_arg(layer_weights[prefix + "ffn_norm.weight"][1])
-    for field, name in (("wq", "attn_q"), ("wk", "attn_k"), ("wv", "attn_v"), ("wo", "attn_output"),
-                        ("wgate", "ffn_gate"), ("wup", "ffn_up"), ("wdown", "ffn_down")):
+    for field, name in (("attn_norm", "attn_norm"), ("ffn_norm", "ffn_norm")):
+        view = layer_weights[f"{prefix}{name}.weight"][1]
+        if config is not None:
+            on_device(name, view)
+            if view.numel() != config.hidden_size:
+                raise ValueError(f"{name}.weight has {view.numel()} values, hidden_size is {config.hidden_size}")
+        ptr, dt = _norm_arg(view)
+        setattr(w, field, ptr)
+        setattr(w, field + "_dtype", dt)
+    dims = projection_dims(config) if config is not None else {}
+    for field, name in _PROJECTIONS:
         info, view = layer_weights[f"{prefix}{name}.weight"]
         if info.ggml_type not in _QUANTIZED:
             raise ValueError(f"Unsupported weight quantization type: {info.ggml_type}")
+        if config is not None:
+            N, K = dims[name]
+            on_device(name, view)
+            if tuple(info.dims) != (K, N):
+                raise ValueError(f"{name}.weight has GGUF dims {tuple(info.dims)}, the layer needs ({K}, {N})")
+            need = qmm.weight_bytes(int(info.ggml_type), N, K)
+            if _nbytes(view) < need:
+                raise ValueError(f"{name}.weight view holds {_nbytes(view)} bytes, N={N} K={K} need {need}")
         setattr(w, field, view.data_ptr())
         setattr(w, field + "_type", int(info.ggml_type))
     return w
@@ -141,10 +187,14 @@ class TransformerLayer:
         if kv_cache is None:
             raise ValueError("the device layer needs a DeviceKVCache")
         x = hidden_states
-        if x.dtype != torch.float16 or not x.is_contiguous() or x.dim() != 2 or x.shape[1] != self.cfg.hidden_size:
+        if (not x.is_cuda or x.dtype != torch.float16 or not x.is_contiguous() or x.dim() != 2
+                or x.shape[1] != self.cfg.hidden_size):
             raise ValueError("hidden_states must be a contiguous fp16 device tensor [seq_len, hidden_size]")
+        if out is not None and (out.device != x.device or out.dtype != torch.float16 or not out.is_contiguous()
+                                or tuple(out.shape) != tuple(x.shape)):
+            raise ValueError("out must be a contiguous fp16 tensor of hidden_states' shape on its device")
         y = torch.empty_like(x) if out is None else out
-        w = layer_weights_struct(layer_weights, f"blk.{layer_idx}.")
+        w = layer_weights_struct(layer_weights, f"blk.{layer_idx}.", self.cfg, x.device)
         s = torch.cuda.current_stream(x.device) if stream is None else stream
         qmm.check(qmm.lib().qmm_forward_layer(self._c, w, x.data_ptr(), y.data_ptr(), layer_idx, x.shape[0], pos_offset,
                                               s.cuda_stream))

@@ -200,8 +200,10 @@ def gemm(ggml_type: int, A, W, N: int, K: int, out=None, out_dtype=None, stream=
     W holds packed GGUF blocks (uint8), or fp16 values [N, K] for GGML_F16 (the matmul_nt
     operand)."""
     torch = _torch()
-    if A.dim() != 2 or A.shape[1] != K or not A.is_contiguous():
+    if not A.is_cuda or A.dim() != 2 or A.shape[1] != K or not A.is_contiguous():
         raise ValueError("A must be a contiguous [M, K] device tensor")
+    if not W.is_cuda or W.device != A.device:
+        raise ValueError("W must be a device tensor on A's device")
     dense = ggml_type == GGML_F16
     if not W.is_contiguous() or W.dtype not in ((torch.uint8, torch.float16) if dense else (torch.uint8,)):
         raise ValueError("W must be a contiguous uint8 device tensor (or float16 for GGML_F16)")
@@ -210,8 +212,8 @@ def gemm(ggml_type: int, A, W, N: int, K: int, out=None, out_dtype=None, stream=
     M = A.shape[0]
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype or torch.float32, device=A.device)
-    elif out.shape != (M, N) or not out.is_contiguous():
-        raise ValueError("out must be a contiguous [M, N] device tensor")
+    elif out.shape != (M, N) or not out.is_contiguous() or out.device != A.device:
+        raise ValueError("out must be a contiguous [M, N] device tensor on A's device")
     check(_lib.qmm_gemm(ggml_type, A.data_ptr(), _dtype_code(A.dtype), W.data_ptr(), out.data_ptr(),
                         _dtype_code(out.dtype), M, N, K, _stream_handle(stream)))
     return out
@@ -225,8 +227,17 @@ def gemm_batch(descs, stream=None) -> None:
 def dequantize(ggml_type: int, W, num_elements: int, out=None, out_dtype=None, stream=None):
     """dequant(W) -> [num_elements] device tensor (fp16 / bf16 / fp32), bit-exact."""
     torch = _torch()
+    if not W.is_cuda or not W.is_contiguous():
+        raise ValueError("W must be a contiguous device tensor")
+    if num_elements < 0:
+        raise ValueError("num_elements must be non-negative")
+    qk = BLOCK_INFO[ggml_type][0] if ggml_type in BLOCK_INFO else 1
+    if num_elements % qk == 0 and W.numel() * W.element_size() < weight_bytes(ggml_type, 1, num_elements):
+        raise ValueError("W is smaller than (num_elements / block) * block_bytes")
     if out is None:
         out = torch.empty((num_elements,), dtype=out_dtype or torch.float16, device=W.device)
+    elif not out.is_cuda or out.device != W.device or not out.is_contiguous() or out.numel() < num_elements:
+        raise ValueError("out must be a contiguous device tensor on W's device with at least num_elements values")
     check(_lib.qmm_dequantize(ggml_type, W.data_ptr(), out.data_ptr(), _dtype_code(out.dtype),
                               num_elements, _stream_handle(stream)))
     return out

@@ -141,8 +141,10 @@ def test_dequantize_host_api_reference_cases(dev, t, seed):
 # ------------------------------------------------------------------------------ GEMV
 
 GEMV_SHAPES = {
-    O.GGML_Q4_0: [(512, 4096), (300, 2304), (64, 256)],          # full windows, tail window, tiny
-    O.GGML_Q8_0: [(512, 4096), (300, 2304), (64, 256)],
+    # full windows, tail window, tiny, and several windows ending in a half window (K = 14336,
+    # the 8B down projection's K: the streamed Q8_0 window's partial last load instruction)
+    O.GGML_Q4_0: [(512, 4096), (300, 2304), (64, 256), (257, 14336)],
+    O.GGML_Q8_0: [(512, 4096), (300, 2304), (64, 256), (257, 14336)],
     O.GGML_Q4_K: [(512, 4096), (300, 2304), (96, 256)],
     O.GGML_Q6_K: [(512, 4096), (257, 6144), (96, 512)],          # 512: fallback (K % 2048 != 0)
 }
@@ -299,7 +301,12 @@ def test_empty_and_invalid_on_device(dev):
 # ------------------------------------------------------------------ full-size shapes
 
 FULL_SHAPES = [
+    # the 8B Q8_0 layer's seven GEMVs (q/o, k/v, gate/up, down), fp32 activations
     ("8b_q8_0_gate", O.GGML_Q8_0, 14336, 4096),
+    ("8b_q8_0_q", O.GGML_Q8_0, 4096, 4096),
+    ("8b_q8_0_kv", O.GGML_Q8_0, 1024, 4096),
+    ("8b_q8_0_down", O.GGML_Q8_0, 4096, 14336),
+    ("8b_q4_0_down", O.GGML_Q4_0, 4096, 14336),
     ("8b_q4_k_q", O.GGML_Q4_K, 4096, 4096),
     ("8b_q6_k_down", O.GGML_Q6_K, 4096, 14336),
     ("8b_q6_k_lm_head", O.GGML_Q6_K, 128256, 4096),
