@@ -232,6 +232,30 @@ int qmm_gemm(int ggml_type, const void* A, int a_dtype, const void* W, void* C, 
     return gemm_impl(ggml_type, A, a_dtype, W, C, c_dtype, M, N, K, static_cast<hipStream_t>(stream));
 }
 
+int qmm_gemm_noalloc(int ggml_type, const void* A, int a_dtype, const void* W, void* C, int c_dtype, int M, int N, int K,
+                     void* stream) {
+    int rc = check_gemm_args(ggml_type, A, a_dtype, W, C, c_dtype, M, N, K);
+    if (rc != QMM_OK) return rc;
+    if (M == 0 || N == 0) return QMM_OK;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e;
+    if (M >= qmm::kGemvMaxM && qmm::gemm_prefill_supported(ggml_type, a_dtype, c_dtype, M, N, K, A, W, C)) {
+        size_t need = 0;
+        e = qmm::launch_gemm_prefill_noalloc(ggml_type, A, a_dtype, W, C, c_dtype, M, N, K, s, &need);
+        if (e == hipErrorOutOfMemory && need > qmm::kNoAllocScratchBytes)
+            return fail(QMM_ERR_OUT_OF_RANGE, "qmm_gemm_noalloc: M=" + std::to_string(M) + " N=" + std::to_string(N) +
+                                                  " K=" + std::to_string(K) + " needs " + std::to_string(need) +
+                                                  " bytes of scratch; the static scratch holds " +
+                                                  std::to_string(qmm::kNoAllocScratchBytes) + " bytes.");
+    } else {
+        e = qmm::launch_gemv(ggml_type, A, a_dtype, W, C, c_dtype, M, N, K, s);  // allocates nothing
+    }
+    if (e != hipSuccess) return hip_fail(e, "qmm_gemm_noalloc kernel launch");
+    return QMM_OK;
+}
+
+size_t qmm_noalloc_scratch_bytes(void) { return qmm::kNoAllocScratchBytes; }
+
 int qmm_gemm_batch(const qmm_gemm_desc* descs, int count, void* stream) {
     if (count < 0 || (count > 0 && descs == nullptr))
         return fail(QMM_ERR_INVALID_ARGUMENT, "descs must hold count >= 0 descriptors.");

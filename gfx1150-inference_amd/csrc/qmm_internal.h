@@ -93,6 +93,13 @@ bool gemm_prefill_supported(int ggml_type, int a_dtype, int c_dtype, int M, int 
 hipError_t launch_gemm_prefill_fused(int ggml_type, const void* A, int a_dtype, int c_dtype, int M, int K,
                                      const void* const* W, void* const* C, const int* N, int count, hipStream_t stream);
 int prefill_max_fused();
+// The prefill of qmm_gemm_noalloc: the workspace (f16 activations, split-K partials) is a static
+// per-device scratch array of kNoAllocScratchBytes; nothing is allocated.  `need` receives the
+// bytes the launch plan uses; when it exceeds the array, nothing is launched and the call returns
+// hipErrorOutOfMemory.  Calls that overlap on one device share the array and race.
+constexpr size_t kNoAllocScratchBytes = size_t{64} << 20;
+hipError_t launch_gemm_prefill_noalloc(int ggml_type, const void* A, int a_dtype, const void* W, void* C, int c_dtype,
+                                       int M, int N, int K, hipStream_t stream, size_t* need);
 // Frees the prefill workspaces (f16 activations, split-K partials) of every device, after
 // synchronizing each device.
 hipError_t release_prefill_workspaces();

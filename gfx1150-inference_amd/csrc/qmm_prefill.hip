@@ -969,6 +969,14 @@ struct PfSeg {
     int ldc;  // elements between rows of C (N for a whole matrix)
 };
 
+// A caller-provided workspace (the allocation-free entry point): `need` receives the bytes the
+// launch plan uses; a plan needing more than `cap` launches nothing.
+struct PfWs {
+    void* buf;
+    size_t cap;
+    size_t need;
+};
+
 // One launch of the 128 x 256 (Wide = false) or 256 x 256 (Wide = true) tile kernel over `segs`
 // with K split `ksplit` ways (at most; the split length is a whole number of steps), then, for a
 // split, the pass that adds the partial tiles (at `part`) into C.
@@ -1046,7 +1054,7 @@ PfPlan plan_prefill(bool wide, int tiles_m, int tiles_n, int steps, int bk, int 
 }
 
 template <class P, typename TA, typename TC, bool Wide>
-hipError_t launch_p(const void* A, const PfSeg* segs, int nseg, int M, int K, hipStream_t stream) {
+hipError_t launch_p(const void* A, const PfSeg* segs, int nseg, int M, int K, hipStream_t stream, PfWs* ext) {
     constexpr int BM = Wide ? kWBM : kBM, BN = Wide ? kWBN : kBN, BK = Wide ? kWBK : 64 * P::kH;
     int cus = 0;
     hipError_t e = cu_count(cus);
@@ -1089,7 +1097,14 @@ hipError_t launch_p(const void* A, const PfSeg* segs, int nseg, int M, int K, hi
     if (plan.ksplit > 1) p_bytes = static_cast<size_t>(plan.ksplit) * M * n_total * 4;
     if (plan.tail_n > 0) p_bytes = static_cast<size_t>(plan.tail_ks) * M * n_tail_total * 4;
     void* ws = nullptr;
-    if (a_bytes + p_bytes > 0 && (e = workspace(stream, a_bytes + p_bytes + 256, &ws)) != hipSuccess) return e;
+    if (ext != nullptr) {
+        // caller-provided scratch: checked before anything is launched
+        ext->need = a_bytes + p_bytes > 0 ? a_bytes + p_bytes + 256 : 0;
+        if (ext->need > ext->cap) return hipErrorOutOfMemory;
+        ws = ext->buf;
+    } else if (a_bytes + p_bytes > 0 && (e = workspace(stream, a_bytes + p_bytes + 256, &ws)) != hipSuccess) {
+        return e;
+    }
     const _Float16* a16 = static_cast<const _Float16*>(A);
     if (!direct) {
         _Float16* dst = static_cast<_Float16*>(ws);
@@ -1107,36 +1122,36 @@ hipError_t launch_p(const void* A, const PfSeg* segs, int nseg, int M, int K, hi
 
 // HN: 64-k halves per step of the 128 x 256 kernel for this format.
 template <template <int> class PF, int HN, typename TA, typename TC>
-hipError_t launch_family(const void* A, const PfSeg* segs, int nseg, int M, int K, hipStream_t stream) {
+hipError_t launch_family(const void* A, const PfSeg* segs, int nseg, int M, int K, hipStream_t stream, PfWs* ext) {
     int cus = 0;
     hipError_t e = cu_count(cus);
     if (e != hipSuccess) return e;
     int64_t wide_tiles_n = 0;
     for (int i = 0; i < nseg; ++i) wide_tiles_n += (segs[i].N + kWBN - 1) / kWBN;
-    if (use_wide(M, wide_tiles_n, K, cus)) return launch_p<PF<kWH>, TA, TC, true>(A, segs, nseg, M, K, stream);
-    return launch_p<PF<HN>, TA, TC, false>(A, segs, nseg, M, K, stream);
+    if (use_wide(M, wide_tiles_n, K, cus)) return launch_p<PF<kWH>, TA, TC, true>(A, segs, nseg, M, K, stream, ext);
+    return launch_p<PF<HN>, TA, TC, false>(A, segs, nseg, M, K, stream, ext);
 }
 
 template <typename TA, typename TC>
-hipError_t dispatch_p(int t, const void* A, const PfSeg* segs, int nseg, int M, int K, hipStream_t stream) {
+hipError_t dispatch_p(int t, const void* A, const PfSeg* segs, int nseg, int M, int K, hipStream_t stream, PfWs* ext) {
     switch (t) {
-        case QMM_TYPE_Q4_K: return launch_family<PQ4K, kHalves, TA, TC>(A, segs, nseg, M, K, stream);
-        case QMM_TYPE_Q6_K: return launch_family<PQ6K, kHalves, TA, TC>(A, segs, nseg, M, K, stream);
-        case QMM_TYPE_Q8_0: return launch_family<PQ80, 2, TA, TC>(A, segs, nseg, M, K, stream);
-        case QMM_TYPE_Q4_0: return launch_family<PQ40, 2, TA, TC>(A, segs, nseg, M, K, stream);
-        case QMM_TYPE_F16: return launch_family<PF16, 2, TA, TC>(A, segs, nseg, M, K, stream);
+        case QMM_TYPE_Q4_K: return launch_family<PQ4K, kHalves, TA, TC>(A, segs, nseg, M, K, stream, ext);
+        case QMM_TYPE_Q6_K: return launch_family<PQ6K, kHalves, TA, TC>(A, segs, nseg, M, K, stream, ext);
+        case QMM_TYPE_Q8_0: return launch_family<PQ80, 2, TA, TC>(A, segs, nseg, M, K, stream, ext);
+        case QMM_TYPE_Q4_0: return launch_family<PQ40, 2, TA, TC>(A, segs, nseg, M, K, stream, ext);
+        case QMM_TYPE_F16: return launch_family<PF16, 2, TA, TC>(A, segs, nseg, M, K, stream, ext);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t dispatch_dtypes(int t, const void* A, int a_dtype, int c_dtype, const PfSeg* segs, int nseg, int M, int K,
-                           hipStream_t stream) {
+                           hipStream_t stream, PfWs* ext = nullptr) {
     if (a_dtype == QMM_DTYPE_F32) {
-        if (c_dtype == QMM_DTYPE_F32) return dispatch_p<float, float>(t, A, segs, nseg, M, K, stream);
-        return dispatch_p<float, __half>(t, A, segs, nseg, M, K, stream);
+        if (c_dtype == QMM_DTYPE_F32) return dispatch_p<float, float>(t, A, segs, nseg, M, K, stream, ext);
+        return dispatch_p<float, __half>(t, A, segs, nseg, M, K, stream, ext);
     }
-    if (c_dtype == QMM_DTYPE_F32) return dispatch_p<__half, float>(t, A, segs, nseg, M, K, stream);
-    return dispatch_p<__half, __half>(t, A, segs, nseg, M, K, stream);
+    if (c_dtype == QMM_DTYPE_F32) return dispatch_p<__half, float>(t, A, segs, nseg, M, K, stream, ext);
+    return dispatch_p<__half, __half>(t, A, segs, nseg, M, K, stream, ext);
 }
 
 }  // namespace
@@ -1160,6 +1175,47 @@ hipError_t launch_gemm_prefill(int ggml_type, const void* A, int a_dtype, const 
 }
 
 int prefill_max_fused() { return kPfMaxSegs; }
+
+// ---- allocation-free prefill: the workspace is a file-scope device array ------------------------
+// Each device the library runs on holds its own copy of `scratch` until the process ends.  In host
+// code `scratch` names a host-side stand-in, never the device memory: kernels get the per-device
+// address that hipGetSymbolAddress returns (looked up once per device, with that device current).
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+std::mutex g_scratch_mutex;
+std::unordered_map<int, void*> g_scratch_ptr;
+
+hipError_t scratch_address(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    auto it = g_scratch_ptr.find(dev);
+    if (it != g_scratch_ptr.end()) {
+        *out = it->second;
+        return hipSuccess;
+    }
+    void* ptr = nullptr;
+    if ((e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch))) != hipSuccess) return e;
+    if (ptr == nullptr) return hipErrorInvalidSymbol;
+    g_scratch_ptr.emplace(dev, ptr);
+    *out = ptr;
+    return hipSuccess;
+}
+}  // namespace
+
+hipError_t launch_gemm_prefill_noalloc(int ggml_type, const void* A, int a_dtype, const void* W, void* C, int c_dtype,
+                                       int M, int N, int K, hipStream_t stream, size_t* need) {
+    *need = 0;
+    PfWs ext{nullptr, kNoAllocScratchBytes, 0};
+    hipError_t e = scratch_address(&ext.buf);
+    if (e != hipSuccess) return e;
+    const PfSeg seg{W, C, N, N};
+    e = dispatch_dtypes(ggml_type, A, a_dtype, c_dtype, &seg, 1, M, K, stream, &ext);
+    *need = ext.need;
+    return e;
+}
 
 hipError_t launch_gemm_prefill_fused(int ggml_type, const void* A, int a_dtype, int c_dtype, int M, int K,
                                      const void* const* W, void* const* C, const int* N, int count, hipStream_t stream) {

@@ -99,6 +99,8 @@ _SIGNATURES = {
     "qmm_gemv_max_m": (_i, []),
     "qmm_weight_bytes": (ctypes.c_size_t, [_i, _i64, _i64]),
     "qmm_gemm": (_i, [_i, _vp, _i, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "qmm_gemm_noalloc": (_i, [_i, _vp, _i, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "qmm_noalloc_scratch_bytes": (ctypes.c_size_t, []),
     "qmm_dequantize": (_i, [_i, _vp, _vp, _i, _i64, _vp]),
     "qmm_embed": (_i, [_i, _vp, _i64, _i, _vp, _i64, _vp, _i, _vp, _vp]),
     "qmm_gemm_batch": (_i, [ctypes.POINTER(GemmDesc), _i, _vp]),

@@ -70,6 +70,17 @@ size_t qmm_weight_bytes(int ggml_type, int64_t n, int64_t k);
 int qmm_gemm(int ggml_type, const void* A, int a_dtype, const void* W, void* C, int c_dtype,
              int M, int N, int K, void* stream);
 
+/* qmm_gemm that allocates nothing (no counterpart in the reference): for callers that cannot
+ * call hipMalloc - code under HIP graph capture, tight serving loops, harnesses that forbid it.
+ * Same arguments, kernels and results as qmm_gemm.  The prefill sizes' workspace (f16 copy of
+ * fp32 or unaligned activations, split-K partial tiles) is a static per-device scratch array of
+ * qmm_noalloc_scratch_bytes() bytes, held by every GPU the library runs on until the process
+ * ends; a call needing more returns QMM_ERR_OUT_OF_RANGE and launches nothing.  All calls on one
+ * GPU share that array: calls that overlap on one GPU (other streams, other threads) race. */
+int qmm_gemm_noalloc(int ggml_type, const void* A, int a_dtype, const void* W, void* C, int c_dtype,
+                     int M, int N, int K, void* stream);
+size_t qmm_noalloc_scratch_bytes(void);
+
 /* One GEMM of a batch.  ev_before / ev_after are optional hipEvent_t handles (NULL = none)
  * recorded on the batch's stream immediately before / after this GEMM's kernel. */
 typedef struct qmm_gemm_desc {
