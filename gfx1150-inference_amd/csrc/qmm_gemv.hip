@@ -404,12 +404,14 @@ struct GF16 {
 // chunks 2q and 2q+1 (fp32, fixed order).
 // ------------------------------------------------------------------------------------------
 template <typename TA>
-__device__ __forceinline__ void load16_act(const TA* p, bool ok, bool vec, uint32_t h[8]);
+__device__ __forceinline__ void load16_act(const TA* p, bool ok, bool vec, uint32_t h[8], float mul, float& amax);
 
 // The loads are issued whether or not the activations exist (p is always a valid address);
-// missing ones (`ok` false) are replaced by zeros afterwards.
+// missing ones (`ok` false) are replaced by zeros afterwards.  fp32 values are multiplied by `mul`
+// (a power of two, 1 unless the window is rescaled) before the f16 rounding; `amax` receives the
+// largest magnitude of the 16 unscaled values.
 template <>
-__device__ __forceinline__ void load16_act<float>(const float* p, bool ok, bool vec, uint32_t h[8]) {
+__device__ __forceinline__ void load16_act<float>(const float* p, bool ok, bool vec, uint32_t h[8], float mul, float& amax) {
     float x[16];
     if (vec) {
 #pragma unroll
@@ -421,8 +423,14 @@ __device__ __forceinline__ void load16_act<float>(const float* p, bool ok, bool 
 #pragma unroll
         for (int i = 0; i < 16; ++i) x[i] = p[i];
     }
+    float mx = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = ok ? x[i] : 0.0f;
+    for (int i = 0; i < 16; ++i) {
+        x[i] = ok ? x[i] : 0.0f;
+        mx = fmaxf(mx, fabsf(x[i]));
+        x[i] *= mul;
+    }
+    amax = mx;
     // pairs (0,2), (1,3), (4,6), (5,7), ... rounded to nearest even (v_cvt_pk_f16_f32)
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
@@ -436,7 +444,8 @@ __device__ __forceinline__ void load16_act<float>(const float* p, bool ok, bool 
 }
 
 template <>
-__device__ __forceinline__ void load16_act<__half>(const __half* p, bool ok, bool vec, uint32_t h[8]) {
+__device__ __forceinline__ void load16_act<__half>(const __half* p, bool ok, bool vec, uint32_t h[8], float, float& amax) {
+    amax = 0.0f;
     uint32_t w[8];
     if (vec) {
         const uint4 a = reinterpret_cast<const uint4*>(p)[0];
@@ -472,12 +481,14 @@ __device__ __forceinline__ int sx_index(int nslots, int slot, int m, int MR, int
 template <class F, int MR, typename TA>
 struct StageItem {
     uint32_t h[8];
-    __device__ __forceinline__ void load(const TA* __restrict__ A, int M, int K, int m0, int w, int item, bool vec) {
+    float amax;  // largest unscaled magnitude of the item (fp32 activations)
+    __device__ __forceinline__ void load(const TA* __restrict__ A, int M, int K, int m0, int w, int item, bool vec,
+                                         float mul = 1.0f) {
         const int m = item >> 8, q = (item >> 6) & 3, lane = item & 63;
         const int k = w * kGemvWindow + F::xk(lane, 2 * q);
         const bool ok = m0 + m < M && k < K;
         const TA* p = A + static_cast<size_t>(ok ? m0 + m : 0) * K + (ok ? k : 0);
-        load16_act<TA>(p, ok, vec, h);
+        load16_act<TA>(p, ok, vec, h, mul, amax);
     }
     __device__ __forceinline__ void store(int nslots, int slot, int item) const {
         const int m = item >> 8, q = (item >> 6) & 3, lane = item & 63;
@@ -489,7 +500,69 @@ struct StageItem {
         for (int j = 0; j < 8; ++j) t = dot2(h[j], ones, t);
         reinterpret_cast<float*>(&gemv_lds[sx_index(nslots, slot, m, MR, lane)])[q] = t;
     }
+    // fp32 activations: the item's magnitude joins its (window, row) maximum (non-negative floats
+    // order like their bit patterns).
+    __device__ __forceinline__ void note_max(uint32_t* wmax) const {
+        if constexpr (std::is_same<TA, float>::value) atomicMax(wmax, __float_as_uint(amax));
+    }
 };
+
+// Range of fp32 activations.  f16 holds magnitudes from 2^-14 (normal) to 65504; a window (4096 k)
+// of one activation row whose largest magnitude lies outside that range (at or above 65504, or in
+// [2^-60, 2^-14)) is staged as x * 2^-e with e = exponent(max) - 14, which brings the maximum into
+// [2^14, 2^15), and the window's group coefficients are multiplied by 2^e.  Both multiplications
+// are exact, so the products stay those of the scaled operands; every other window has e = 0 and
+// is staged and multiplied exactly as fp16 activations are.  Infinite or NaN maxima keep e = 0
+// (they propagate as in fp32 arithmetic).  The exponent depends only on the window's own values,
+// so a row's result does not depend on M.
+__device__ __forceinline__ int window_exp(uint32_t maxbits) {
+    const bool big = maxbits >= 0x477FE000u && maxbits < 0x7F800000u;  // [65504, inf)
+    const bool tiny = maxbits >= 0x21800000u && maxbits < 0x38800000u;  // [2^-60, 2^-14)
+    return big || tiny ? static_cast<int>(maxbits >> 23) - 127 - 14 : 0;
+}
+__device__ __forceinline__ float exp2_int(int e) { return __uint_as_float(static_cast<uint32_t>(127 + e) << 23); }
+
+// (window, row) maxima of fp32 activations, in LDS: nwin * MR entries for the kernels that stage
+// every window at once (at most 17 fit the LDS), 3 * MR for the windowed kernel.
+constexpr int kWmaxEntries = 32;
+template <typename TA>
+constexpr int wmax_size(int n) { return std::is_same<TA, float>::value ? n : 1; }
+
+__device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// 2^e of activation row m in staged window `w` (1 for fp16 activations).
+template <int MR, typename TA>
+__device__ __forceinline__ void window_factors(const uint32_t* wmax_w, float (&pm)[MR]) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        if constexpr (std::is_same<TA, float>::value) pm[m] = exp2_int(window_exp(wmax_w[m]));
+        else pm[m] = 1.0f;
+    }
+}
+
+// After all windows of fp32 activations are staged (and a barrier): re-stages each (window, row)
+// whose maximum is outside the f16 range, scaled by its power of two.  The branch is uniform and
+// rare; it ends with a barrier when taken.
+template <class F, int MR, int NW, typename TA>
+__device__ __forceinline__ void restage_out_of_range(const TA* __restrict__ A, const uint32_t* wmax, int M, int K, int m0,
+                                                     int nwin, int tid, bool vec) {
+    if constexpr (std::is_same<TA, float>::value) {
+        bool need = false;
+        for (int i = 0; i < nwin * MR; ++i) need = need || window_exp(wmax[i]) != 0;
+        if (!need) return;
+        const int items = nwin * MR * 256;
+        for (int it = tid; it < items; it += 64 * NW) {
+            const int w = it / (MR * 256), item = it - w * (MR * 256);
+            const int e = window_exp(wmax[w * MR + (item >> 8)]);
+            if (e != 0) {
+                StageItem<F, MR, TA> s2;
+                s2.load(A, M, K, m0, w, item, vec, exp2_int(-e));
+                s2.store(nwin, w, item);
+            }
+        }
+        __syncthreads();
+    }
+}
 
 template <typename TC>
 __device__ __forceinline__ void store_out(TC* p, float v);
@@ -502,11 +575,18 @@ __device__ __forceinline__ void store_out<__half>(__half* p, float v) {
 
 // acc[m][y] += the window's contribution of row y for activation row m.
 // FULL: every lane slot of the window is inside K (no validity masks).
-template <class F, int MR, int YT, bool FULL>
+// SC: fp32 activations; pm[m] = 2^e of activation row m in this window (1 unless rescaled).
+template <class F, int MR, int YT, bool FULL, bool SC = false>
 __device__ __forceinline__ void mac_window(const typename F::Raw (&cur)[YT], int nslots, int slot, int lane, int kv,
-                                           const Consts& KC, float (&acc)[MR][YT]) {
+                                           const Consts& KC, float (&acc)[MR][YT], const float (&pm)[MR]) {
     if constexpr (F::kType == QMM_TYPE_F16) {
-        // dense weights: no group scales; activations outside K are staged as zeros
+        // dense weights: no group scales; activations outside K are staged as zeros.  A rescaled
+        // window (pm != 1) is summed on its own and added as pm * sum.
+        float s0[MR][YT];
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int y = 0; y < YT; ++y) s0[m][y] = !SC || pm[m] == 1.0f ? acc[m][y] : 0.0f;
 #pragma unroll
         for (int cj = 0; cj < kChunks; ++cj) {
             u32x4 xp[MR];
@@ -518,15 +598,19 @@ __device__ __forceinline__ void mac_window(const typename F::Raw (&cur)[YT], int
                 F::chunk_codes(cur[y], cj, KC, w);
 #pragma unroll
                 for (int m = 0; m < MR; ++m) {
-                    float s = acc[m][y];
+                    float s = s0[m][y];
                     s = dot2(xp[m].x, w[0], s);
                     s = dot2(xp[m].y, w[1], s);
                     s = dot2(xp[m].z, w[2], s);
                     s = dot2(xp[m].w, w[3], s);
-                    acc[m][y] = s;
+                    s0[m][y] = s;
                 }
             }
         }
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int y = 0; y < YT; ++y) acc[m][y] = !SC || pm[m] == 1.0f ? s0[m][y] : __fmaf_rn(pm[m], s0[m][y], acc[m][y]);
         return;
     }
     constexpr int G = F::kG;
@@ -583,8 +667,10 @@ __device__ __forceinline__ void mac_window(const typename F::Raw (&cur)[YT], int
 #pragma unroll
             for (int y = 0; y < YT; ++y) {
                 float t = acc[m][y];
-                t = __fmaf_rn(a[y][g], S[m][y], t);
-                t = __fmaf_rn(-B[y][g], sxg, t);
+                const float ag = SC ? a[y][g] * pm[m] : a[y][g];   // exact: pm is a power of two
+                const float bg = SC ? B[y][g] * pm[m] : B[y][g];
+                t = __fmaf_rn(ag, S[m][y], t);
+                t = __fmaf_rn(-bg, sxg, t);
                 acc[m][y] = t;
             }
         }
@@ -771,6 +857,8 @@ __device__ __forceinline__ SegRef<TC> seg_of(const GemvSegs<TC>& sg, int g) {
 template <class F, int MR, int YT, int NW, typename TA, typename TC>
 __global__ __launch_bounds__(64 * NW, QMM_GEMV_MIN_WAVES)
 void gemv_resident_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K, int a_vec, int nrg, GemvFuse fz) {
+    constexpr bool kF32 = std::is_same<TA, float>::value;
+    __shared__ uint32_t wmax[wmax_size<TA>(kWmaxEntries)];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -823,6 +911,9 @@ void gemv_resident_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int 
         if constexpr (PD >= 2) { load_item(gl, wl, b2); next(gl, wl); }
         if constexpr (kFoldable<F, MR, YT, NW, TA>) stage_fused<F, MR, NW>(A, fz, M, K, m0, nwin, tid);
     } else {
+        if constexpr (kF32) {
+            if (tid < nwin * MR) wmax[tid] = 0u;
+        }
         StageItem<F, MR, TA> st[kFirst];
 #pragma unroll
         for (int j = 0; j < kFirst; ++j) {
@@ -834,12 +925,14 @@ void gemv_resident_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int 
         load_item(gl, wl, b0); next(gl, wl);
         if constexpr (PD >= 1) { load_item(gl, wl, b1); next(gl, wl); }
         if constexpr (PD >= 2) { load_item(gl, wl, b2); next(gl, wl); }
+        if constexpr (kF32) lds_barrier();  // the maxima are cleared before any item joins them
 #pragma unroll
         for (int j = 0; j < kFirst; ++j) {
             const int it = tid + 64 * NW * j;
             if (it < items) {
-                const int w = it / (MR * 256);
-                st[j].store(nwin, w, it - w * (MR * 256));
+                const int w = it / (MR * 256), item = it - w * (MR * 256);
+                st[j].store(nwin, w, item);
+                st[j].note_max(&wmax[w * MR + (item >> 8)]);
             }
         }
         for (int it = tid + 64 * NW * kFirst; it < items; it += 64 * NW) {
@@ -847,9 +940,11 @@ void gemv_resident_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int 
             StageItem<F, MR, TA> s2;
             s2.load(A, M, K, m0, w, item, vec);
             s2.store(nwin, w, item);
+            s2.note_max(&wmax[w * MR + (item >> 8)]);
         }
     }
     __syncthreads();
+    restage_out_of_range<F, MR, NW, TA>(A, wmax, M, K, m0, nwin, tid, vec);
     if (!active) return;
 
     float acc[MR][YT];
@@ -860,8 +955,10 @@ void gemv_resident_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int 
 
     auto compute = [&](const Raw (&b)[YT]) {
         const int kv = min(K - wc * kGemvWindow, kGemvWindow);
-        if (kv == kGemvWindow) mac_window<F, MR, YT, true>(b, nwin, wc, lane, kv, KC, acc);
-        else mac_window<F, MR, YT, false>(b, nwin, wc, lane, kv, KC, acc);
+        float pm[MR];
+        window_factors<MR, TA>(&wmax[kF32 ? wc * MR : 0], pm);
+        if (kv == kGemvWindow) mac_window<F, MR, YT, true, kF32>(b, nwin, wc, lane, kv, KC, acc, pm);
+        else mac_window<F, MR, YT, false, kF32>(b, nwin, wc, lane, kv, KC, acc, pm);
         if (wc == nwin - 1) {
             const SegRef<TC> sr = seg_of(sg, gc);
             reduce_store<MR, YT, TC>(acc, sr.C, M, sr.N, m0, fz.pair ? gc : (gc - sr.g0) * YT, lane, fz);
@@ -938,6 +1035,8 @@ template <class F, int MR, int YT, int NW, int NS, typename TA, typename TC>
 __global__ __launch_bounds__(64 * NW, QMM_GEMV_MIN_WAVES)
 void gemv_stream_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K, int a_vec, int nrg, GemvFuse fz) {
     using WS = WinSlot<F>;
+    constexpr bool kF32 = std::is_same<TA, float>::value;
+    __shared__ uint32_t wmax[wmax_size<TA>(kWmaxEntries)];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -993,14 +1092,20 @@ void gemv_stream_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K,
     if (fused) {
         if constexpr (kFoldable<F, MR, YT, NW, TA>) stage_fused<F, MR, NW>(A, fz, M, K, m0, nwin, tid);
     } else {
+        if constexpr (kF32) {
+            if (tid < nwin * MR) wmax[tid] = 0u;
+            lds_barrier();  // the maxima are cleared before any item joins them
+        }
         for (int it = tid; it < items; it += 64 * NW) {
             const int w = it / (MR * 256), item = it - w * (MR * 256);
             StageItem<F, MR, TA> s2;
             s2.load(A, M, K, m0, w, item, vec);
             s2.store(nwin, w, item);
+            s2.note_max(&wmax[w * MR + (item >> 8)]);
         }
     }
     __syncthreads();
+    restage_out_of_range<F, MR, NW, TA>(A, wmax, M, K, m0, nwin, tid, vec);
     if (!active) {
         wait_vmcnt<0>();  // no LDS DMA outstanding when the wave ends
         return;
@@ -1025,8 +1130,10 @@ void gemv_stream_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K,
         Raw b[YT];
 #pragma unroll
         for (int y = 0; y < YT; ++y) b[y] = F::load(wslots + (slot * YT + y) * WS::kBytes, lane, kv);
-        if (kv == kGemvWindow) mac_window<F, MR, YT, true>(b, nwin, wc, lane, kv, KC, acc);
-        else mac_window<F, MR, YT, false>(b, nwin, wc, lane, kv, KC, acc);
+        float pm[MR];
+        window_factors<MR, TA>(&wmax[kF32 ? wc * MR : 0], pm);
+        if (kv == kGemvWindow) mac_window<F, MR, YT, true, kF32>(b, nwin, wc, lane, kv, KC, acc, pm);
+        else mac_window<F, MR, YT, false, kF32>(b, nwin, wc, lane, kv, KC, acc, pm);
         if (wc == nwin - 1) {
             const SegRef<TC> sr = seg_of(sg, gc);
             reduce_store<MR, YT, TC>(acc, sr.C, M, sr.N, m0, fz.pair ? gc : (gc - sr.g0) * YT, lane, fz);
@@ -1050,6 +1157,11 @@ void gemv_window_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W,
                         int M, int N, int K, int a_vec) {
     constexpr int kItems = MR * 256;
     constexpr int kPer = (kItems + 64 * NW - 1) / (64 * NW);
+    constexpr bool kF32 = std::is_same<TA, float>::value;
+    // fp32 activations: maxima of window w in wmax[w % 3]; entries of window w + 2 are cleared
+    // while window w is multiplied (after every read of window w - 1's, before window w + 2 is
+    // staged one barrier later).
+    __shared__ uint32_t wmax[wmax_size<TA>(3 * MR)];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wv = tid >> 6;
@@ -1080,13 +1192,44 @@ void gemv_window_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W,
 #pragma unroll
     for (int i = 0; i < kPer; ++i)
         if (tid + 64 * NW * i < kItems) st[i].load(A, M, K, m0, 0, tid + 64 * NW * i, vec);
+    if constexpr (kF32) {
+        if (tid < 2 * MR) wmax[tid] = 0u;
+        lds_barrier();
+    }
 #pragma unroll
     for (int i = 0; i < kPer; ++i)
-        if (tid + 64 * NW * i < kItems) st[i].store(2, 0, tid + 64 * NW * i);
+        if (tid + 64 * NW * i < kItems) {
+            st[i].store(2, 0, tid + 64 * NW * i);
+            st[i].note_max(&wmax[(tid + 64 * NW * i) >> 8]);
+        }
     __syncthreads();
 
     for (int w = 0; w < nwin; ++w) {
         const bool more = w + 1 < nwin;
+        float pm[MR];
+        if constexpr (kF32) {
+            const uint32_t* wm = &wmax[(w % 3) * MR];
+            bool need = false;
+#pragma unroll
+            for (int m = 0; m < MR; ++m) need = need || window_exp(wm[m]) != 0;
+            if (need) {  // rare: re-stage window w with its rows' factors
+#pragma unroll
+                for (int i = 0; i < kPer; ++i) {
+                    const int it = tid + 64 * NW * i;
+                    const int e = it < kItems ? window_exp(wm[it >> 8]) : 0;
+                    if (e != 0) {
+                        StageItem<F, MR, TA> s2;
+                        s2.load(A, M, K, m0, w, it, vec, exp2_int(-e));
+                        s2.store(2, w & 1, it);
+                    }
+                }
+                __syncthreads();
+            }
+            window_factors<MR, TA>(wm, pm);
+            if (tid < MR) wmax[((w + 2) % 3) * MR + tid] = 0u;
+        } else {
+            window_factors<MR, TA>(wmax, pm);
+        }
         {
             // unconditional weight prefetch (the last one re-reads window w)
             const int wn = more ? w + 1 : w;
@@ -1102,13 +1245,16 @@ void gemv_window_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W,
         }
         {
             const int kv = min(K - w * kGemvWindow, kGemvWindow);
-            if (kv == kGemvWindow) mac_window<F, MR, YT, true>(cur, 2, w & 1, lane, kv, KC, acc);
-            else mac_window<F, MR, YT, false>(cur, 2, w & 1, lane, kv, KC, acc);
+            if (kv == kGemvWindow) mac_window<F, MR, YT, true, kF32>(cur, 2, w & 1, lane, kv, KC, acc, pm);
+            else mac_window<F, MR, YT, false, kF32>(cur, 2, w & 1, lane, kv, KC, acc, pm);
         }
         if (more) {
 #pragma unroll
             for (int i = 0; i < kPer; ++i)
-                if (tid + 64 * NW * i < kItems) st[i].store(2, (w + 1) & 1, tid + 64 * NW * i);
+                if (tid + 64 * NW * i < kItems) {
+                    st[i].store(2, (w + 1) & 1, tid + 64 * NW * i);
+                    st[i].note_max(&wmax[kF32 ? ((w + 1) % 3) * MR + ((tid + 64 * NW * i) >> 8) : 0]);
+                }
         }
 #pragma unroll
         for (int y = 0; y < YT; ++y) cur[y] = nxt[y];
@@ -1268,12 +1414,14 @@ hipError_t launch_fast(const void* A, const Seg* segs, int nseg, int M, int K, b
     if (fz.pair && (YT != 2 || MR != 1 || nseg != 2 || segs[0].N != segs[1].N || sizeof(TC) != 2)) return hipErrorNotSupported;
     if (fz.kind != 0 && static_cast<int64_t>(nwin) * MR * 256 > static_cast<int64_t>(kFuseOwn) * threads)
         return hipErrorNotSupported;
+    // fp32 activations: one LDS maximum per staged (window, row)
+    const bool wmax_fits = !std::is_same<TA, float>::value || MR * nwin <= kWmaxEntries;
 #if QMM_GEMV_STREAM
     if constexpr (F::kStream) {
         constexpr int NS = QMM_GEMV_NS;
         const size_t row_bytes = static_cast<size_t>(K / F::kQK) * F::kBlockBytes;
         const size_t st_lds = res_lds + static_cast<size_t>(NW) * NS * YT * WinSlot<F>::kBytes;
-        bool ok = row_bytes % 16 == 0 && st_lds <= di.max_lds;
+        bool ok = row_bytes % 16 == 0 && st_lds <= di.max_lds && wmax_fits;
         for (int j = 0; j < nseg; ++j) ok = ok && (reinterpret_cast<uintptr_t>(segs[j].W) & 15u) == 0;
         if (ok) {
             const void* kern = reinterpret_cast<const void*>(&gemv_stream_kernel<F, MR, YT, NW, NS, TA, TC>);
@@ -1290,7 +1438,7 @@ hipError_t launch_fast(const void* A, const Seg* segs, int nseg, int M, int K, b
         }
     }
 #endif
-    if (res_lds <= di.max_lds) {
+    if (res_lds <= di.max_lds && wmax_fits) {
         const void* kern = reinterpret_cast<const void*>(&gemv_resident_kernel<F, MR, YT, NW, TA, TC>);
         int occ = 0;
         if ((e = occupancy(kern, threads, res_lds, occ)) != hipSuccess) return e;

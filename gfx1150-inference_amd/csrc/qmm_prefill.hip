@@ -379,6 +379,7 @@ struct PfSegs {
     int ldc[kPfMaxSegs];
     int tile_end[kPfMaxSegs];
     size_t part_off[kPfMaxSegs];
+    const float* rs;  // per activation row output factor (a power of two), or nullptr
 };
 
 // Segment of the workgroup's n-tile tn (uniform), and tn's index inside that segment.
@@ -584,7 +585,8 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int n = n0 + 32 * wv + 8 * g + 4 * h;
-            const float vs[4] = {acc[i][4 * g], acc[i][4 * g + 1], acc[i][4 * g + 2], acc[i][4 * g + 3]};
+            const float sm = sg.rs != nullptr ? sg.rs[m] : 1.0f;
+            const float vs[4] = {acc[i][4 * g] * sm, acc[i][4 * g + 1] * sm, acc[i][4 * g + 2] * sm, acc[i][4 * g + 3] * sm};
             if (ksplit > 1) {
                 float* dst = part + (static_cast<size_t>(kz) * M + m) * N;
 #pragma unroll
@@ -813,13 +815,14 @@ void prefill_wide_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> s
     for (int i = 0; i < 8; ++i) {
         const int m = m0 + 32 * i + l32;
         if (m >= M) continue;
+        const float sm = sg.rs != nullptr ? sg.rs[m] : 1.0f;
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int n = n0 + 64 * wv + 32 * nb + 8 * g + 4 * h;
-                const float vs[4] = {acc[nb][i][4 * g], acc[nb][i][4 * g + 1], acc[nb][i][4 * g + 2],
-                                     acc[nb][i][4 * g + 3]};
+                const float vs[4] = {acc[nb][i][4 * g] * sm, acc[nb][i][4 * g + 1] * sm, acc[nb][i][4 * g + 2] * sm,
+                                     acc[nb][i][4 * g + 3] * sm};
                 if (ksplit > 1) {
                     float* dst = part + (static_cast<size_t>(kz) * M + m) * N;
 #pragma unroll
@@ -859,6 +862,38 @@ __global__ __launch_bounds__(256) void to_f16_kernel(const TA* __restrict__ A, _
         v[e] = static_cast<_Float16>(x);
     }
     __builtin_memcpy(out + static_cast<size_t>(m) * lda + k, v, 16);
+}
+
+// fp32 activations [M, K] -> f16 [M, lda], one workgroup per row.  A row whose largest magnitude
+// lies outside the f16 range (at or above 65504, or in [2^-60, 2^-14)) is rounded as x * 2^-e with
+// e = exponent(max) - 14 (its maximum lands in [2^14, 2^15)), and rs[m] = 2^e multiplies the row's
+// outputs; both scalings are exact.  Other rows are rounded unchanged and rs[m] = 1.  Infinite or
+// NaN values keep e = 0 and propagate.
+__global__ __launch_bounds__(256) void to_f16_rows_kernel(const float* __restrict__ A, _Float16* __restrict__ out,
+                                                          float* __restrict__ rs, int K, int lda) {
+    __shared__ float red[4];
+    const int m = blockIdx.x;
+    const int tid = threadIdx.x;
+    const float* row = A + static_cast<size_t>(m) * K;
+    float mx = 0.0f;
+    for (int k = tid; k < K; k += 256) mx = fmaxf(mx, fabsf(row[k]));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const uint32_t mb = __float_as_uint(mx);
+    const bool big = mb >= 0x477FE000u && mb < 0x7F800000u;
+    const bool tiny = mb >= 0x21800000u && mb < 0x38800000u;
+    const int e = big || tiny ? static_cast<int>(mb >> 23) - 127 - 14 : 0;
+    const float down = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
+    if (tid == 0) rs[m] = __uint_as_float(static_cast<uint32_t>(127 + e) << 23);
+    for (int k = 8 * tid; k < lda; k += 8 * 256) {
+        _Float16 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = static_cast<_Float16>(k + j < K ? row[k + j] * down : 0.0f);
+        __builtin_memcpy(out + static_cast<size_t>(m) * lda + k, v, 16);
+    }
 }
 
 // C[m, n] (rows ldc apart) = sum_z part[z][m][n] in a fixed order, for part blocks [ksplit][M][N].
@@ -982,7 +1017,7 @@ struct PfWs {
 // split, the pass that adds the partial tiles (at `part`) into C.
 template <class P, typename TC, bool Wide>
 hipError_t launch_grid(const _Float16* a16, int lda, const PfSeg* segs, int nseg, int M, int K, int ksplit,
-                       float* part, hipStream_t stream) {
+                       float* part, const float* rs, hipStream_t stream) {
     constexpr int BM = Wide ? kWBM : kBM, BN = Wide ? kWBN : kBN, BK = Wide ? kWBK : 64 * P::kH;
     constexpr int threads = Wide ? kWThreads : kThreads;
     const int tiles_m = (M + BM - 1) / BM;
@@ -990,6 +1025,7 @@ hipError_t launch_grid(const _Float16* a16, int lda, const PfSeg* segs, int nseg
     const int klen = ((steps + ksplit - 1) / ksplit) * BK;
     ksplit = (steps * BK + klen - 1) / klen;
     PfSegs<TC> sg;
+    sg.rs = rs;
     size_t off = 0;
     int tiles_n = 0;
     for (int i = 0; i < kPfMaxSegs; ++i) {
@@ -1092,7 +1128,9 @@ hipError_t launch_p(const void* A, const PfSeg* segs, int nseg, int M, int K, hi
 
     const bool direct = sizeof(TA) == 2 && K % BK == 0 && (reinterpret_cast<uintptr_t>(A) & 15u) == 0;
     const int lda = direct ? K : steps * BK;
-    const size_t a_bytes = direct ? 0 : static_cast<size_t>(M) * lda * 2;
+    // f16 copy of the activations, then (fp32 activations) the rows' output factors
+    const size_t a16_bytes = direct ? 0 : ((static_cast<size_t>(M) * lda * 2 + 255) / 256) * 256;
+    const size_t a_bytes = a16_bytes + (sizeof(TA) == 4 ? static_cast<size_t>(M) * 4 : 0);
     size_t p_bytes = 0;
     if (plan.ksplit > 1) p_bytes = static_cast<size_t>(plan.ksplit) * M * n_total * 4;
     if (plan.tail_n > 0) p_bytes = static_cast<size_t>(plan.tail_ks) * M * n_tail_total * 4;
@@ -1106,18 +1144,25 @@ hipError_t launch_p(const void* A, const PfSeg* segs, int nseg, int M, int K, hi
         return e;
     }
     const _Float16* a16 = static_cast<const _Float16*>(A);
+    float* rs = nullptr;
     if (!direct) {
         _Float16* dst = static_cast<_Float16*>(ws);
-        const int64_t n8 = static_cast<int64_t>(M) * (lda / 8);
-        hipLaunchKernelGGL((to_f16_kernel<TA>), dim3(static_cast<unsigned>((n8 + 255) / 256)), dim3(256), 0, stream,
-                           static_cast<const TA*>(A), dst, M, K, lda);
+        if constexpr (sizeof(TA) == 4) {
+            rs = reinterpret_cast<float*>(static_cast<char*>(ws) + a16_bytes);
+            hipLaunchKernelGGL(to_f16_rows_kernel, dim3(static_cast<unsigned>(M)), dim3(256), 0, stream,
+                               static_cast<const float*>(A), dst, rs, K, lda);
+        } else {
+            const int64_t n8 = static_cast<int64_t>(M) * (lda / 8);
+            hipLaunchKernelGGL((to_f16_kernel<TA>), dim3(static_cast<unsigned>((n8 + 255) / 256)), dim3(256), 0, stream,
+                               static_cast<const TA*>(A), dst, M, K, lda);
+        }
         if ((e = hipGetLastError()) != hipSuccess) return e;
         a16 = dst;
     }
     float* part = p_bytes > 0 ? reinterpret_cast<float*>(static_cast<char*>(ws) + ((a_bytes + 255) / 256) * 256) : nullptr;
-    if (plan.tail_n == 0) return launch_grid<P, TC, Wide>(a16, lda, segs, nseg, M, K, plan.ksplit, part, stream);
-    if ((e = launch_grid<P, TC, Wide>(a16, lda, main_segs, n_main, M, K, 1, nullptr, stream)) != hipSuccess) return e;
-    return launch_grid<P, TC, Wide>(a16, lda, tail_segs, n_tail, M, K, plan.tail_ks, part, stream);
+    if (plan.tail_n == 0) return launch_grid<P, TC, Wide>(a16, lda, segs, nseg, M, K, plan.ksplit, part, rs, stream);
+    if ((e = launch_grid<P, TC, Wide>(a16, lda, main_segs, n_main, M, K, 1, nullptr, rs, stream)) != hipSuccess) return e;
+    return launch_grid<P, TC, Wide>(a16, lda, tail_segs, n_tail, M, K, plan.tail_ks, part, rs, stream);
 }
 
 // HN: 64-k halves per step of the 128 x 256 kernel for this format.
