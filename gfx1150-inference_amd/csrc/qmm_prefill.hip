@@ -41,6 +41,11 @@
 #ifndef QMM_PF_WIDE_VALU
 #define QMM_PF_WIDE_VALU 3
 #endif
+// The wide tile is used while its tiles cover at least 1 / QMM_PF_WIDE_MIN of the CUs (K is
+// split over workgroups below that).
+#ifndef QMM_PF_WIDE_MIN
+#define QMM_PF_WIDE_MIN 2
+#endif
 
 namespace qmm {
 namespace {
@@ -990,7 +995,7 @@ bool use_wide(int M, int64_t wide_tiles_n, int K, int cus) {
     const int64_t pad128 = (static_cast<int64_t>(M) + kBM - 1) / kBM * kBM;
     const int64_t lda = (static_cast<int64_t>(K) + kWBK - 1) / kWBK * kWBK;
     const int64_t tiles = (pad256 / kWBM) * wide_tiles_n;
-    return M >= kWBM && pad256 <= pad128 + 64 && 2 * tiles >= cus && static_cast<int64_t>(M) * lda < (int64_t{1} << 31);
+    return M >= kWBM && pad256 <= pad128 + 64 && QMM_PF_WIDE_MIN * tiles >= cus && static_cast<int64_t>(M) * lda < (int64_t{1} << 31);
 #else
     (void)M, (void)wide_tiles_n, (void)K, (void)cus;
     return false;

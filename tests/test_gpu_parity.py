@@ -85,6 +85,30 @@ def test_dequant_synthetic_bit_exact(dev, t, out):
 
 
 @pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("blocks", [1, 3, 9, 13, 257])
+def test_dequant_ragged_sizes_leave_tail_untouched(dev, t, blocks):
+    """Sizes that are not whole multiples of 256 weights (Q4_0 / Q8_0) or of eight super-blocks,
+    written into a larger buffer: values bit-exact, the sentinel past num_elements untouched."""
+    import torch
+    import qmm
+    rng = np.random.default_rng(31 * blocks + t)
+    qk, bb = O.BLOCK_INFO[t]
+    n = blocks * qk
+    raw = O.synth_weights(t, 1, n, rng)
+    for dt, view in ((torch.float16, torch.int16), (torch.float32, torch.int32)):
+        out = torch.full((n + 512,), -7.0, dtype=dt, device=dev)
+        qmm.dequantize(t, to_dev(raw, dev), n, out=out)
+        torch.cuda.synchronize()
+        got = out.cpu()
+        want = O.DEQUANT_F32[t](raw, n)
+        if dt == torch.float16:
+            np.testing.assert_array_equal(got[:n].numpy().view(np.uint16), want.astype(np.float16).view(np.uint16))
+        else:
+            np.testing.assert_array_equal(got[:n].numpy().view(np.uint32), want.view(np.uint32))
+        assert torch.all(got[n:] == -7.0), f"{O.TYPE_NAMES[t]} n={n}: write past num_elements"
+
+
+@pytest.mark.parametrize("t", TYPES)
 def test_dequant_random_bytes_nan_aware(dev, t):
     import torch
     import qmm
