@@ -61,6 +61,11 @@ constexpr int kChunks = 8;          // 8-weight activation chunks per lane slot
 #ifndef QMM_GEMV_DEPTH
 #define QMM_GEMV_DEPTH 0
 #endif
+// Largest M whose launches switch to 16-wave workgroups when the staged activations exceed
+// 40 KB of LDS (fewer workgroups per CU fit then; larger ones keep the waves per CU up).
+#ifndef QMM_GEMV_NW16_MAXM
+#define QMM_GEMV_NW16_MAXM 2
+#endif
 
 // Register-resident constants (v_and_or_b32 on gfx9 takes no literal operands).
 struct Consts {
@@ -1498,7 +1503,8 @@ hipError_t dispatch_fast(const void* A, const Seg* segs, int nseg, int M, int K,
     // tiles use the windowed kernel at such K).
     const int nwin = (K + kGemvWindow - 1) / kGemvWindow;
     const size_t res_lds = static_cast<size_t>(min(M, 4)) * nwin * kSlotBytes;
-    if (M <= 2 && res_lds > 40 * 1024) return dispatch_rows<F, 16, TA, TC>(A, segs, nseg, M, N, K, a_vec, fz, stream);
+    if (M <= QMM_GEMV_NW16_MAXM && res_lds > 40 * 1024)
+        return dispatch_rows<F, 16, TA, TC>(A, segs, nseg, M, N, K, a_vec, fz, stream);
     return dispatch_rows<F, QMM_GEMV_NW, TA, TC>(A, segs, nseg, M, N, K, a_vec, fz, stream);
 }
 

@@ -24,9 +24,12 @@ int set_last_error(int code, const std::string& msg);
 // Frees the host-pointer entry points' staging buffers (after synchronizing each device).
 hipError_t release_host_staging();
 
-// M below this runs the GEMV family (bit-identical per row for every M);
-// M at or above it runs the MFMA prefill GEMM.
-constexpr int kGemvMaxM = 32;
+// M below this runs the GEMV family (row m bit-identical to the M = 1 call for every such M, as the
+// reference asserts for M = 4, 7 and 16: tests/test_phase5_scale.py:274-310); M at or above it
+// runs the MFMA prefill GEMM (its 32-row tile up to M = 32), whose rows agree with M = 1 within
+// the prefill bound.  The GEMV's per-row vector work grows with M, the MFMA tile's does not:
+// at M = 17..31 the 32-row tile is 3.5-6x faster on the 70B shapes.
+constexpr int kGemvMaxM = 17;
 
 inline int block_elems(int t) {
     switch (t) {

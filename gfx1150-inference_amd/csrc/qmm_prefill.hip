@@ -46,6 +46,13 @@
 #ifndef QMM_PF_WIDE_MIN
 #define QMM_PF_WIDE_MIN 2
 #endif
+// Largest M that runs the 32-row tile (one 32-row tile per weight slice when M <= 32).
+#ifndef QMM_PF_SMALL_MAXM
+#define QMM_PF_SMALL_MAXM 32
+#endif
+#ifndef QMM_PF_SMALL_FILL
+#define QMM_PF_SMALL_FILL 1
+#endif
 
 namespace qmm {
 namespace {
@@ -56,7 +63,7 @@ constexpr int kHalves = 4;      // 64-k halves per step for Q4_K / Q6_K (one sup
                                 // 32-weight block formats and F16 take 2 (fewer raw registers:
                                 // measured 2-7 % faster for Q8_0 / Q4_0, no spill for F16)
 constexpr int kThreads = 512;   // 8 waves: two per SIMD, so one wave's load stalls are covered
-constexpr int kChunksPerHalf = kBM * 64 / 8;  // 16-byte chunks (8 f16) per 64-k half stage = 1024
+constexpr int kSmallBM = 32;    // activation rows of the small-M tile (M <= kSmallBM)
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -433,13 +440,21 @@ __device__ __forceinline__ void for_each_index(F& f, std::integer_sequence<int, 
     (f(std::integral_constant<int, Q>{}), ...);
 }
 
-template <class P, typename TC>
-__global__ __launch_bounds__(kThreads, 1)
+// BM = 128 (kBM) or 32 (kSmallBM: one MFMA tile of activation rows per wave, for M <= 32, where
+// the 128-row tile would spend three quarters of its matrix-core work on padding rows; the
+// smaller tile's registers and LDS let two workgroups share a CU).
+template <class P, typename TC, int BM>
+__global__ __launch_bounds__(kThreads, BM == kBM ? 1 : 2)
 void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, float* __restrict__ part_base, int M, int K,
                     int klen, int tiles_m, int tiles_n, int ksplit) {
     constexpr int kH = P::kH;      // 64-k halves per step
     constexpr int kBK = 64 * kH;   // k per step
-    __shared__ __align__(16) u32x4p sA[2][kH * kChunksPerHalf];
+    constexpr int NI = BM / 32;    // 32 x 32 MFMA tiles of activation rows per wave
+    constexpr int CPH = BM * 8;    // 16-byte chunks (8 f16) per 64-k half stage
+    constexpr int NJ = CPH >= kThreads ? CPH / kThreads : 1;  // chunks per thread and half
+    constexpr int kAThreads = CPH >= kThreads ? kThreads : CPH;  // threads that stage chunks
+    static_assert(BM % 32 == 0 && (CPH % kThreads == 0 || kThreads % CPH == 0), "tile shape");
+    __shared__ __align__(16) u32x4p sA[2][kH * CPH];
 
     // Tile order: m fastest, then n-tile, then k split; blocks sharing a weight slice (same
     // n-tile and k range, different m) are consecutive and dealt to one XCD.
@@ -455,12 +470,14 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
     const int N = sg.N[sgi];
     const int ldc = sg.ldc[sgi];
     float* __restrict__ part = part_base + sg.part_off[sgi];
-    const int m0 = tm * kBM, n0 = tn * kBN;
+    const int m0 = tm * BM, n0 = tn * kBN;
     const int kb = kz * klen;
     const int kend = min(K, kb + klen);
     const int nsteps = (kend - kb + kBK - 1) / kBK;
 
     const int tid = threadIdx.x;
+    // threads past the chunk count (small tile) load a copy of another thread's chunks, store nothing
+    const bool a_owner = kAThreads == kThreads || tid < kAThreads;
     const int lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5;
@@ -469,49 +486,50 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
     const size_t row_bytes = static_cast<size_t>(K / P::kQK) * P::kBytes;
     const uint8_t* wrow = W + static_cast<size_t>(min(n0 + 32 * wv + l32, N - 1)) * row_bytes;
 
-    // Thread tid copies half-stage chunks p = tid + 512 j (j = 0..1) of both halves: row p >> 3,
-    // chunk (p & 7) ^ swizzle, so each thread's 4 global reads are 16-byte aligned f16 runs and
+    // Thread tid copies half-stage chunks p = tid + 512 j (j < NJ) of every half: row p >> 3,
+    // chunk (p & 7) ^ swizzle, so each thread's global reads are 16-byte aligned f16 runs and
     // its LDS writes are in place.
-    const _Float16* arow[2];
-    int apos[2];
+    const _Float16* arow[NJ];
+    int apos[NJ];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int p = tid + 512 * j;
+    for (int j = 0; j < NJ; ++j) {
+        const int p = (kAThreads == kThreads ? tid : tid % kAThreads) + kThreads * j;
         const int r = p >> 3;
         const int c = (p & 7) ^ ((r >> 1) & 7);
         arow[j] = A16 + static_cast<size_t>(min(m0 + r, M - 1)) * lda + kb + 8 * c;
         apos[j] = p;
     }
-    auto load_a = [&](int t, u32x4p (&ar)[2 * kH]) {
+    auto load_a = [&](int t, u32x4p (&ar)[NJ * kH]) {
         const int kk = min(t, nsteps - 1) * kBK;  // past the end: re-read the last step
 #pragma unroll
         for (int u = 0; u < kH; ++u)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) ar[2 * u + j] = *reinterpret_cast<const u32x4p*>(arow[j] + kk + 64 * u);
+            for (int j = 0; j < NJ; ++j) ar[NJ * u + j] = *reinterpret_cast<const u32x4p*>(arow[j] + kk + 64 * u);
     };
-    auto store_a = [&](int slot, const u32x4p (&ar)[2 * kH]) {
+    auto store_a = [&](int slot, const u32x4p (&ar)[NJ * kH]) {
+        if (!a_owner) return;
 #pragma unroll
         for (int u = 0; u < kH; ++u)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) sA[slot][kChunksPerHalf * u + apos[j]] = ar[2 * u + j];
+            for (int j = 0; j < NJ; ++j) sA[slot][CPH * u + apos[j]] = ar[NJ * u + j];
     };
     auto load_raw = [&](int t, typename P::Raw& raw) {
         const int k0 = kb + min(t, nsteps - 1) * kBK;
         raw = P::load(wrow, k0, h, kend - k0);
     };
     // activation fragments of sub-step (U, S) of the step held in `slot`
-    auto read_a = [&](int slot, int U, int S, f16x8 (&af)[4]) {
-        const u32x4p* sa = sA[slot] + kChunksPerHalf * U;
+    auto read_a = [&](int slot, int U, int S, f16x8 (&af)[NI]) {
+        const u32x4p* sa = sA[slot] + CPH * U;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < NI; ++i) {
             const u32x4p av = sa[a_slot(32 * i + l32, a_chunk(S, h))];
             __builtin_memcpy(&af[i], &av, 16);
         }
     };
 
-    f32x16 acc[4];
+    f32x16 acc[NI];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
 
@@ -530,11 +548,11 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
     // one barrier per step covers both the write-after-read and the read-after-write order.
     using Raw = typename P::Raw;
     using Sc = typename P::Sc;
-    u32x4p an[2 * kH];
+    u32x4p an[NJ * kH];
     Raw cur, nxt;
     Sc sc[2];          // [half]
     uint32_t wf[2][4]; // [buffer][dword]
-    f16x8 af[2][4];    // [buffer][i]
+    f16x8 af[2][NI];   // [buffer][i]
 
     load_raw(0, cur);
     load_a(0, an);
@@ -573,8 +591,8 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
             f16x8 bw;
             __builtin_memcpy(&bw, wf[B], 16);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bw, af[B][i], acc[i], 0, 0, 0);
-            interleave_substep<5>();
+            for (int i = 0; i < NI; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bw, af[B][i], acc[i], 0, 0, 0);
+            if constexpr (NI == 4) interleave_substep<5>();
             __builtin_amdgcn_sched_barrier(0);
         };
         for_each_index(sub, std::make_integer_sequence<int, kQ>{});
@@ -584,7 +602,7 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
     // D element v of tile i: weight row n = n0 + 32wv + 8(v/4) + 4h + v%4, activation row
     // m = m0 + 32i + l32.
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NI; ++i) {
         const int m = m0 + 32 * i + l32;
         if (m >= M) continue;
 #pragma unroll
@@ -1017,14 +1035,26 @@ struct PfWs {
     size_t need;
 };
 
-// One launch of the 128 x 256 (Wide = false) or 256 x 256 (Wide = true) tile kernel over `segs`
-// with K split `ksplit` ways (at most; the split length is a whole number of steps), then, for a
-// split, the pass that adds the partial tiles (at `part`) into C.
-template <class P, typename TC, bool Wide>
+// Tile kinds: 128 x 256, 256 x 256 (wide) and 32 x 256 (small M).
+enum PfTile { kTileStd = 0, kTileWide = 1, kTileSmall = 2 };
+template <class P, int Tile>
+struct PfShape {
+    static constexpr bool kWide = Tile == kTileWide;
+    static constexpr int BM = kWide ? kWBM : Tile == kTileSmall ? kSmallBM : kBM;
+    static constexpr int BN = kWide ? kWBN : kBN;
+    static constexpr int BK = kWide ? kWBK : 64 * P::kH;
+    static constexpr int threads = kWide ? kWThreads : kThreads;
+};
+
+// One launch of the tile kernel `Tile` over `segs` with K split `ksplit` ways (at most; the split
+// length is a whole number of steps), then, for a split, the pass that adds the partial tiles (at
+// `part`) into C.
+template <class P, typename TC, int Tile>
 hipError_t launch_grid(const _Float16* a16, int lda, const PfSeg* segs, int nseg, int M, int K, int ksplit,
                        float* part, const float* rs, hipStream_t stream) {
-    constexpr int BM = Wide ? kWBM : kBM, BN = Wide ? kWBN : kBN, BK = Wide ? kWBK : 64 * P::kH;
-    constexpr int threads = Wide ? kWThreads : kThreads;
+    using Sh = PfShape<P, Tile>;
+    constexpr int BM = Sh::BM, BN = Sh::BN, BK = Sh::BK;
+    constexpr int threads = Sh::threads;
     const int tiles_m = (M + BM - 1) / BM;
     const int steps = (K + BK - 1) / BK;
     const int klen = ((steps + ksplit - 1) / ksplit) * BK;
@@ -1045,11 +1075,11 @@ hipError_t launch_grid(const _Float16* a16, int lda, const PfSeg* segs, int nseg
         if (used && ksplit > 1) off += static_cast<size_t>(ksplit) * M * segs[i].N;
     }
     const int tiles = tiles_m * tiles_n * ksplit;
-    if constexpr (Wide)
+    if constexpr (Sh::kWide)
         hipLaunchKernelGGL((prefill_wide_kernel<P, TC>), dim3(tiles), dim3(threads), 0, stream, a16, lda, sg,
                            ksplit > 1 ? part : nullptr, M, K, klen, tiles_m, tiles_n, ksplit);
     else
-        hipLaunchKernelGGL((prefill_kernel<P, TC>), dim3(tiles), dim3(threads), 0, stream, a16, lda, sg,
+        hipLaunchKernelGGL((prefill_kernel<P, TC, BM>), dim3(tiles), dim3(threads), 0, stream, a16, lda, sg,
                            ksplit > 1 ? part : nullptr, M, K, klen, tiles_m, tiles_n, ksplit);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -1077,9 +1107,9 @@ struct PfPlan {
     int tail_ks = 1;
 };
 
-PfPlan plan_prefill(bool wide, int tiles_m, int tiles_n, int steps, int bk, int cus) {
+PfPlan plan_prefill(bool wide, int tiles_m, int tiles_n, int steps, int bk, int cus, int fill = 1) {
     PfPlan p;
-    while (tiles_m * tiles_n * p.ksplit * 2 <= cus && steps / (p.ksplit * 2) >= 1024 / bk) p.ksplit *= 2;
+    while (tiles_m * tiles_n * p.ksplit * 2 <= fill * cus && steps / (p.ksplit * 2) >= 1024 / bk) p.ksplit *= 2;
     if (!wide || p.ksplit > 1 || steps < 32) return p;
     const int64_t T = static_cast<int64_t>(tiles_m) * tiles_n;
     const int64_t r = T % cus;
@@ -1094,9 +1124,10 @@ PfPlan plan_prefill(bool wide, int tiles_m, int tiles_n, int steps, int bk, int 
     return p;
 }
 
-template <class P, typename TA, typename TC, bool Wide>
+template <class P, typename TA, typename TC, int Tile>
 hipError_t launch_p(const void* A, const PfSeg* segs, int nseg, int M, int K, hipStream_t stream, PfWs* ext) {
-    constexpr int BM = Wide ? kWBM : kBM, BN = Wide ? kWBN : kBN, BK = Wide ? kWBK : 64 * P::kH;
+    using Sh = PfShape<P, Tile>;
+    constexpr int BM = Sh::BM, BN = Sh::BN, BK = Sh::BK;
     int cus = 0;
     hipError_t e = cu_count(cus);
     if (e != hipSuccess) return e;
@@ -1108,7 +1139,8 @@ hipError_t launch_p(const void* A, const PfSeg* segs, int nseg, int M, int K, hi
         n_total += segs[i].N;
     }
     const int steps = (K + BK - 1) / BK;
-    const PfPlan plan = plan_prefill(Wide, tiles_m, tiles_n, steps, BK, cus);
+    // the small tile's workgroups fit QMM_PF_SMALL_FILL to a CU (its grid is split to fill them)
+    const PfPlan plan = plan_prefill(Sh::kWide, tiles_m, tiles_n, steps, BK, cus, Tile == kTileSmall ? QMM_PF_SMALL_FILL : 1);
 
     // the tail launch's segments: rows from n-tile ns on, as column ranges of the callers' C
     PfSeg main_segs[kPfMaxSegs], tail_segs[kPfMaxSegs];
@@ -1165,9 +1197,9 @@ hipError_t launch_p(const void* A, const PfSeg* segs, int nseg, int M, int K, hi
         a16 = dst;
     }
     float* part = p_bytes > 0 ? reinterpret_cast<float*>(static_cast<char*>(ws) + ((a_bytes + 255) / 256) * 256) : nullptr;
-    if (plan.tail_n == 0) return launch_grid<P, TC, Wide>(a16, lda, segs, nseg, M, K, plan.ksplit, part, rs, stream);
-    if ((e = launch_grid<P, TC, Wide>(a16, lda, main_segs, n_main, M, K, 1, nullptr, rs, stream)) != hipSuccess) return e;
-    return launch_grid<P, TC, Wide>(a16, lda, tail_segs, n_tail, M, K, plan.tail_ks, part, rs, stream);
+    if (plan.tail_n == 0) return launch_grid<P, TC, Tile>(a16, lda, segs, nseg, M, K, plan.ksplit, part, rs, stream);
+    if ((e = launch_grid<P, TC, Tile>(a16, lda, main_segs, n_main, M, K, 1, nullptr, rs, stream)) != hipSuccess) return e;
+    return launch_grid<P, TC, Tile>(a16, lda, tail_segs, n_tail, M, K, plan.tail_ks, part, rs, stream);
 }
 
 // HN: 64-k halves per step of the 128 x 256 kernel for this format.
@@ -1178,8 +1210,9 @@ hipError_t launch_family(const void* A, const PfSeg* segs, int nseg, int M, int 
     if (e != hipSuccess) return e;
     int64_t wide_tiles_n = 0;
     for (int i = 0; i < nseg; ++i) wide_tiles_n += (segs[i].N + kWBN - 1) / kWBN;
-    if (use_wide(M, wide_tiles_n, K, cus)) return launch_p<PF<kWH>, TA, TC, true>(A, segs, nseg, M, K, stream, ext);
-    return launch_p<PF<HN>, TA, TC, false>(A, segs, nseg, M, K, stream, ext);
+    if (use_wide(M, wide_tiles_n, K, cus)) return launch_p<PF<kWH>, TA, TC, kTileWide>(A, segs, nseg, M, K, stream, ext);
+    if (M <= QMM_PF_SMALL_MAXM) return launch_p<PF<HN>, TA, TC, kTileSmall>(A, segs, nseg, M, K, stream, ext);
+    return launch_p<PF<HN>, TA, TC, kTileStd>(A, segs, nseg, M, K, stream, ext);
 }
 
 template <typename TA, typename TC>

@@ -63,8 +63,9 @@ size_t qmm_weight_bytes(int ggml_type, int64_t n, int64_t k);
  * --------------------------------------------------------------------------------- */
 
 /* C[M,N] (c_dtype) = A[M,K] (a_dtype) @ dequant(W)[N,K]^T with fp32 accumulation.
- * M < QMM_GEMV_MAX_M runs the bandwidth-bound GEMV family, whose row m result is
- * bit-identical for every M; larger M runs the f16-MFMA prefill GEMM.
+ * M < qmm_gemv_max_m() (17) runs the bandwidth-bound GEMV family, whose row m result is
+ * bit-identical for every such M; larger M runs the f16-MFMA prefill GEMM (a 32-row tile up
+ * to M = 32), whose rows agree with the M = 1 call within the prefill accuracy bound.
  * Generalises launch_matmul_q{4_0,8_0,4_k,6_k}_device (reference
  * src/kernels/dequantize.h:98-132, dispatch at dequantize.hip:778/896/1014/1132). */
 int qmm_gemm(int ggml_type, const void* A, int a_dtype, const void* W, void* C, int c_dtype,
@@ -126,7 +127,7 @@ int qmm_dequantize(int ggml_type, const void* W, void* out, int out_dtype,
 int qmm_embed(int ggml_type, const void* table, int64_t n_rows, int hidden, const int64_t* ids,
               int64_t n_ids, void* out, int out_dtype, int* bad, void* stream);
 
-/* Largest M served by the GEMV family (exclusive bound), and the prefill threshold. */
+/* Largest M served by the GEMV family (exclusive bound; 17), and the prefill threshold. */
 int qmm_gemv_max_m(void);
 
 /* Per-type device launchers with the reference's argument meaning: fp16 A [M,K],

@@ -4,7 +4,7 @@ the drop-in ``matmul_module`` entry points for the dense matmuls and the layer o
 Bars (written into each check):
 * F16 GEMM through the C ABI: the operands are exact fp16 values, so against the fp64 product of
   the same values max_i|y - y64| / max_i|y64| <= 1e-5 with fp32 output (fp32 accumulation only);
-* GEMV sizes give row results bit-identical for every M < 32, fused launches bit-identical to
+* GEMV sizes give row results bit-identical for every M < qmm_gemv_max_m, fused launches bit-identical to
   single ones;
 * matmul_module functions: the reference tests' own bars (tests/test_layer.py) against the CPU
   restatement in oracle/layer_oracle.py: 2e-3 absolute per kernel, 5e-3 for a whole layer;
@@ -62,7 +62,8 @@ def gemm_f16(A, W, dev, out_dtype="f32"):
     return C.float().cpu().numpy()
 
 
-# GEMV fast path (K % 16 == 0), GEMV fallback (K % 16 != 0), prefill (M >= 32, K % 8 == 0),
+# GEMV fast path (K % 16 == 0), GEMV fallback (K % 16 != 0), prefill (M >= 17, K % 8 == 0; the
+# 32-row tile up to M = 32),
 # prefill-unsupported K (K % 8 != 0: the fallback GEMV serves every M).
 @pytest.mark.parametrize("M,N,K", [(1, 300, 4096), (3, 129, 8192 + 64), (31, 64, 640), (1, 40, 200), (5, 17, 1001),
                                    (32, 300, 512), (100, 513, 1000), (64, 256, 4104), (40, 33, 99)])
@@ -83,9 +84,11 @@ def test_f16_gemm_wide_tile(dev):
 
 
 def test_f16_gemv_rows_bit_identical_across_m(dev):
-    A, W = dense_case(5, 31, 777, 2048)
+    import qmm
+    mmax = qmm.gemv_max_m() - 1
+    A, W = dense_case(5, mmax, 777, 2048)
     full = gemm_f16(A, W, dev)
-    for M in (1, 2, 4, 7, 16):
+    for M in (1, 2, 4, 7, mmax):
         assert np.array_equal(gemm_f16(A[:M], W, dev), full[:M])
 
 

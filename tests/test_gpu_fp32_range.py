@@ -82,9 +82,10 @@ def test_gemv_fp32_beyond_f16_range(dev, t, K):
 
 
 @pytest.mark.parametrize("t", [O.GGML_Q4_K, O.GGML_Q6_K, O.GGML_Q8_0])
-def test_prefill_fp32_beyond_f16_range(dev, t):
-    rng = np.random.default_rng(7 + t)
-    M, N, K = 48, 256, 4096
+@pytest.mark.parametrize("M", [48, 20])  # 128-row and 32-row tiles
+def test_prefill_fp32_beyond_f16_range(dev, t, M):
+    rng = np.random.default_rng(7 + t + M)
+    N, K = 256, 4096
     w, w64 = weights(t, N, K, rng)
     x = rng.standard_normal((M, K)).astype(np.float32)
     x[0] *= 1e6

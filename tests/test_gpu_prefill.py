@@ -70,7 +70,8 @@ def sampled_cols(rng, N):
 
 def test_prefill_threshold(dev):
     import qmm
-    assert qmm.gemv_max_m() == 32
+    # M <= 16 stays in the GEMV family: the reference asserts M = 4, 7, 16 bit-identical to M = 1
+    assert qmm.gemv_max_m() == 17
 
 
 @pytest.mark.parametrize("t", TYPES)
@@ -82,6 +83,25 @@ def test_prefill_vs_fp64_and_f16_operands(dev, t):
         y = run(t, x, raw, N, K, dev)
         assert O.max_rel_err(y, O.matmul_f64(t, x, raw, N, K)) <= TOL_F64, (O.TYPE_NAMES[t], M, N, K)
         assert O.max_rel_err(y, O.matmul_f16_operands(t, x, raw, N, K)) <= TOL_F16, (O.TYPE_NAMES[t], M, N, K)
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_prefill_small_tile_vs_fp64_and_f16_operands(dev, t):
+    """M = 17..32 run the 32-row tile: the threshold row count, ragged M, N and K tails, fp16
+    activations and outputs, and a long K over few tiles (split over workgroups, then summed)."""
+    rng = np.random.default_rng(4200 + t)
+    kq = t in (O.GGML_Q4_K, O.GGML_Q6_K)
+    cases = [(17, 256, 512, False), (24, 300, 1024 if kq else 544, True), (31, 257, 256 if kq else 96, False),
+             (32, 512, 8192, True), (20, 64, 4096, False)]
+    for M, N, K, half in cases:
+        raw = O.synth_weights(t, N, K, rng)
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        if half:
+            x = x.astype(np.float16).astype(np.float32)
+        y = run(t, x, raw, N, K, dev, a16=half, c16=half)
+        tol16 = 1e-3 if half else TOL_F16  # fp16 outputs round to 2^-11 relative
+        assert O.max_rel_err(y, O.matmul_f64(t, x, raw, N, K)) <= TOL_F64, (O.TYPE_NAMES[t], M, N, K)
+        assert O.max_rel_err(y, O.matmul_f16_operands(t, x, raw, N, K)) <= tol16, (O.TYPE_NAMES[t], M, N, K)
 
 
 @pytest.mark.parametrize("t", TYPES)
