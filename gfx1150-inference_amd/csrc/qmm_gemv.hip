@@ -1498,10 +1498,18 @@ hipError_t dispatch_fast(const void* A, const Seg* segs, int nseg, int M, int K,
                          hipStream_t stream) {
     int N = 0;
     for (int j = 0; j < nseg; ++j) N += segs[j].N;
+    // M > 4: blocks of 8 activation rows (two weight rows per wave item) stream the weights half as
+    // often as blocks of 4 (70B down at M = 8: 149 -> 110 us, gate 86 -> 79 us), where they add
+    // no padded row over the 4-row tiling (M % 8 == 0 or >= 5).  F16, and fp32 activations beyond
+    // two windows (resident LDS), keep 4-row blocks: their 8-row windowed kernels would spill.
+    const int nwin = (K + kGemvWindow - 1) / kGemvWindow;
+    if constexpr (F::kType != QMM_TYPE_F16) {
+        if (M > 4 && !fz.pair && (M % 8 == 0 || M % 8 >= 5) && (std::is_same<TA, __half>::value || nwin <= 2))
+            return launch_fast<F, 8, 2, 8, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
+    }
     // Resident activations above 40 KB of LDS leave room for at most three workgroups per CU:
     // 16-wave workgroups then keep more waves (bytes in flight) per CU.  M = 1, 2 only (larger M
     // tiles use the windowed kernel at such K).
-    const int nwin = (K + kGemvWindow - 1) / kGemvWindow;
     const size_t res_lds = static_cast<size_t>(min(M, 4)) * nwin * kSlotBytes;
     if (M <= QMM_GEMV_NW16_MAXM && res_lds > 40 * 1024)
         return dispatch_rows<F, 16, TA, TC>(A, segs, nseg, M, N, K, a_vec, fz, stream);

@@ -175,7 +175,7 @@ GEMV_SHAPES = {
 
 
 @pytest.mark.parametrize("t", TYPES)
-@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 8])
 def test_gemv_vs_fp64(dev, t, M):
     rng = np.random.default_rng(1000 * t + M)
     for N, K in GEMV_SHAPES[t]:
@@ -209,9 +209,32 @@ def test_gemv_rows_bit_identical_across_m(dev, t):
         Mmax = min(qmm.gemv_max_m() - 1, 31)
         x = rng.standard_normal((Mmax, K)).astype(np.float32)
         single = np.stack([gemm(t, x[m:m + 1], raw, N, K, dev)[0] for m in range(Mmax)])
-        for M in (2, 3, 4, 7, 16, Mmax):
+        # 4-row blocks (M % 8 in 1..4) and 8-row blocks (M % 8 == 0 or >= 5)
+        for M in sorted({2, 3, 4, 5, 7, 8, 9, 12, 13, 16, Mmax}):
             y = gemm(t, x[:M], raw, N, K, dev)
             np.testing.assert_array_equal(y, single[:M], err_msg=f"{O.TYPE_NAMES[t]} M={M} N={N} K={K}")
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_gemv_rows_bit_identical_across_m_windowed_f16_io(dev, t):
+    """fp16 activations and outputs at K = 16384 (four windows: the 8-row blocks take the windowed
+    kernel, the M = 1 call the resident one): every row equals its M = 1 call bit for bit."""
+    import torch
+    import qmm
+    rng = np.random.default_rng(701 + t)
+    N, K = 80, 16384
+    raw = O.synth_weights(t, N, K, rng)
+    x = rng.standard_normal((16, K)).astype(np.float16)
+    W = torch.from_numpy(raw).to(dev)
+
+    def run(a):
+        C = qmm.gemm(t, torch.from_numpy(np.ascontiguousarray(a)).to(dev), W, N, K, out_dtype=torch.float16)
+        torch.cuda.synchronize()
+        return C.cpu().numpy()
+    single = np.concatenate([run(x[m:m + 1]) for m in range(16)])
+    for M in (5, 8, 13, 16):
+        np.testing.assert_array_equal(run(x[:M]).view(np.uint16), single[:M].view(np.uint16),
+                                      err_msg=f"{O.TYPE_NAMES[t]} M={M}")
 
 
 @pytest.mark.parametrize("t", TYPES)
