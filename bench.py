@@ -351,10 +351,11 @@ def time_gemv(torch, qmm, hip, weights, t, n, k, M, io, reps):
     return us
 
 
-def run_small_m(torch, qmm, hip, gen, dev, Ms=(1, 4, 8, 16, 31)):
-    """Small-M GEMV (prompt chunks shorter than the prefill threshold, src/inference.py:255-286)
-    on the 70B gate (Q4_K 28672 x 8192) and down (Q6_K 8192 x 28672) shapes, fp16 I/O: µs per
-    call and algorithmic GB/s (weights once + activations + outputs)."""
+def run_small_m(torch, qmm, hip, gen, dev, Ms=(1, 4, 8, 12, 16, 17, 24, 31)):
+    """Small M (prompt chunks of fewer than 32 tokens, src/inference.py:255-286) on the 70B gate
+    (Q4_K 28672 x 8192) and down (Q6_K 8192 x 28672) shapes, fp16 I/O: µs per call and algorithmic
+    GB/s (weights once + activations + outputs).  M <= 16 runs the GEMV (4- or 8-row blocks), M >= 17
+    the 32-row MFMA tile."""
     res = {}
     for name, t, n, k, copies in (("gate_q4_k_28672x8192", Q4_K, 28672, 8192, 12),
                                   ("down_q6_k_8192x28672", Q6_K, 8192, 28672, 8)):
@@ -709,6 +710,9 @@ def main():
                          "print its results as JSON")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run only the counter-collection workload (copy calibration + dominant GEMV)")
+    ap.add_argument("--small-m-only", action="store_true",
+                    help="run only the small-M (70B gate / down at M = 1..31) and dequantize sections and print "
+                         "their results as JSON")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -728,6 +732,10 @@ def main():
     log(f"device {props.name} {getattr(props, 'gcnArchName', '')} CUs={props.multi_processor_count}")
     if args.pmc_workload:
         pmc_workload(torch, qmm, dev, gen)
+        return
+    if args.small_m_only:
+        print(json.dumps({"70b_small_m": run_small_m(torch, qmm, hip, gen, dev),
+                          "dequant_70b": run_dequant(torch, qmm, hip, gen, dev)}), flush=True)
         return
     if args.prefill_only:
         print(json.dumps({"prefill_8b_m512": run_prefill(torch, qmm, hip, gen, dev, max(3, args.steps // 2), 2)}),

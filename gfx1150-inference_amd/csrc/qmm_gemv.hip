@@ -15,7 +15,11 @@
 //         sum_k x_k * w_k = a_g * S_g - B_g * sx_g,   S_g = sum_k x_k * (1024 + q_k),
 //     where sx_g is the sum of the group's fp16 activations and B_g folds the 1024 offset, the
 //     format's code offset and the Q4_K min.  All products are exact; only fp32 sums round.
-//   * fp32 activations are rounded to fp16 once, when staged (|x| must stay below 65504).
+//   * fp32 activations are rounded to fp16 once, when staged; a (row, window) whose largest
+//     magnitude lies outside f16's range is staged scaled by a power of two that the window's
+//     group coefficients undo exactly (window_exp below).
+//   * Activation rows are tiled in blocks of MR = 1, 2, 4 or 8 per workgroup (all rows of a
+//     block share each weight byte loaded); blocks of 8 for M > 4 where they add no padded rows.
 //   * The arithmetic of row (m, n) is the same instruction sequence for every M, YT and grid,
 //     so every M < kGemvMaxM is bit-identical to M = 1 (the reference's prefill-vs-M=1
 //     invariant, tests/test_phase5_scale.py:274-310); the cross-lane reduction is a fixed DPP

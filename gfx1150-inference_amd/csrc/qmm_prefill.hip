@@ -12,6 +12,8 @@
 //     Q4_K / Q6_K super-block per weight row, so each row's bytes arrive in one batch); wave w
 //     owns weight rows [32w, 32w + 32) of the tile and all 128 activation rows (4 MFMA tiles of
 //     32 x 32, fp32 accumulators).
+//   * M <= 32 (from kGemvMaxM = 17 up): the same kernel with a 32-row activation tile, one MFMA
+//     tile per wave; its smaller register and LDS footprint fits two workgroups per CU.
 //   * Activation tiles (128 x 256 f16, 64 KiB) are double-buffered in LDS: the next step's tile
 //     is loaded into registers during the current step and written to the free slot near its end
 //     (one barrier per step).
