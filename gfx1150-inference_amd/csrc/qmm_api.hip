@@ -4,6 +4,7 @@
 // Error conventions follow the reference launchers (src/kernels/dequantize.hip:7-15, 734-736,
 // 771-773): a shape the block format cannot represent is QMM_ERR_INVALID_ARGUMENT (the
 // reference's std::invalid_argument), a HIP failure is QMM_ERR_HIP (std::runtime_error).
+#include <atomic>
 #include <cmath>
 #include <mutex>
 #include <string>
@@ -14,6 +15,7 @@
 namespace {
 
 thread_local std::string g_last_error;
+std::atomic<int> g_gemv_max_m{qmm::kGemvMaxMDefault};  // qmm_set_gemv_max_m
 
 int fail(int code, const std::string& msg) {
     g_last_error = msg;
@@ -82,13 +84,14 @@ int check_dequant_args(int t, const void* W, void* out, int out_dtype, int64_t n
     return QMM_OK;
 }
 
+// gmax: the GEMV / prefill threshold the call was issued under (qmm::gemv_max_m() read once).
 int gemm_impl(int t, const void* A, int a_dtype, const void* W, void* C, int c_dtype, int M, int N, int K,
-              hipStream_t stream) {
+              hipStream_t stream, int gmax) {
     int rc = check_gemm_args(t, A, a_dtype, W, C, c_dtype, M, N, K);
     if (rc != QMM_OK) return rc;
     if (M == 0 || N == 0) return QMM_OK;
     hipError_t e;
-    if (M >= qmm::kGemvMaxM && qmm::gemm_prefill_supported(t, a_dtype, c_dtype, M, N, K, A, W, C))
+    if (M >= gmax && qmm::gemm_prefill_supported(t, a_dtype, c_dtype, M, N, K, A, W, C))
         e = qmm::launch_gemm_prefill(t, A, a_dtype, W, C, c_dtype, M, N, K, stream);
     else
         e = qmm::launch_gemv(t, A, a_dtype, W, C, c_dtype, M, N, K, stream);
@@ -144,10 +147,10 @@ Span c_span(const qmm_gemm_desc& d) { return span_of(d.C, static_cast<size_t>(d.
 // Descriptors [i, j) may run as one launch: same activations, dtypes, type, M and K; no events
 // between them; no output overlapping another output or any input, so the fused launch computes
 // what the sequential launches would; and, for prefill sizes, weights the prefill kernel takes.
-bool fusable(const qmm_gemm_desc* d, int i, int j) {
+bool fusable(const qmm_gemm_desc* d, int i, int j, int gmax) {
     const qmm_gemm_desc& h = d[i];
     if (h.M <= 0) return false;
-    const bool prefill = h.M >= qmm::kGemvMaxM;
+    const bool prefill = h.M >= gmax;
     for (int x = i; x < j; ++x) {
         const qmm_gemm_desc& e = d[x];
         if (e.N <= 0 || e.A != h.A || e.a_dtype != h.a_dtype || e.ggml_type != h.ggml_type ||
@@ -182,7 +185,7 @@ int matmul_host(int t, const void* hA, const void* hB, void* hC, int M, int N, i
     if ((e = ws_ensure(ws, need)) != hipSuccess) return hip_fail(e, "workspace hipMalloc");
     if ((e = hipMemcpy(ws.buf[0], hA, sa, hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "hipMemcpy A");
     if ((e = hipMemcpy(ws.buf[1], hB, sb, hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "hipMemcpy B");
-    rc = gemm_impl(t, ws.buf[0], QMM_DTYPE_F16, ws.buf[1], ws.buf[2], QMM_DTYPE_F16, M, N, K, nullptr);
+    rc = gemm_impl(t, ws.buf[0], QMM_DTYPE_F16, ws.buf[1], ws.buf[2], QMM_DTYPE_F16, M, N, K, nullptr, qmm::gemv_max_m());
     if (rc != QMM_OK) return rc;
     if ((e = hipMemcpy(hC, ws.buf[2], sc, hipMemcpyDeviceToHost)) != hipSuccess) return hip_fail(e, "hipMemcpy C");
     return QMM_OK;
@@ -212,13 +215,23 @@ int dequant_host(int t, const void* hq, void* hout, int num_elements) {
 
 int qmm::set_last_error(int code, const std::string& msg) { return fail(code, msg); }
 
+int qmm::gemv_max_m() { return g_gemv_max_m.load(std::memory_order_relaxed); }
+
 extern "C" {
 
 const char* qmm_last_error(void) { return g_last_error.c_str(); }
 
 int qmm_version(void) { return 1000; }
 
-int qmm_gemv_max_m(void) { return qmm::kGemvMaxM; }
+int qmm_gemv_max_m(void) { return qmm::gemv_max_m(); }
+
+int qmm_set_gemv_max_m(int m) {
+    if (m < 1 || m > qmm::kGemvMaxMLimit)
+        return fail(QMM_ERR_INVALID_ARGUMENT, "qmm_set_gemv_max_m: m must be in [1, " + std::to_string(qmm::kGemvMaxMLimit) +
+                                                  "], got " + std::to_string(m) + ".");
+    g_gemv_max_m.store(m, std::memory_order_relaxed);
+    return QMM_OK;
+}
 
 size_t qmm_weight_bytes(int ggml_type, int64_t n, int64_t k) {
     if (!gemm_type(ggml_type) || n < 0 || k < 0) return 0;
@@ -229,7 +242,7 @@ size_t qmm_weight_bytes(int ggml_type, int64_t n, int64_t k) {
 
 int qmm_gemm(int ggml_type, const void* A, int a_dtype, const void* W, void* C, int c_dtype, int M, int N, int K,
              void* stream) {
-    return gemm_impl(ggml_type, A, a_dtype, W, C, c_dtype, M, N, K, static_cast<hipStream_t>(stream));
+    return gemm_impl(ggml_type, A, a_dtype, W, C, c_dtype, M, N, K, static_cast<hipStream_t>(stream), qmm::gemv_max_m());
 }
 
 int qmm_gemm_noalloc(int ggml_type, const void* A, int a_dtype, const void* W, void* C, int c_dtype, int M, int N, int K,
@@ -239,7 +252,7 @@ int qmm_gemm_noalloc(int ggml_type, const void* A, int a_dtype, const void* W, v
     if (M == 0 || N == 0) return QMM_OK;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     hipError_t e;
-    if (M >= qmm::kGemvMaxM && qmm::gemm_prefill_supported(ggml_type, a_dtype, c_dtype, M, N, K, A, W, C)) {
+    if (M >= qmm::gemv_max_m() && qmm::gemm_prefill_supported(ggml_type, a_dtype, c_dtype, M, N, K, A, W, C)) {
         size_t need = 0;
         e = qmm::launch_gemm_prefill_noalloc(ggml_type, A, a_dtype, W, C, c_dtype, M, N, K, s, &need);
         if (e == hipErrorOutOfMemory && need > qmm::kNoAllocScratchBytes)
@@ -270,12 +283,13 @@ int qmm_gemm_batch(const qmm_gemm_desc* descs, int count, void* stream) {
         if (ev && (e = hipEventRecord(static_cast<hipEvent_t>(ev), s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
         return QMM_OK;
     };
+    const int gmax = qmm::gemv_max_m();  // one threshold for the whole batch
     int i = 0;
     while (i < count) {
         // longest run starting at i that one launch can serve
-        const int max_fused = descs[i].M >= qmm::kGemvMaxM ? qmm::prefill_max_fused() : qmm::gemv_max_fused();
+        const int max_fused = descs[i].M >= gmax ? qmm::prefill_max_fused() : qmm::gemv_max_fused();
         int j = i + 1;
-        while (j < count && j - i < max_fused && fusable(descs, i, j + 1)) ++j;
+        while (j < count && j - i < max_fused && fusable(descs, i, j + 1, gmax)) ++j;
         if (j - i >= 2) {
             const void* W[8];
             void* C[8];
@@ -288,7 +302,7 @@ int qmm_gemm_batch(const qmm_gemm_desc* descs, int count, void* stream) {
             const qmm_gemm_desc& h = descs[i];
             int rc = record(h.ev_before);
             if (rc != QMM_OK) return rc;
-            hipError_t e = h.M >= qmm::kGemvMaxM
+            hipError_t e = h.M >= gmax
                                ? qmm::launch_gemm_prefill_fused(h.ggml_type, h.A, h.a_dtype, h.c_dtype, h.M, h.K, W, C, N,
                                                                 j - i, s)
                                : qmm::launch_gemv_fused(h.ggml_type, h.A, h.a_dtype, h.c_dtype, h.M, h.K, W, C, N, j - i, s);
@@ -299,7 +313,7 @@ int qmm_gemm_batch(const qmm_gemm_desc* descs, int count, void* stream) {
             }
             if (e != hipErrorNotSupported) return hip_fail(e, "qmm_gemm_batch fused kernel launch");
             // not fusable after all (e.g. byte-load fallback): run the first one alone
-            if ((rc = gemm_impl(h.ggml_type, h.A, h.a_dtype, h.W, h.C, h.c_dtype, h.M, h.N, h.K, s)) != QMM_OK) return rc;
+            if ((rc = gemm_impl(h.ggml_type, h.A, h.a_dtype, h.W, h.C, h.c_dtype, h.M, h.N, h.K, s, gmax)) != QMM_OK) return rc;
             if ((rc = record(h.ev_after)) != QMM_OK) return rc;
             ++i;
             continue;
@@ -307,7 +321,7 @@ int qmm_gemm_batch(const qmm_gemm_desc* descs, int count, void* stream) {
         const qmm_gemm_desc& d = descs[i];
         int rc = record(d.ev_before);
         if (rc != QMM_OK) return rc;
-        if ((rc = gemm_impl(d.ggml_type, d.A, d.a_dtype, d.W, d.C, d.c_dtype, d.M, d.N, d.K, s)) != QMM_OK) return rc;
+        if ((rc = gemm_impl(d.ggml_type, d.A, d.a_dtype, d.W, d.C, d.c_dtype, d.M, d.N, d.K, s, gmax)) != QMM_OK) return rc;
         if ((rc = record(d.ev_after)) != QMM_OK) return rc;
         ++i;
     }

@@ -1,4 +1,4 @@
-// Decode-path GEMV family (M < kGemvMaxM): C[m, n] = sum_k A[m, k] * dequant(W)[n, k].
+// Decode-path GEMV family (M < gemv_max_m(), 17 by default): C[m, n] = sum_k A[m, k] * dequant(W)[n, k].
 //
 // MI355X design (replaces the reference's wave32 one-output-per-wave kernels,
 // src/kernels/dequantize.hip:97-148, 152-210, 232-332, 377-505, 549-685):
@@ -21,7 +21,7 @@
 //   * Activation rows are tiled in blocks of MR = 1, 2, 4 or 8 per workgroup (all rows of a
 //     block share each weight byte loaded); blocks of 8 for M > 4 where they add no padded rows.
 //   * The arithmetic of row (m, n) is the same instruction sequence for every M, YT and grid,
-//     so every M < kGemvMaxM is bit-identical to M = 1 (the reference's prefill-vs-M=1
+//     so every M < gemv_max_m() is bit-identical to M = 1 (the reference's prefill-vs-M=1
 //     invariant, tests/test_phase5_scale.py:274-310); the cross-lane reduction is a fixed DPP
 //     sequence (no atomics, deterministic).
 #include <climits>

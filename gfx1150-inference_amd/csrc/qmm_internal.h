@@ -24,12 +24,16 @@ int set_last_error(int code, const std::string& msg);
 // Frees the host-pointer entry points' staging buffers (after synchronizing each device).
 hipError_t release_host_staging();
 
-// M below this runs the GEMV family (row m bit-identical to the M = 1 call for every such M, as the
-// reference asserts for M = 4, 7 and 16: tests/test_phase5_scale.py:274-310); M at or above it
-// runs the MFMA prefill GEMM (its 32-row tile up to M = 32), whose rows agree with M = 1 within
-// the prefill bound.  The GEMV's per-row vector work grows with M, the MFMA tile's does not:
-// at M = 17..31 the 32-row tile is 3.5-6x faster on the 70B shapes.
-constexpr int kGemvMaxM = 17;
+// M below gemv_max_m() runs the GEMV family (row m bit-identical to the M = 1 call for every such
+// M, as the reference asserts for M = 4, 7 and 16: tests/test_phase5_scale.py:274-310); M at or
+// above it runs the MFMA prefill GEMM (its 32-row tile up to M = 32), whose rows agree with M = 1
+// within the prefill bound.  The GEMV's per-row vector work grows with M, the MFMA tile's does
+// not: at M = 17..31 the 32-row tile is 3.5-6x faster on the 70B shapes.  The default is 17;
+// qmm_set_gemv_max_m moves it (up to 65536, the GEMV kernels' grid rows), e.g. for callers that
+// need every M bit-identical to M = 1, as the reference's TILE_M = 4 kernels give.
+constexpr int kGemvMaxMDefault = 17;
+constexpr int kGemvMaxMLimit = 65536;
+int gemv_max_m();
 
 inline int block_elems(int t) {
     switch (t) {
@@ -81,7 +85,7 @@ hipError_t launch_gemv(int ggml_type, const void* A, int a_dtype, const void* W,
 // hipErrorNotSupported when the fused path does not apply (the caller then launches each).
 hipError_t launch_gemv_fused(int ggml_type, const void* A, int a_dtype, int c_dtype, int M, int K,
                              const void* const* W, void* const* C, const int* N, int count, hipStream_t stream);
-// GEMV of up to gemv_max_fused() matrices sharing fp16 activations A [M, K] (M < kGemvMaxM), with
+// GEMV of up to gemv_max_fused() matrices sharing fp16 activations A [M, K] (M < gemv_max_m()), with
 // work folded in (`fz`); hipErrorNotSupported when the shapes or alignments need a kernel without
 // the folding (the caller then runs the separate kernels).
 hipError_t launch_gemv_ex(int ggml_type, const void* A, int c_dtype, int M, int K, const void* const* W, void* const* C,

@@ -1,4 +1,4 @@
-// Prefill GEMM (M >= kGemvMaxM): C[M, N] = A[M, K] @ dequant(W)[N, K]^T on f16 MFMA with fp32
+// Prefill GEMM (M >= gemv_max_m(), 17 by default): C[M, N] = A[M, K] @ dequant(W)[N, K]^T on f16 MFMA with fp32
 // accumulation.  Replaces the reference's TILE_M = 4 "prefill" kernels
 // (src/kernels/dequantize.hip:152-210, 279-332, 440-505, 616-685), which re-read and re-decode
 // every weight for each group of 4 activation rows on the vector ALUs.
@@ -12,7 +12,7 @@
 //     Q4_K / Q6_K super-block per weight row, so each row's bytes arrive in one batch); wave w
 //     owns weight rows [32w, 32w + 32) of the tile and all 128 activation rows (4 MFMA tiles of
 //     32 x 32, fp32 accumulators).
-//   * M <= 32 (from kGemvMaxM = 17 up): the same kernel with a 32-row activation tile, one MFMA
+//   * M <= 32 (from the default threshold of 17 up): the same kernel with a 32-row activation tile, one MFMA
 //     tile per wave; its smaller register and LDS footprint fits two workgroups per CU.
 //   * Activation tiles (128 x 256 f16, 64 KiB) are double-buffered in LDS: the next step's tile
 //     is loaded into registers during the current step and written to the free slot near its end

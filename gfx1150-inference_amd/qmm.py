@@ -97,6 +97,7 @@ _SIGNATURES = {
     "qmm_last_error": (ctypes.c_char_p, []),
     "qmm_version": (_i, []),
     "qmm_gemv_max_m": (_i, []),
+    "qmm_set_gemv_max_m": (_i, [_i]),
     "qmm_weight_bytes": (ctypes.c_size_t, [_i, _i64, _i64]),
     "qmm_gemm": (_i, [_i, _vp, _i, _vp, _vp, _i, _i, _i, _i, _vp]),
     "qmm_gemm_noalloc": (_i, [_i, _vp, _i, _vp, _vp, _i, _i, _i, _i, _vp]),
@@ -173,6 +174,12 @@ def weight_bytes(ggml_type: int, n: int, k: int) -> int:
 
 def gemv_max_m() -> int:
     return int(_lib.qmm_gemv_max_m())
+
+
+def set_gemv_max_m(m: int) -> None:
+    """Moves the GEMV / prefill threshold: M < m runs the GEMV family (rows bit-identical to the
+    M = 1 call); the default is 17."""
+    check(_lib.qmm_set_gemv_max_m(int(m)))
 
 
 def _torch():

@@ -127,8 +127,17 @@ int qmm_dequantize(int ggml_type, const void* W, void* out, int out_dtype,
 int qmm_embed(int ggml_type, const void* table, int64_t n_rows, int hidden, const int64_t* ids,
               int64_t n_ids, void* out, int out_dtype, int* bad, void* stream);
 
-/* Largest M served by the GEMV family (exclusive bound; 17), and the prefill threshold. */
+/* Largest M served by the GEMV family (exclusive bound; 17 by default), and the prefill threshold. */
 int qmm_gemv_max_m(void);
+
+/* Sets that threshold for the process (1 <= m <= 65536; QMM_ERR_INVALID_ARGUMENT otherwise).
+ * No counterpart in the reference, whose TILE_M = 4 kernels keep every row of every M
+ * bit-identical to the M = 1 call (src/kernels/dequantize.hip:152-210, 440-505, 616-685); a
+ * caller that needs that invariant beyond M = 16 raises the threshold above its largest M and
+ * gets the GEMV family's rows, at the GEMV's cost (its per-row vector work grows with M).  Calls
+ * read the threshold once (a qmm_gemm_batch call for all its descriptors); changing it while
+ * other threads issue calls changes which family their later calls take. */
+int qmm_set_gemv_max_m(int m);
 
 /* Per-type device launchers with the reference's argument meaning: fp16 A [M,K],
  * packed B [N,K], fp16 C [M,N], all device pointers, on `stream`.

@@ -33,6 +33,25 @@ def test_version_and_limits():
     assert qmm.gemv_max_m() >= 16  # the reference's M in {4, 7, 16} bit-identity cases stay in GEMV
 
 
+def test_gemv_threshold_setting():
+    """qmm_set_gemv_max_m moves the GEMV / prefill threshold within [1, 65536]; out-of-range
+    values are rejected and leave it unchanged (host logic only, no kernel runs)."""
+    before = qmm.gemv_max_m()
+    assert before == 17
+    try:
+        qmm.set_gemv_max_m(1024)
+        assert qmm.gemv_max_m() == 1024
+        for bad in (0, -3, 65537):
+            with pytest.raises(ValueError, match="qmm_set_gemv_max_m"):
+                qmm.set_gemv_max_m(bad)
+            assert qmm.gemv_max_m() == 1024
+        qmm.set_gemv_max_m(65536)
+        assert qmm.gemv_max_m() == 65536
+    finally:
+        qmm.set_gemv_max_m(before)
+    assert qmm.gemv_max_m() == before
+
+
 @pytest.mark.parametrize("t,n,k,expected", [
     (qmm.GGML_Q4_0, 4096, 4096, 9_437_184),
     (qmm.GGML_Q8_0, 4096, 4096, 17_825_792),

@@ -216,6 +216,30 @@ def test_gemv_rows_bit_identical_across_m(dev, t):
 
 
 @pytest.mark.parametrize("t", TYPES)
+def test_raised_threshold_keeps_every_m_bit_identical(dev, t):
+    """With the GEMV / prefill threshold raised (qmm_set_gemv_max_m), M = 40 and 100 run the GEMV
+    family and every row equals its M = 1 call bit for bit, as the reference's TILE_M = 4 kernels
+    give at any M; at the default threshold the same rows come from the MFMA tiles and agree with
+    them within the prefill bar."""
+    import qmm
+    rng = np.random.default_rng(811 + t)
+    N, K = 96, 4096
+    raw = O.synth_weights(t, N, K, rng)
+    x = rng.standard_normal((100, K)).astype(np.float32)
+    single = np.stack([gemm(t, x[m:m + 1], raw, N, K, dev)[0] for m in range(100)])
+    before = qmm.gemv_max_m()
+    try:
+        qmm.set_gemv_max_m(4096)
+        for M in (40, 100):
+            np.testing.assert_array_equal(gemm(t, x[:M], raw, N, K, dev), single[:M],
+                                          err_msg=f"{O.TYPE_NAMES[t]} M={M}")
+    finally:
+        qmm.set_gemv_max_m(before)
+    y = gemm(t, x[:40], raw, N, K, dev)
+    assert O.max_rel_err(y, single[:40]) <= 1e-2
+
+
+@pytest.mark.parametrize("t", TYPES)
 def test_gemv_rows_bit_identical_across_m_windowed_f16_io(dev, t):
     """fp16 activations and outputs at K = 16384 (four windows: the 8-row blocks take the windowed
     kernel, the M = 1 call the resident one): every row equals its M = 1 call bit for bit."""
