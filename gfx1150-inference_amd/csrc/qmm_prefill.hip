@@ -52,6 +52,9 @@
 #ifndef QMM_PF_SMALL_MAXM
 #define QMM_PF_SMALL_MAXM 32
 #endif
+#ifndef QMM_PF_VEC_STORE
+#define QMM_PF_VEC_STORE 1
+#endif
 #ifndef QMM_PF_SMALL_FILL
 #define QMM_PF_SMALL_FILL 1
 #endif
@@ -413,6 +416,44 @@ __device__ __forceinline__ int a_slot(int r, int c) { return 8 * r + (c ^ ((r >>
 // Sub-step S, lane half h -> activation chunk of the half stage.
 __device__ __forceinline__ int a_chunk(int s, int h) { return 4 * (s >> 1) + 2 * h + (s & 1); }
 
+// Four consecutive outputs n..n+3 of row m (n a multiple of 4) from a wave's accumulators: one
+// 16-byte (fp32) or 8-byte (fp16) store when all four exist and the address is aligned for it,
+// element stores otherwise.  With K split, the fp32 partial tile `ksplit` block kz instead.
+template <typename TC>
+__device__ __forceinline__ void store_quad(TC* __restrict__ C, float* __restrict__ part, int ksplit, int kz, int M, int N,
+                                           int ldc, int m, int n, const float (&vs)[4]) {
+    if (ksplit > 1) {
+        float* dst = part + (static_cast<size_t>(kz) * M + m) * N + n;
+        if (QMM_PF_VEC_STORE && n + 3 < N && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+            *reinterpret_cast<float4*>(dst) = make_float4(vs[0], vs[1], vs[2], vs[3]);
+            return;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (n + e < N) dst[e] = vs[e];
+        return;
+    }
+    TC* dst = C + static_cast<size_t>(m) * ldc + n;
+    if constexpr (sizeof(TC) == 4) {
+        if (QMM_PF_VEC_STORE && n + 3 < N && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+            *reinterpret_cast<float4*>(dst) = make_float4(vs[0], vs[1], vs[2], vs[3]);
+            return;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (n + e < N) reinterpret_cast<float*>(dst)[e] = vs[e];
+    } else {
+        if (QMM_PF_VEC_STORE && n + 3 < N && (reinterpret_cast<uintptr_t>(dst) & 7u) == 0) {
+            *reinterpret_cast<uint2*>(dst) = make_uint2(float_to_half_bits(vs[0]) | (float_to_half_bits(vs[1]) << 16),
+                                                        float_to_half_bits(vs[2]) | (float_to_half_bits(vs[3]) << 16));
+            return;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (n + e < N) reinterpret_cast<uint16_t*>(dst)[e] = float_to_half_bits(vs[e]);
+    }
+}
+
 // Workgroup barrier for LDS traffic only: this wave's LDS operations are complete, then
 // s_barrier.  Unlike __syncthreads() it does not wait for outstanding global loads (the
 // prefetches stay in flight); the empty asm statements keep the compiler from moving memory
@@ -612,20 +653,7 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
             const int n = n0 + 32 * wv + 8 * g + 4 * h;
             const float sm = sg.rs != nullptr ? sg.rs[m] : 1.0f;
             const float vs[4] = {acc[i][4 * g] * sm, acc[i][4 * g + 1] * sm, acc[i][4 * g + 2] * sm, acc[i][4 * g + 3] * sm};
-            if (ksplit > 1) {
-                float* dst = part + (static_cast<size_t>(kz) * M + m) * N;
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (n + e < N) dst[n + e] = vs[e];
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if (n + e < N) {
-                        if constexpr (sizeof(TC) == 4) reinterpret_cast<float*>(C)[static_cast<size_t>(m) * ldc + n + e] = vs[e];
-                        else reinterpret_cast<uint16_t*>(C)[static_cast<size_t>(m) * ldc + n + e] = float_to_half_bits(vs[e]);
-                    }
-                }
-            }
+            store_quad<TC>(C, part, ksplit, kz, M, N, ldc, m, n, vs);
         }
     }
 }
@@ -848,20 +876,7 @@ void prefill_wide_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> s
                 const int n = n0 + 64 * wv + 32 * nb + 8 * g + 4 * h;
                 const float vs[4] = {acc[nb][i][4 * g] * sm, acc[nb][i][4 * g + 1] * sm, acc[nb][i][4 * g + 2] * sm,
                                      acc[nb][i][4 * g + 3] * sm};
-                if (ksplit > 1) {
-                    float* dst = part + (static_cast<size_t>(kz) * M + m) * N;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (n + e < N) dst[n + e] = vs[e];
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        if (n + e < N) {
-                            if constexpr (sizeof(TC) == 4) reinterpret_cast<float*>(C)[static_cast<size_t>(m) * ldc + n + e] = vs[e];
-                            else reinterpret_cast<uint16_t*>(C)[static_cast<size_t>(m) * ldc + n + e] = float_to_half_bits(vs[e]);
-                        }
-                    }
-                }
+                store_quad<TC>(C, part, ksplit, kz, M, N, ldc, m, n, vs);
             }
     }
 }

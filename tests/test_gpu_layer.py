@@ -242,7 +242,7 @@ def make_layer(r, hidden, inter, heads, kvh, d, types):
 # run as paired rows writing SwiGLU's output; of different types, as separate launches.
 @pytest.mark.parametrize("prefill,neox,up_type", [(4, False, O.GGML_Q4_0), (40, False, O.GGML_Q4_0),
                                                   (64, False, O.GGML_Q4_K), (0, False, O.GGML_Q4_K),
-                                                  (40, True, O.GGML_Q4_K)])
+                                                  (40, True, O.GGML_Q4_K), (20, False, O.GGML_Q4_K)])
 def test_forward_layer_prefill_then_decode(dev, prefill, neox, up_type):
     import torch
     import qmm
