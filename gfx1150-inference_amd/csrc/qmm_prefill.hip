@@ -937,18 +937,70 @@ __global__ __launch_bounds__(256) void to_f16_rows_kernel(const float* __restric
 }
 
 // C[m, n] (rows ldc apart) = sum_z part[z][m][n] in a fixed order, for part blocks [ksplit][M][N].
+// Four consecutive elements per thread: with N % 4 == 0 (no quad crosses a row) and 16-byte
+// aligned partials, 16-byte loads, the partial blocks requested four at a time before they are
+// added (in z order), and one 8- or 16-byte store where C's row allows it; element by element
+// otherwise.
 template <typename TC>
 __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ part, TC* __restrict__ C, int M, int N,
                                                      int ldc, int ksplit) {
     const int64_t mn = static_cast<int64_t>(M) * N;
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= mn) return;
-    float s = part[i];
-    for (int z = 1; z < ksplit; ++z) s += part[static_cast<size_t>(z) * mn + i];
-    const int64_t m = i / N;
-    const size_t o = static_cast<size_t>(m) * ldc + static_cast<size_t>(i - m * N);
-    if constexpr (sizeof(TC) == 4) C[o] = s;
-    else reinterpret_cast<uint16_t*>(C)[o] = float_to_half_bits(s);
+    const int64_t i0 = 4 * (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x);
+    if (i0 >= mn) return;
+    const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(part) & 15u) == 0 && (mn & 3) == 0;
+    if (!vec) {
+        for (int64_t i = i0; i < min(i0 + 4, mn); ++i) {
+            float s = part[i];
+            for (int z = 1; z < ksplit; ++z) s += part[static_cast<size_t>(z) * mn + i];
+            const int64_t m = i / N;
+            const size_t o = static_cast<size_t>(m) * ldc + static_cast<size_t>(i - m * N);
+            if constexpr (sizeof(TC) == 4) C[o] = s;
+            else reinterpret_cast<uint16_t*>(C)[o] = float_to_half_bits(s);
+        }
+        return;
+    }
+    const float4* p4 = reinterpret_cast<const float4*>(part) + i0 / 4;
+    const int64_t zs = mn / 4;  // float4 stride between partial blocks
+    float4 s = p4[0];
+    for (int z = 1; z < ksplit; z += 4) {
+        float4 v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = p4[static_cast<size_t>(min(z + j, ksplit - 1)) * zs];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (z + j < ksplit) {
+                s.x += v[j].x;
+                s.y += v[j].y;
+                s.z += v[j].z;
+                s.w += v[j].w;
+            }
+        }
+    }
+    const int64_t m = i0 / N;
+    const int64_t n = i0 - m * N;
+    TC* dst = C + static_cast<size_t>(m) * ldc + n;
+    if constexpr (sizeof(TC) == 4) {
+        if ((reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+            *reinterpret_cast<float4*>(dst) = s;
+        } else {
+            dst[0] = s.x;
+            dst[1] = s.y;
+            dst[2] = s.z;
+            dst[3] = s.w;
+        }
+    } else {
+        const uint32_t lo = float_to_half_bits(s.x) | (static_cast<uint32_t>(float_to_half_bits(s.y)) << 16);
+        const uint32_t hi = float_to_half_bits(s.z) | (static_cast<uint32_t>(float_to_half_bits(s.w)) << 16);
+        if ((reinterpret_cast<uintptr_t>(dst) & 7u) == 0) {
+            *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+        } else {
+            uint16_t* d16 = reinterpret_cast<uint16_t*>(dst);
+            d16[0] = static_cast<uint16_t>(lo);
+            d16[1] = static_cast<uint16_t>(lo >> 16);
+            d16[2] = static_cast<uint16_t>(hi);
+            d16[3] = static_cast<uint16_t>(hi >> 16);
+        }
+    }
 }
 
 // Grow-only device workspace per (device, stream): the f16 copy of the activations and the
@@ -1103,7 +1155,7 @@ hipError_t launch_grid(const _Float16* a16, int lda, const PfSeg* segs, int nseg
     if (ksplit > 1) {
         for (int i = 0; i < nseg; ++i) {
             const int64_t mn = static_cast<int64_t>(M) * segs[i].N;
-            hipLaunchKernelGGL((reduce_kernel<TC>), dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, stream,
+            hipLaunchKernelGGL((reduce_kernel<TC>), dim3(static_cast<unsigned>((mn + 1023) / 1024)), dim3(256), 0, stream,
                                part + sg.part_off[i], sg.C[i], M, segs[i].N, segs[i].ldc, ksplit);
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
