@@ -915,8 +915,20 @@ __global__ __launch_bounds__(256) void to_f16_rows_kernel(const float* __restric
     const int m = blockIdx.x;
     const int tid = threadIdx.x;
     const float* row = A + static_cast<size_t>(m) * K;
+    // 16-byte loads where the row allows them, several in flight per thread (the maximum does not
+    // depend on the order)
+    const bool vec = (K & 7) == 0 && (reinterpret_cast<uintptr_t>(row) & 15u) == 0;
     float mx = 0.0f;
-    for (int k = tid; k < K; k += 256) mx = fmaxf(mx, fabsf(row[k]));
+    if (vec) {
+        const float4* r4 = reinterpret_cast<const float4*>(row);
+#pragma unroll 4
+        for (int k = tid; k < K / 4; k += 256) {
+            const float4 v = r4[k];
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+    } else {
+        for (int k = tid; k < K; k += 256) mx = fmaxf(mx, fabsf(row[k]));
+    }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
     if ((tid & 63) == 0) red[tid >> 6] = mx;
@@ -928,10 +940,20 @@ __global__ __launch_bounds__(256) void to_f16_rows_kernel(const float* __restric
     const int e = big || tiny ? static_cast<int>(mb >> 23) - 127 - 14 : 0;
     const float down = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
     if (tid == 0) rs[m] = __uint_as_float(static_cast<uint32_t>(127 + e) << 23);
+#pragma unroll 2
     for (int k = 8 * tid; k < lda; k += 8 * 256) {
+        float x[8];
+        if (vec && k + 8 <= K) {
+            const float4 a = *reinterpret_cast<const float4*>(row + k);
+            const float4 b = *reinterpret_cast<const float4*>(row + k + 4);
+            x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = k + j < K ? row[k + j] : 0.0f;
+        }
         _Float16 v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = static_cast<_Float16>(k + j < K ? row[k + j] * down : 0.0f);
+        for (int j = 0; j < 8; ++j) v[j] = static_cast<_Float16>(x[j] * down);
         __builtin_memcpy(out + static_cast<size_t>(m) * lda + k, v, 16);
     }
 }
