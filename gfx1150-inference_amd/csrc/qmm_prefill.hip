@@ -52,6 +52,9 @@
 #ifndef QMM_PF_SMALL_MAXM
 #define QMM_PF_SMALL_MAXM 32
 #endif
+#ifndef QMM_PF_LDS_EPILOGUE
+#define QMM_PF_LDS_EPILOGUE 1
+#endif
 #ifndef QMM_PF_VEC_STORE
 #define QMM_PF_VEC_STORE 1
 #endif
@@ -861,6 +864,59 @@ void prefill_wide_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> s
         step(std::integral_constant<int, 1>{}, t + 1);
     }
     if (t < nsteps) step(std::integral_constant<int, 0>{}, t);
+
+#if QMM_PF_LDS_EPILOGUE
+    if constexpr (sizeof(TC) == 2) {
+        if (ksplit == 1) {
+            // fp16 tile through LDS, so that every store instruction writes whole row segments:
+            // the 256 x 256 tile (128 KiB) goes into the two activation stages (rows 0..127 and
+            // 128..255, 512 bytes each, 16-byte chunks XOR-swizzled by row so that the 32 rows a
+            // write instruction touches fall in different banks), then each wave stores 64 rows,
+            // two 512-byte row segments per instruction.
+            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // trailing stage copies have landed
+            __syncthreads();
+            uint8_t* const st0 = reinterpret_cast<uint8_t*>(sA0);
+            uint8_t* const st1 = reinterpret_cast<uint8_t*>(sA1);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int m = 32 * i + l32;
+                const float sm = sg.rs != nullptr && m0 + m < M ? sg.rs[m0 + m] : 1.0f;
+                uint8_t* const row = (m < 128 ? st0 : st1) + (m & 127) * 512;
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int n = 64 * wv + 32 * nb + 8 * g + 4 * h;  // tile-local, multiple of 4
+                        const uint32_t w0 = float_to_half_bits(acc[nb][i][4 * g] * sm) |
+                                            (static_cast<uint32_t>(float_to_half_bits(acc[nb][i][4 * g + 1] * sm)) << 16);
+                        const uint32_t w1 = float_to_half_bits(acc[nb][i][4 * g + 2] * sm) |
+                                            (static_cast<uint32_t>(float_to_half_bits(acc[nb][i][4 * g + 3] * sm)) << 16);
+                        *reinterpret_cast<uint2*>(row + (((n >> 3) ^ (m & 31)) << 4) + ((n >> 2) & 1) * 8) = make_uint2(w0, w1);
+                    }
+            }
+            __syncthreads();
+            const int c = lane & 31;  // 16-byte chunk of the row: columns 8c .. 8c + 7
+#pragma unroll 4
+            for (int k = 0; k < 32; ++k) {
+                const int m = 64 * wv + 2 * k + (lane >> 5);
+                const uint8_t* row = (m < 128 ? st0 : st1) + (m & 127) * 512;
+                const uint4 v = *reinterpret_cast<const uint4*>(row + ((c ^ (m & 31)) << 4));
+                const int gm = m0 + m, gn = n0 + 8 * c;
+                if (gm >= M || gn >= N) continue;
+                uint16_t* dst = reinterpret_cast<uint16_t*>(C) + static_cast<size_t>(gm) * ldc + gn;
+                if (gn + 7 < N && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+                    *reinterpret_cast<uint4*>(dst) = v;
+                } else {
+                    const uint32_t wv4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (gn + e < N) dst[e] = static_cast<uint16_t>(wv4[e >> 1] >> (16 * (e & 1)));
+                }
+            }
+            return;
+        }
+    }
+#endif
 
     // D element v of tile (nb, i): weight row n = n0 + 64wv + 32nb + 8(v/4) + 4h + v%4,
     // activation row m = m0 + 32i + l32.
