@@ -645,6 +645,80 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
         cur = nxt;
     }
 
+#if QMM_PF_LDS_EPILOGUE
+    // Output tile through LDS (both activation stages: 256 x kH x BM bytes), so that every store
+    // instruction writes whole row segments: fp16 rows of 512 bytes (fp16 C), or fp32 rows of
+    // 1 KiB (fp32 C; with 256-k steps only, where they fit).  Without a K split only: the split's
+    // fp32 partial tiles measured no faster this way.  16-byte chunks are XOR-swizzled by row so
+    // that the 32 rows one write instruction touches fall in different banks.
+    constexpr bool kLdsF16 = sizeof(TC) == 2;
+    constexpr bool kLdsF32 = sizeof(TC) == 4 && kH == 4;
+    if ((kLdsF16 || kLdsF32) && ksplit == 1) {
+        constexpr bool f16 = kLdsF16;
+        __syncthreads();  // every wave is done with the activation stages
+        uint8_t* const st = reinterpret_cast<uint8_t*>(&sA[0][0]);
+        constexpr int rowb = f16 ? 512 : 1024;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int m = 32 * i + l32;
+            const float sm = sg.rs != nullptr && m0 + m < M ? sg.rs[m0 + m] : 1.0f;
+            uint8_t* const row = st + m * rowb;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int n = 32 * wv + 8 * g + 4 * h;  // tile-local, multiple of 4
+                const float v0 = acc[i][4 * g] * sm, v1 = acc[i][4 * g + 1] * sm;
+                const float v2 = acc[i][4 * g + 2] * sm, v3 = acc[i][4 * g + 3] * sm;
+                if constexpr (f16) {
+                    const uint32_t w0 = float_to_half_bits(v0) | (static_cast<uint32_t>(float_to_half_bits(v1)) << 16);
+                    const uint32_t w1 = float_to_half_bits(v2) | (static_cast<uint32_t>(float_to_half_bits(v3)) << 16);
+                    *reinterpret_cast<uint2*>(row + (((n >> 3) ^ (m & 31)) << 4) + ((n >> 2) & 1) * 8) = make_uint2(w0, w1);
+                } else {
+                    *reinterpret_cast<float4*>(row + (((n >> 2) ^ (m & 31)) << 4)) = make_float4(v0, v1, v2, v3);
+                }
+            }
+        }
+        __syncthreads();
+        if constexpr (f16) {
+            const int c = lane & 31;  // 16-byte chunk: columns 8c .. 8c + 7
+#pragma unroll
+            for (int k = 0; k < BM / 16; ++k) {  // two rows per instruction, BM / 8 rows per wave
+                const int m = (BM / 8) * wv + 2 * k + (lane >> 5);
+                const uint4 v = *reinterpret_cast<const uint4*>(st + m * 512 + ((c ^ (m & 31)) << 4));
+                const int gm = m0 + m, gn = n0 + 8 * c;
+                if (gm >= M || gn >= N) continue;
+                uint16_t* dst = reinterpret_cast<uint16_t*>(C) + static_cast<size_t>(gm) * ldc + gn;
+                if (gn + 7 < N && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+                    *reinterpret_cast<uint4*>(dst) = v;
+                } else {
+                    const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (gn + e < N) dst[e] = static_cast<uint16_t>(vw[e >> 1] >> (16 * (e & 1)));
+                }
+            }
+        } else {
+            const int c = lane;  // 16-byte chunk: columns 4c .. 4c + 3
+#pragma unroll
+            for (int k = 0; k < BM / 8; ++k) {  // one row per instruction
+                const int m = (BM / 8) * wv + k;
+                const float4 v = *reinterpret_cast<const float4*>(st + m * 1024 + ((c ^ (m & 31)) << 4));
+                const int gm = m0 + m, gn = n0 + 4 * c;
+                if (gm >= M || gn >= N) continue;
+                float* dst = reinterpret_cast<float*>(C) + static_cast<size_t>(gm) * ldc + gn;
+                if (gn + 3 < N && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+                    *reinterpret_cast<float4*>(dst) = v;
+                } else {
+                    const float vf[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (gn + e < N) dst[e] = vf[e];
+                }
+            }
+        }
+        return;
+    }
+#endif
+
     // D element v of tile i: weight row n = n0 + 32wv + 8(v/4) + 4h + v%4, activation row
     // m = m0 + 32i + l32.
 #pragma unroll
