@@ -41,7 +41,7 @@
 #define QMM_PF_WIDE 1
 #endif
 #ifndef QMM_PF_WIDE_VALU
-#define QMM_PF_WIDE_VALU 3
+#define QMM_PF_WIDE_VALU 4  // VALU operations per MFMA round of the 256 x 256 tile's schedule
 #endif
 // The wide tile is used while its tiles cover at least 1 / QMM_PF_WIDE_MIN of the CUs (K is
 // split over workgroups below that).
