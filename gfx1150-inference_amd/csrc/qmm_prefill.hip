@@ -141,7 +141,8 @@ struct PQ4K {
     // step at k0 (multiple of 64H): super-block k0/256, qs chunks c = c0 + U with c0 = (k0/64)%4
     // (always 0 when H = 4); lane half h takes qs bytes 16h..16h+15 of chunk c (low nibbles:
     // sub-block 2c, high: 2c+1).
-    __device__ static Raw load(const uint8_t* row, int k0, int h, int) {
+    __device__ static void prep(Raw&, int) {}
+    __device__ static Raw load(const uint8_t* row, int k0, int h, int, int) {
         const uint8_t* sb = row + static_cast<size_t>(k0 >> 8) * kBytes;
         const int c0 = H == 4 ? 0 : ((k0 >> 6) & 2);
         Raw r;
@@ -199,38 +200,92 @@ struct PQ6K {
     static constexpr int kH = H;
     static_assert(H == 2 || H == 4, "steps of 128 or 256 k");
     static constexpr int kQK = kQK_K, kBytes = kBytesQ6_K;
-    struct Raw { u32x4p la[H / 2], lb[H / 2], qh[H / 2]; uint32_t sc[H], d; };
+    struct Raw {
+        u32x4p la[H / 2], lb[H / 2], qh[H / 2], s;  // ql / qh slices, sub-scales (H = 2: s.x, s.y)
+        uint32_t tail, d;                          // the dword after s (f = 2), d
+        int f;                                     // byte shift: 0 or 2, uniform over the wave
+    };
     struct Sc { h2 a0, a1; };
     // step at k0 (multiple of 64H): super-block k0/256.  Half U covers the block's 64-weight
     // quarter 2*n2 + (U&1) of 128-weight half n2 = U>>1 (H = 4) or (k0/128)%2 (H = 2), groups
     // t = 2(U&1) + (S>>1).  Lane half h takes l = 16h..16h+15 of ql (groups t even: ql[64n2 + l],
     // odd: ql[64n2 + 32 + l]; U&1 picks the nibble) and of qh[32n2 + l]; sub-scale word U holds
     // sc[8n2 + 4(U&1) + (0..3)].
-    __device__ static Raw load(const uint8_t* row, int k0, int h, int) {
+    //
+    // Alignment (256-k steps): a 210-byte block starts 2 bytes off a 4-byte boundary when its
+    // index is odd (with 4-aligned rows), and 16-byte loads at such addresses measured 16 %
+    // slower over a whole launch (8B down at M = 512).  For those blocks every slice is loaded
+    // from 2 bytes lower (f = 2, 4-aligned) and prep() shifts it back: dword k of a slice is
+    // bytes 2..3 of loaded dword k and bytes 0..1 of dword k + 1, the last one taken from the
+    // slice that follows in memory (the other lane half's register, fetched with
+    // v_permlane32_swap, or `tail`).  With al == 0 (rows not 4-aligned) blocks are read as they lie.
+    __device__ static Raw load(const uint8_t* row, int k0, int h, int, int al) {
         const uint8_t* sb = row + static_cast<size_t>(k0 >> 8) * kBytes;
-        const int nb = H == 4 ? 0 : ((k0 >> 7) & 1);
         Raw r;
-#pragma unroll
-        for (int j = 0; j < H / 2; ++j) {
-            const int n2 = nb + j;
-            r.la[j] = ld16(sb + 64 * n2 + 16 * h);
-            r.lb[j] = ld16(sb + 64 * n2 + 32 + 16 * h);
-            r.qh[j] = ld16(sb + 128 + 32 * n2 + 16 * h);
-        }
-        if constexpr (H == 4) {
-            const u32x4p s = ld16(sb + 192);
-            r.sc[0] = s.x, r.sc[1] = s.y, r.sc[2] = s.z, r.sc[3] = s.w;
+        if constexpr (H == 2) {
+            // 128-k steps (256 x 256 tile): blocks are read as they lie; the realignment's extra
+            // loads and shifts measured 7 % slower in this one-wave-per-SIMD tile.
+            const int nb = (k0 >> 7) & 1;
+            r.la[0] = ld16(sb + 64 * nb + 16 * h);
+            r.lb[0] = ld16(sb + 64 * nb + 32 + 16 * h);
+            r.qh[0] = ld16(sb + 128 + 32 * nb + 16 * h);
+            r.s.x = ld4(sb + 192 + 8 * nb);
+            r.s.y = ld4(sb + 196 + 8 * nb);
+            r.s.z = r.s.w = r.tail = 0u;
+            r.f = 0;
         } else {
-            r.sc[0] = ld4(sb + 192 + 8 * nb);
-            r.sc[1] = ld4(sb + 196 + 8 * nb);
+            const int f = al && ((k0 >> 8) & 1) ? 2 : 0;
+            const uint8_t* sf = sb - f;  // in bounds: f = 2 only for blocks with an odd index
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                r.la[j] = ld16(sf + 64 * j + 16 * h);
+                r.lb[j] = ld16(sf + 64 * j + 32 + 16 * h);
+                r.qh[j] = ld16(sf + 128 + 32 * j + 16 * h);
+            }
+            r.s = ld16(sf + 192);
+            r.tail = ld4(sb + 204 + f);  // f = 2: bytes 206..209 (after s); f = 0: unused
+            r.f = f;
         }
         r.d = ld2(sb + 208);
         return r;
     }
+    // Realigns a 256-k step's slices (f = 2) once its loads have landed; f is uniform over the
+    // wave, so this is a branch, not a select.
+    __device__ static void prep(Raw& r, int h) {
+        if constexpr (H == 4) {
+            if (r.f != 0) {
+                // nx(R): the dword after slice R in memory.  Lane half 0's slice R is followed by
+                // half 1's R; half 1's by half 0's next slice (la0 lb0 la1 lb1 qh0 qh1 s, s
+                // loaded by both halves).  swap(a, b) gives lanes 0..31 lane l + 32's a and lanes
+                // 32..63 lane l - 32's b.
+                auto nextof = [&](uint32_t a, uint32_t b) {
+                    const auto sw = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+                    return h ? static_cast<uint32_t>(sw[0]) : static_cast<uint32_t>(sw[1]);
+                };
+                auto fix = [](u32x4p& v, uint32_t nx) {
+                    const u32x4p o = v;
+                    v.x = __builtin_amdgcn_alignbyte(o.y, o.x, 2);
+                    v.y = __builtin_amdgcn_alignbyte(o.z, o.y, 2);
+                    v.z = __builtin_amdgcn_alignbyte(o.w, o.z, 2);
+                    v.w = __builtin_amdgcn_alignbyte(nx, o.w, 2);
+                };
+                const uint32_t n0 = nextof(r.la[0].x, r.lb[0].x), n1 = nextof(r.lb[0].x, r.la[1].x);
+                const uint32_t n2 = nextof(r.la[1].x, r.lb[1].x), n3 = nextof(r.lb[1].x, r.qh[0].x);
+                const uint32_t n4 = nextof(r.qh[0].x, r.qh[1].x), n5 = nextof(r.qh[1].x, r.s.x);
+                fix(r.la[0], n0);
+                fix(r.lb[0], n1);
+                fix(r.la[1], n2);
+                fix(r.lb[1], n3);
+                fix(r.qh[0], n4);
+                fix(r.qh[1], n5);
+                fix(r.s, r.tail);
+            }
+        }
+    }
     template <int U>
     __device__ static Sc scales(const Raw& r, int, int h, int) {
         // sub-scales of word U, bytes h and h + 2
-        const uint32_t sc = r.sc[U];
+        const uint32_t sc = U == 0 ? r.s.x : U == 1 ? r.s.y : U == 2 ? r.s.z : r.s.w;
         const float d = half_bits_to_float(r.d);
         Sc s;
         s.a0 = splat(d * static_cast<float>(static_cast<int8_t>(sc >> (8 * h))));
@@ -268,7 +323,8 @@ struct PQ80 {
     static constexpr int kQK = kQK8_0, kBytes = kBytesQ8_0;
     struct Raw { u32x4p q[2 * H]; uint32_t d[2 * H]; };
     struct Sc { h2 a0, a1; };
-    __device__ static Raw load(const uint8_t* row, int k0, int h, int kv) {
+    __device__ static void prep(Raw&, int) {}
+    __device__ static Raw load(const uint8_t* row, int k0, int h, int kv, int) {
         const uint8_t* b0 = row + static_cast<size_t>(k0 >> 5) * kBytes;
         Raw r;
 #pragma unroll
@@ -310,7 +366,8 @@ struct PQ40 {
     struct Raw { u32x4p q[2 * H]; uint32_t d[2 * H]; };
     struct Sc { h2 a0, a1; };
     // lane half h takes the block's low (h = 0, k 0..15) or high (h = 1, k 16..31) nibbles.
-    __device__ static Raw load(const uint8_t* row, int k0, int, int kv) {
+    __device__ static void prep(Raw&, int) {}
+    __device__ static Raw load(const uint8_t* row, int k0, int, int kv, int) {
         const uint8_t* b0 = row + static_cast<size_t>(k0 >> 5) * kBytes;
         Raw r;
 #pragma unroll
@@ -356,7 +413,8 @@ struct PF16 {
     struct Raw { u32x4p w[H][4]; };
     struct Sc { uint32_t keep[4]; };
     __device__ static constexpr int off(int U, int S, int h) { return 64 * U + 32 * (S >> 1) + 16 * h + 8 * (S & 1); }
-    __device__ static Raw load(const uint8_t* row, int k0, int h, int kv) {
+    __device__ static void prep(Raw&, int) {}
+    __device__ static Raw load(const uint8_t* row, int k0, int h, int kv, int) {
         Raw r;
 #pragma unroll
         for (int U = 0; U < H; ++U)
@@ -530,6 +588,7 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
     const int l32 = lane & 31;
 
     const size_t row_bytes = static_cast<size_t>(K / P::kQK) * P::kBytes;
+    const int wal = ((reinterpret_cast<uintptr_t>(W) | row_bytes) & 3) == 0;  // 4-aligned rows
     const uint8_t* wrow = W + static_cast<size_t>(min(n0 + 32 * wv + l32, N - 1)) * row_bytes;
 
     // Thread tid copies half-stage chunks p = tid + 512 j (j < NJ) of every half: row p >> 3,
@@ -561,7 +620,7 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
     };
     auto load_raw = [&](int t, typename P::Raw& raw) {
         const int k0 = kb + min(t, nsteps - 1) * kBK;
-        raw = P::load(wrow, k0, h, kend - k0);
+        raw = P::load(wrow, k0, h, kend - k0, wal);
     };
     // activation fragments of sub-step (U, S) of the step held in `slot`
     auto read_a = [&](int slot, int U, int S, f16x8 (&af)[NI]) {
@@ -604,6 +663,7 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
     load_a(0, an);
     store_a(0, an);
     lds_barrier();
+    P::prep(cur, h);
     sc[0] = P::template scales<0>(cur, kb, h, kend - kb);
     P::template frag<0, 0>(cur, sc[0], h, wf[0]);
     read_a(0, 0, 0, af[0]);
@@ -631,7 +691,10 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
             if constexpr (qn == kQ) read_a(slot ^ 1, 0, 0, af[B ^ 1]);
             if constexpr ((q & 3) == 1 && U + 1 < kH)
                 sc[(U + 1) & 1] = P::template scales<(U + 1) % kH>(cur, k0, h, kend - k0);
-            if constexpr (q == kQ - 3) sc[0] = P::template scales<0>(nxt, k0 + kBK, h, kend - k0 - kBK);
+            if constexpr (q == kQ - 3) {
+                P::prep(nxt, h);
+                sc[0] = P::template scales<0>(nxt, k0 + kBK, h, kend - k0 - kBK);
+            }
             if constexpr (qn < kQ) P::template frag<Un % kH, Sn>(cur, sc[Un & 1], h, wf[B ^ 1]);
             else P::template frag<0, 0>(nxt, sc[0], h, wf[B ^ 1]);
             f16x8 bw;
@@ -812,6 +875,7 @@ void prefill_wide_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> s
     const int l32 = lane & 31;
 
     const size_t row_bytes = static_cast<size_t>(K / P::kQK) * P::kBytes;
+    const int wal = ((reinterpret_cast<uintptr_t>(W) | row_bytes) & 3) == 0;  // 4-aligned rows
     const uint8_t* wrow[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb)
@@ -841,7 +905,7 @@ void prefill_wide_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> s
     auto load_raw = [&](int t, Raw (&raw)[2]) {
         const int k0 = kb + min(t, nsteps - 1) * kWBK;
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) raw[nb] = P::load(wrow[nb], k0, h, kend - k0);
+        for (int nb = 0; nb < 2; ++nb) raw[nb] = P::load(wrow[nb], k0, h, kend - k0, wal);
     };
     auto read_a = [&](const u32x4p* stage, int U, int S, f16x8 (&af)[8]) {
         const u32x4p* sa = stage + kWChunksPerHalf * U;
@@ -884,6 +948,7 @@ void prefill_wide_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> s
     lds_barrier();
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
+        P::prep(cur[nb], h);
         sc[nb][0] = P::template scales<0>(cur[nb], kb, h, kend - kb);
         P::template frag<0, 0>(cur[nb], sc[nb][0], h, wf[0][nb]);
     }
@@ -913,7 +978,10 @@ void prefill_wide_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> s
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) {
                 if constexpr (q == 1) sc[nb][1] = P::template scales<1>(cur[nb], k0, h, kend - k0);
-                if constexpr (q == kQ - 3) sc[nb][0] = P::template scales<0>(nxt[nb], k0 + kWBK, h, kend - k0 - kWBK);
+                if constexpr (q == kQ - 3) {
+                    P::prep(nxt[nb], h);
+                    sc[nb][0] = P::template scales<0>(nxt[nb], k0 + kWBK, h, kend - k0 - kWBK);
+                }
                 if constexpr (qn < kQ) P::template frag<Un, Sn>(cur[nb], sc[nb][Un], h, wf[B ^ 1][nb]);
                 else P::template frag<0, 0>(nxt[nb], sc[nb][0], h, wf[B ^ 1][nb]);
             }

@@ -274,3 +274,37 @@ def test_prefill_workspace_release_and_regrow(dev):
     torch.cuda.synchronize()
     assert torch.equal(y1, y2)
     assert O.max_rel_err(y2.cpu().numpy().astype(np.float64), O.matmul_f64(t, A.cpu().numpy(), raw, N, K)) <= TOL_F64
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_prefill_unaligned_weights_bit_identical(dev, t):
+    """Weights 2 bytes past a 4-byte boundary, and rows whose byte length is 2 mod 4
+    (Q6_K with an odd number of super-blocks per row): the prefill loads such rows' blocks as
+    they lie, 4-aligned rows through the aligned-load-and-shift path (Q6_K blocks at odd indices
+    start 2 bytes off a 4-byte boundary).  Every case matches the call on a 256-aligned copy of
+    the same bytes bit for bit, on the 32-row, 128-row and 256-row (wide) tiles; Q4_K weights that
+    are not 16-byte aligned run the GEMV family instead (checked against fp64)."""
+    import torch
+    import qmm
+    rng = np.random.default_rng(4400 + t)
+    kq = t in (O.GGML_Q4_K, O.GGML_Q6_K)
+    cases = [(24, 300, 2048 if kq else 544), (96, 512, 1280 if kq else 1024), (256, 32768, 512)]
+    for M, N, K in cases:
+        raw = O.synth_weights(t, N, K, rng)
+        A = to_dev(rng.standard_normal((M, K)).astype(np.float16), dev)
+        W = to_dev(raw, dev)
+        ref = qmm.gemm(t, A, W, N, K, out_dtype=torch.float32)
+        buf = torch.zeros(raw.size + 16, dtype=torch.uint8, device=dev)
+        buf[2:2 + raw.size] = W
+        y = qmm.gemm(t, A, buf[2:2 + raw.size], N, K, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        if t == O.GGML_Q4_K:
+            # the prefill reads Q4_K headers with 16-byte loads: such weights take the GEMV family
+            sub = raw[:min(N, 64) * O.weight_bytes(t, 1, K)]
+            yo = O.matmul_f64(t, A.cpu().numpy().astype(np.float32), sub, min(N, 64), K)
+            assert O.max_rel_err(y[:, :min(N, 64)].cpu().numpy().astype(np.float64), yo) <= TOL_F64
+        else:
+            assert torch.equal(y, ref), (O.TYPE_NAMES[t], M, N, K)
+        yo = O.matmul_f16_operands(t, A.cpu().numpy().astype(np.float32), raw, N, K) if N <= 512 else None
+        if yo is not None:
+            assert O.max_rel_err(ref.cpu().numpy().astype(np.float64), yo) <= TOL_F16, (O.TYPE_NAMES[t], M, N, K)
