@@ -77,6 +77,32 @@ def test_batch_shared_input_matches_single_launches(dev, t, M):
         assert O.max_rel_err(c.cpu().numpy().astype(np.float64), O.matmul_f64(t, xx, raw, n, K)) <= GEMV_TOL
 
 
+@pytest.mark.parametrize("K", [4096, 8192])
+def test_batch_gate_up_large_rows_match_single_launches(dev, K):
+    """Fused Q4_K gate + up at M = 1 with 16384 rows or more: two rows per wave item (and, with
+    one 4096-k window, 4-wave workgroups), odd row counts in both matrices.  Each output matches
+    its matrix's single launch (one row per item) bit for bit, and fp64 on sampled rows."""
+    import torch
+    import qmm
+    t = O.GGML_Q4_K
+    rng = np.random.default_rng(950 + K)
+    x = rng.standard_normal((1, K)).astype(np.float16)
+    A = to_dev(x, dev)
+    ns = [14337, 8191]
+    raws = [O.synth_weights(t, n, K, rng) for n in ns]
+    Ws = [to_dev(r, dev) for r in raws]
+    Cs = [torch.full((1, n), float("nan"), device=dev, dtype=torch.float16) for n in ns]
+    qmm.gemm_batch(descs_of([(t, A, w, c, n, K) for n, w, c in zip(ns, Ws, Cs)]))
+    torch.cuda.synchronize()
+    rb = O.weight_bytes(t, 1, K)
+    for n, w, c, raw in zip(ns, Ws, Cs, raws):
+        assert torch.equal(c.cpu(), single(t, A, w, n, K, torch.float16)), n
+        rows = np.concatenate([np.sort(rng.choice(n, size=30, replace=False)), [n - 1]])
+        sub = np.concatenate([raw[r * rb:(r + 1) * rb] for r in rows])
+        yo = O.matmul_f64(t, x.astype(np.float32), sub, rows.size, K)
+        assert O.max_rel_err(c.cpu().numpy().astype(np.float64)[:, rows], yo) <= GEMV_TOL, n
+
+
 @pytest.mark.parametrize("t", [O.GGML_Q4_K, O.GGML_Q6_K])
 def test_batch_more_descriptors_than_one_launch_takes(dev, t):
     # Seven descriptors on one input: served by more than one fused launch.

@@ -381,6 +381,7 @@ FULL_SHAPES = [
     ("8b_q4_k_q", O.GGML_Q4_K, 4096, 4096),
     ("8b_q6_k_down", O.GGML_Q6_K, 4096, 14336),
     ("8b_q6_k_lm_head", O.GGML_Q6_K, 128256, 4096),
+    ("8b_q4_k_gate_up_rows", O.GGML_Q4_K, 28672, 4096),
     ("70b_q4_k_gate", O.GGML_Q4_K, 28672, 8192),
     ("70b_q4_k_kv", O.GGML_Q4_K, 1024, 8192),
     ("70b_q6_k_down", O.GGML_Q6_K, 8192, 28672),
