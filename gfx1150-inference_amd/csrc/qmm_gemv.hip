@@ -1513,6 +1513,17 @@ hipError_t dispatch_rows(const void* A, const Seg* segs, int nseg, int M, int N,
         if (N >= 2048) return launch_fast<F, 2, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
         return launch_fast<F, 2, 1, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
     }
+    if (M <= 4 && !fz.pair) {
+        // M = 3, 4 where four staged rows exceed the LDS but two fit (70B down, K = 28672): two
+        // 2-row blocks of resident activations instead of the windowed kernel's one barrier per
+        // window (70B down at M = 4: 76 -> 69 us); rows keep the M = 1 arithmetic.
+        DevInfo di;
+        const hipError_t e = device_info(di);
+        if (e != hipSuccess) return e;
+        const size_t per_row = static_cast<size_t>((K + kGemvWindow - 1) / kGemvWindow) * kSlotBytes;
+        if (4 * per_row > di.max_lds && 2 * per_row <= di.max_lds)
+            return launch_fast<F, 2, 2, 16, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
+    }
     if (N >= 4096) return launch_fast<F, 4, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
     return launch_fast<F, 4, 1, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
 }

@@ -262,6 +262,29 @@ def test_gemv_rows_bit_identical_across_m_windowed_f16_io(dev, t):
 
 
 @pytest.mark.parametrize("t", TYPES)
+def test_gemv_rows_bit_identical_across_m_long_k(dev, t):
+    """K = 28672 (seven windows, the 70B down): M = 3, 4 run two 2-row blocks of resident
+    activations (four staged rows do not fit the LDS), M = 2 one, M = 5, 8 the windowed 8-row
+    kernel; fp32 and fp16 activations.  Every row equals its M = 1 call bit for bit."""
+    import torch
+    import qmm
+    rng = np.random.default_rng(741 + t)
+    N, K = 48, 28672
+    raw = O.synth_weights(t, N, K, rng)
+    W = torch.from_numpy(raw).to(dev)
+    for dt in (np.float32, np.float16):
+        x = rng.standard_normal((8, K)).astype(dt)
+
+        def run(a):
+            C = qmm.gemm(t, torch.from_numpy(np.ascontiguousarray(a)).to(dev), W, N, K, out_dtype=torch.float32)
+            torch.cuda.synchronize()
+            return C.cpu().numpy()
+        single = np.concatenate([run(x[m:m + 1]) for m in range(8)])
+        for M in (2, 3, 4, 5, 8):
+            np.testing.assert_array_equal(run(x[:M]), single[:M], err_msg=f"{O.TYPE_NAMES[t]} M={M} {dt.__name__}")
+
+
+@pytest.mark.parametrize("t", TYPES)
 def test_golden_gemv(dev, t):
     kat = np.load(GOLDEN, allow_pickle=False)
     name = O.TYPE_NAMES[t]
