@@ -109,6 +109,29 @@ def test_dequant_ragged_sizes_leave_tail_untouched(dev, t, blocks):
 
 
 @pytest.mark.parametrize("t", TYPES)
+def test_dequant_weights_2_bytes_off_bit_exact(dev, t):
+    """Packed weights starting 2 bytes past a 4-byte boundary (and at one), odd and even block
+    counts: the Q6_K dequantizer reads blocks that sit 2 bytes off a 4-byte boundary with aligned
+    loads and shifts them back, never below the first block.  Values bit-exact."""
+    import torch
+    import qmm
+    rng = np.random.default_rng(77 + t)
+    qk, bb = O.BLOCK_INFO[t]
+    for blocks in (1, 2, 13, 258):
+        n = blocks * qk
+        raw = O.synth_weights(t, 1, n, rng)
+        want = O.DEQUANT_F32[t](raw, n).astype(np.float16).view(np.uint16)
+        for off in (0, 2):
+            buf = torch.zeros(raw.size + 16, dtype=torch.uint8, device=dev)
+            buf[off:off + raw.size] = to_dev(raw, dev)
+            out = torch.empty((n,), dtype=torch.float16, device=dev)
+            qmm.dequantize(t, buf[off:off + raw.size], n, out=out)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(out.cpu().numpy().view(np.uint16), want,
+                                          err_msg=f"{O.TYPE_NAMES[t]} blocks={blocks} off={off}")
+
+
+@pytest.mark.parametrize("t", TYPES)
 def test_dequant_random_bytes_nan_aware(dev, t):
     import torch
     import qmm
