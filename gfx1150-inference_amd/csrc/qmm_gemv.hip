@@ -1501,10 +1501,12 @@ hipError_t dispatch_rows(const void* A, const Seg* segs, int nseg, int M, int N,
             if (nseg == 1 && N >= 2048 && N < 8192)
                 return launch_fast<F, 1, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
         }
-        // Q4_K over 16384 rows and more (fused gate + up): two rows per item, so that every wave
-        // holds the same number of items (70B gate + up 2 x 28672 x 8192: 49.1 -> 47.5 us).
+        // Q4_K over 16384 rows and more (gate + up in one launch), without a fused prologue or
+        // epilogue: two rows per item, so that every wave holds the same number of items (70B
+        // gate + up 2 x 28672 x 8192: 49.1 -> 47.5 us).
         if constexpr (F::kType == QMM_TYPE_Q4_K) {
-            if (N >= 16384) return launch_fast<F, 1, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
+            if (N >= 16384 && fz.kind == 0 && fz.ea == nullptr)
+                return launch_fast<F, 1, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
         }
         return launch_fast<F, 1, 1, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
     }
@@ -1549,7 +1551,7 @@ hipError_t dispatch_fast(const void* A, const Seg* segs, int nseg, int M, int K,
     // Q4_K at M = 1 over one window and 16384 rows or more (8B gate + up): 4-wave workgroups
     // (8B gate + up 2 x 14336 x 4096: 14.9 -> 13.8 us).
     if constexpr (F::kType == QMM_TYPE_Q4_K) {
-        if (M == 1 && !fz.pair && nwin == 1 && N >= 16384)
+        if (M == 1 && !fz.pair && fz.kind == 0 && fz.ea == nullptr && nwin == 1 && N >= 16384)
             return launch_fast<F, 1, 2, 4, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
     }
     if (M <= QMM_GEMV_NW16_MAXM && res_lds > 40 * 1024)
