@@ -1116,8 +1116,27 @@ __global__ __launch_bounds__(256) void to_f16_rows_kernel(const float* __restric
     // 16-byte loads where the row allows them, several in flight per thread (the maximum does not
     // depend on the order)
     const bool vec = (K & 7) == 0 && (reinterpret_cast<uintptr_t>(row) & 15u) == 0;
+    // Rows of up to 16384 values (padded) are read once: each thread keeps its eight-value units
+    // in registers between the maximum and the conversion, all its loads in flight at once.
+    constexpr int kU = 8;
+    const bool cached = vec && lda <= 8 * 256 * kU;
+    float4 va[kU], vb[kU];
     float mx = 0.0f;
-    if (vec) {
+    if (cached) {
+        const float4* r4 = reinterpret_cast<const float4*>(row);
+#pragma unroll
+        for (int i = 0; i < kU; ++i) {
+            const int k = 8 * (tid + 256 * i);
+            const bool in = k < K;  // K % 8 == 0: a unit is inside the row or past it
+            va[i] = in ? r4[k / 4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            vb[i] = in ? r4[k / 4 + 1] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int i = 0; i < kU; ++i) {
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(va[i].x), fabsf(va[i].y)), fmaxf(fabsf(va[i].z), fabsf(va[i].w))));
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(vb[i].x), fabsf(vb[i].y)), fmaxf(fabsf(vb[i].z), fabsf(vb[i].w))));
+        }
+    } else if (vec) {
         const float4* r4 = reinterpret_cast<const float4*>(row);
 #pragma unroll 4
         for (int k = tid; k < K / 4; k += 256) {
@@ -1138,6 +1157,19 @@ __global__ __launch_bounds__(256) void to_f16_rows_kernel(const float* __restric
     const int e = big || tiny ? static_cast<int>(mb >> 23) - 127 - 14 : 0;
     const float down = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
     if (tid == 0) rs[m] = __uint_as_float(static_cast<uint32_t>(127 + e) << 23);
+    if (cached) {
+#pragma unroll
+        for (int i = 0; i < kU; ++i) {
+            const int k = 8 * (tid + 256 * i);
+            if (k >= lda) break;
+            const float x[8] = {va[i].x, va[i].y, va[i].z, va[i].w, vb[i].x, vb[i].y, vb[i].z, vb[i].w};
+            _Float16 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = static_cast<_Float16>(x[j] * down);
+            __builtin_memcpy(out + static_cast<size_t>(m) * lda + k, v, 16);
+        }
+        return;
+    }
 #pragma unroll 2
     for (int k = 8 * tid; k < lda; k += 8 * 256) {
         float x[8];
