@@ -137,6 +137,25 @@ def test_prefill_dtypes(dev, t, a16, c16):
     assert O.max_rel_err(y, O.matmul_f16_operands(t, xa, raw, N, K)) <= tol_b
 
 
+@pytest.mark.parametrize("K", [16384, 16640])
+def test_prefill_fp32_activations_long_rows(dev, K):
+    """fp32 activations are converted to f16 row by row before the MFMA tiles: rows of up to
+    16384 values (after padding to the step) are read once and held in registers, longer ones
+    take the two-pass conversion.  Both sides of that bound, against fp64 and the f16-operand
+    product, with one row scaled past f16's range (its rescaling path)."""
+    t = O.GGML_Q4_K
+    rng = np.random.default_rng(4500 + K)
+    M, N = 40, 64
+    raw = O.synth_weights(t, N, K, rng)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x[3] *= 1e6
+    y = run(t, x, raw, N, K, dev)
+    assert np.all(np.isfinite(y))
+    assert O.max_rel_err(y, O.matmul_f64(t, x, raw, N, K)) <= TOL_F64
+    keep = np.arange(M) != 3  # the rescaled row: fp64 bar only (its operands differ from a plain f16 cast)
+    assert O.max_rel_err(y[keep], O.matmul_f16_operands(t, x[keep], raw, N, K)) <= TOL_F16
+
+
 @pytest.mark.parametrize("t", TYPES)
 def test_prefill_reference_quantizer_inputs(dev, t):
     # Inputs built like the reference's own tests (quantize_*_cpu of N(0,1)-scaled weights),
