@@ -92,6 +92,28 @@ def test_f16_gemv_rows_bit_identical_across_m(dev):
         assert np.array_equal(gemm_f16(A[:M], W, dev), full[:M])
 
 
+def test_f16_gemv_rows_bit_identical_across_m_long_k(dev):
+    """K = 28672 fp16 weights: four staged activation rows (224 KiB) exceed the LDS, so M = 3, 4
+    run two 2-row blocks, M = 2 one, M = 5, 8 the windowed kernel; fp32 and fp16 activations.
+    Every row equals its M = 1 call bit for bit and an fp64 product within the GEMV bar."""
+    N, K = 96, 28672
+    A, W = dense_case(29, 8, N, K)
+    import torch
+    import qmm
+    Wd = t(W, dev)
+    for dt in (np.float32, np.float16):
+        x = A.astype(dt)
+
+        def run(a):
+            C = qmm.gemm(F16, t(a, dev), Wd, N, K, out_dtype=torch.float32)
+            torch.cuda.synchronize()
+            return C.cpu().numpy()
+        single = np.concatenate([run(x[m:m + 1]) for m in range(8)])
+        assert rel(single, A.astype(np.float64) @ W.astype(np.float64).T) <= 1e-5
+        for M in (2, 3, 4, 5, 8):
+            np.testing.assert_array_equal(run(x[:M]), single[:M], err_msg=f"M={M} {dt.__name__}")
+
+
 def test_f16_fused_batch_bit_identical(dev):
     import torch
     import qmm
