@@ -8,8 +8,9 @@ the same per row.  Bars:
 * per activation row m: max_n |y[m, n] - y64[m, n]| / max_n |y64[m, n]| <= 1e-3 (GEMV) or 1e-2
   (prefill) against the fp64 product on the exact weights, with rows scaled by 1e6, 3e4 and 1e-7
   next to ordinary rows;
-* GEMV rows bit-identical for every M (M = 4 against four M = 1 calls), including the windowed
-  kernel that M = 4 takes at K = 28672 against the resident one that M = 1 takes.
+* GEMV rows bit-identical for every M (M = 3 and 4 against M = 1 calls), including the two
+  2-row blocks of resident activations that M = 3, 4 take at K = 28672 (four staged rows do not
+  fit the LDS) against the one-row kernel of M = 1.
 """
 
 import numpy as np
@@ -79,6 +80,8 @@ def test_gemv_fp32_beyond_f16_range(dev, t, K):
     for m in range(4):
         y1 = run(t, x[m:m + 1], w, N, K, dev)
         assert np.array_equal(y1[0], y4[m]), f"{O.TYPE_NAMES.get(t, t)} K={K}: row {m} differs from M=1"
+    y3 = run(t, x[:3], w, N, K, dev)
+    assert np.array_equal(y3, y4[:3]), f"{O.TYPE_NAMES.get(t, t)} K={K}: M=3 rows differ from M=4"
 
 
 @pytest.mark.parametrize("t", [O.GGML_Q4_K, O.GGML_Q6_K, O.GGML_Q8_0])

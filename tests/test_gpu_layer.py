@@ -121,7 +121,8 @@ def test_rope(dev, neox, seq, pos, heads, d, base):
 
 @pytest.mark.parametrize("q_len,kv_len,start,heads,kvh,d", [(12, 12, 0, 16, 4, 64), (1, 25, 24, 16, 4, 64),
                                                             (1, 1000, 999, 32, 8, 128), (40, 300, 260, 8, 2, 128),
-                                                            (3, 3, 0, 4, 4, 256), (5, 130, 125, 4, 2, 96)])
+                                                            (3, 3, 0, 4, 4, 256), (5, 130, 125, 4, 2, 96),
+                                                            (1, 1024, 1023, 16, 2, 64), (1, 2100, 2099, 16, 4, 128)])
 def test_gqa_attention(dev, q_len, kv_len, start, heads, kvh, d):
     import torch
     import qmm
