@@ -218,7 +218,8 @@ __global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restri
                                                        int chunks) {
     constexpr int G = 8;  // keys per batch
     const int lane = threadIdx.x & 63;
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    // wave-uniform (scalar registers), so the head, chunk and row arithmetic below is scalar
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t total = static_cast<int64_t>(q_len) * heads * chunks;
     if (wave >= total) return;
     // waves of one workgroup: consecutive heads of the same (m, c), so the query heads that share
@@ -341,7 +342,9 @@ __global__ __launch_bounds__(256) void attention_keys_kernel(const _Float16* __r
                                                             int causal, int chunks, DecodeRope dr) {
     constexpr int kMaxPairs = 64;  // head_dim <= 128
     const int lane = threadIdx.x & 63;
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    // wave-uniform (scalar registers), so the head, chunk and row arithmetic below is scalar
+    const int wl = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + wl;
     const int64_t total = static_cast<int64_t>(q_len) * heads * chunks;
     if (wave >= total) return;
     const int h = static_cast<int>(wave % heads);
@@ -359,11 +362,33 @@ __global__ __launch_bounds__(256) void attention_keys_kernel(const _Float16* __r
     const uint32_t* qp = reinterpret_cast<const uint32_t*>(Q + (static_cast<size_t>(m) * heads + h) * head_dim);
     const int pos = start_pos + m;                       // the new key (kRope: m == 0)
     const int j_new = kRope && pos >= s0 && pos < s0 + kAttnChunk ? pos - s0 : -1;
+    // The chunk's K and V rows are requested first: they do not depend on the rotation below, so
+    // one memory round trip covers them, the query and the new key.
+    // A dummy lane (and the new key's lane, which takes its key from LDS) reads a row below the
+    // new key: s0 when the new key is not the chunk's first, else row 0 (pos > 0), else it is masked
+    const int dummy = j_new == 0 ? 0 : s0;
+    const int sj = lane < n && lane != j_new ? s0 + lane : (kRope ? min(dummy, max(pos - 1, 0)) : s0);
+    const u32x4* kr = reinterpret_cast<const u32x4*>(Kc + static_cast<size_t>(sj) * row + static_cast<size_t>(kvh) * head_dim);
+    u32x4 kv[kMaxPairs / 4];
+#pragma unroll
+    for (int i = 0; i < kMaxPairs / 4; ++i)
+        if (4 * i < pairs) kv[i] = kr[i];
+    // the chunk's V rows are requested together with the K rows (they do not depend on the scores):
+    // lane l <-> dims 2l, 2l + 1 of every row; rows past the chunk re-read its last key
+    const bool own = 2 * lane < head_dim;
+    const int vl = own ? lane : 0;
+    const uint32_t* vbase = reinterpret_cast<const uint32_t*>(Vc + static_cast<size_t>(kvh) * head_dim);  // uniform
+    const size_t vrow = row / 2;  // in f16 pairs
+    uint32_t vv[kAttnChunk];
+    // in the kRope launch the new key's value comes from v_new and rows past the chunk's keys are
+    // replaced by zeros below, so the loads stay below the new key's row where it is in this chunk
+    const int vlast = j_new > 0 ? j_new - 1 : max(n - 1, 0);
+#pragma unroll
+    for (int j = 0; j < kAttnChunk; ++j) vv[j] = (vbase + static_cast<size_t>(s0 + min(j, vlast)) * vrow)[vl];
     __shared__ __align__(16) _Float16 rot[4][2][2 * kMaxPairs];  // [wave][q, k_new][dim]
     if constexpr (kRope) {
         // lane p rotates pair p (dims 2p, 2p + 1, or p, p + head_dim / 2) of the query and of the
         // new key, as rope_kernel does
-        const int wl = threadIdx.x >> 6;
         if (lane < pairs) {
             const float cs = dr.cs[lane], sn = dr.sn[lane];
             const int i0 = dr.neox ? lane : 2 * lane, i1 = dr.neox ? lane + pairs : 2 * lane + 1;
@@ -390,34 +415,14 @@ __global__ __launch_bounds__(256) void attention_keys_kernel(const _Float16* __r
         __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         qp = reinterpret_cast<const uint32_t*>(rot[wl][0]);
     }
-    // a dummy lane (and the new key's lane, which takes its key from LDS) reads a row below the
-    // new key: s0 when the new key is not the chunk's first, else row 0 (pos > 0), else it is masked
-    const int dummy = j_new == 0 ? 0 : s0;
-    const int sj = lane < n && lane != j_new ? s0 + lane : (kRope ? min(dummy, max(pos - 1, 0)) : s0);
-    const u32x4* kr = reinterpret_cast<const u32x4*>(Kc + static_cast<size_t>(sj) * row + static_cast<size_t>(kvh) * head_dim);
-    u32x4 kv[kMaxPairs / 4];
-#pragma unroll
-    for (int i = 0; i < kMaxPairs / 4; ++i)
-        if (4 * i < pairs) kv[i] = kr[i];
     if constexpr (kRope) {
         if (lane == j_new) {
-            const u32x4* kn = reinterpret_cast<const u32x4*>(rot[threadIdx.x >> 6][1]);
+            const u32x4* kn = reinterpret_cast<const u32x4*>(rot[wl][1]);
 #pragma unroll
             for (int i = 0; i < kMaxPairs / 4; ++i)
                 if (4 * i < pairs) kv[i] = kn[i];
         }
     }
-    // the chunk's V rows are requested together with the K rows (they do not depend on the scores):
-    // lane l <-> dims 2l, 2l + 1 of every row; rows past the chunk re-read its last key
-    const bool own = 2 * lane < head_dim;
-    const uint32_t* vbase = reinterpret_cast<const uint32_t*>(Vc + static_cast<size_t>(kvh) * head_dim) + (own ? lane : 0);
-    const size_t vrow = row / 2;  // in f16 pairs
-    uint32_t vv[kAttnChunk];
-    // in the kRope launch the new key's value comes from v_new and rows past the chunk's keys are
-    // replaced by zeros below, so the loads stay below the new key's row where it is in this chunk
-    const int vlast = j_new > 0 ? j_new - 1 : max(n - 1, 0);
-#pragma unroll
-    for (int j = 0; j < kAttnChunk; ++j) vv[j] = vbase[static_cast<size_t>(s0 + min(j, vlast)) * vrow];
     if constexpr (kRope) {
         const uint32_t vn = own ? reinterpret_cast<const uint32_t*>(dr.v_new + static_cast<size_t>(kvh) * head_dim)[lane] : 0u;
 #pragma unroll
@@ -443,7 +448,8 @@ __global__ __launch_bounds__(256) void attention_keys_kernel(const _Float16* __r
     float acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
     for (int j = 0; j < kAttnChunk; ++j) {
-        const float pj = __shfl(e, j, 64);  // 0 beyond the chunk's keys
+        // lane j's weight, read into a scalar register (0 beyond the chunk's keys)
+        const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
         h2v v;
         __builtin_memcpy(&v, &vv[j], 4);
         acc0 += pj * static_cast<float>(v[0]);
@@ -1209,7 +1215,7 @@ hipError_t release_layer_workspaces() {
                 if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
                 if ((e = hipFree(it->second.buf)) != hipSuccess) {
                     it = m->erase(it);  // the runtime owns the pointer now, whatever it reported
-                    hipSetDevice(cur);
+                    (void)hipSetDevice(cur);  // the free's error is the one reported
                     return e;
                 }
             }
