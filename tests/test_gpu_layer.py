@@ -238,12 +238,13 @@ def make_layer(r, hidden, inter, heads, kvh, d, types):
     return packed, deq
 
 
-# Decode positions cover the new key as the first of a 64-key chunk (64) and position 0 (no
-# prefill); NeoX pairs are rotated in the decode attention kernel too.  Gate and up of one type
+# Decode positions cover the new key as the first of a 64-key chunk (64, 128, 192), as the last
+# (127, 191), and position 0 (no prefill); NeoX pairs are rotated in the decode attention kernel too.  Gate and up of one type
 # run as paired rows writing SwiGLU's output; of different types, as separate launches.
 @pytest.mark.parametrize("prefill,neox,up_type", [(4, False, O.GGML_Q4_0), (40, False, O.GGML_Q4_0),
                                                   (64, False, O.GGML_Q4_K), (0, False, O.GGML_Q4_K),
-                                                  (40, True, O.GGML_Q4_K), (20, False, O.GGML_Q4_K)])
+                                                  (40, True, O.GGML_Q4_K), (20, False, O.GGML_Q4_K),
+                                                  (127, False, O.GGML_Q4_K), (191, True, O.GGML_Q4_K)])
 def test_forward_layer_prefill_then_decode(dev, prefill, neox, up_type):
     import torch
     import qmm
@@ -266,13 +267,14 @@ def test_forward_layer_prefill_then_decode(dev, prefill, neox, up_type):
     cfg = {"num_heads": heads, "num_kv_heads": kvh, "head_dim": d, "rms_norm_eps": 1e-5, "rope_freq_base": 10000.0,
            "rope_neox": neox}
     total = prefill + 2
+    cap = max(80, total)  # KV cache rows
     x = (r.standard_normal((total, hidden)) * 0.5).astype(np.float16)
-    kc, vc = np.zeros((80, kvh, d), np.float16), np.zeros((80, kvh, d), np.float16)
+    kc, vc = np.zeros((cap, kvh, d), np.float16), np.zeros((cap, kvh, d), np.float16)
     want_pre = L.layer_forward(x[:prefill], deq, cfg, kc, vc, 0) if prefill else None
     want_dec = L.layer_forward(x[prefill:prefill + 1], deq, cfg, kc, vc, prefill)
     want_dec2 = L.layer_forward(x[prefill + 1:], deq, cfg, kc, vc, prefill + 1)
     lib = qmm.lib()
-    qmm.check(lib.qmm_kv_cache_init(3, 80, kvh, d))
+    qmm.check(lib.qmm_kv_cache_init(3, cap, kvh, d))
     try:
         X = t16(x, dev)
         Y = torch.empty_like(X)
