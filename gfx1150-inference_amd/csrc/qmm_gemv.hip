@@ -707,26 +707,16 @@ template <class F, int MR, int YT, int NW, typename TA>
 constexpr bool kFoldable = MR == 1 && std::is_same<TA, __half>::value && (NW <= 8 || (YT == 1 && F::kType != QMM_TYPE_F16));
 typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
 
-// The loads (fused_load) are issued before the kernel's first weight items and the rest
-// (fused_finish) runs after them, so the staging waits only for its own loads while the weight
-// bytes are still in flight.
-struct FusedRegs {
-    h16x8 av[kFuseOwn][2], rv[kFuseOwn][2], wv[kFuseOwn][2];
-    int kk[kFuseOwn];
-};
-
 template <class F, int MR, int NW>
-__device__ __forceinline__ void fused_load(const __half* A, const GemvFuse& fz, int M, int K, int m0, int nwin, int tid,
-                                           FusedRegs& fr) {
+__device__ __forceinline__ void stage_fused(const __half* A, const GemvFuse& fz, int M, int K, int m0, int nwin, int tid) {
     static_assert(MR == 1, "one activation row");
+    __shared__ float red[NW];
     const int items = nwin * 256;
     const _Float16* a16 = reinterpret_cast<const _Float16*>(A) + static_cast<size_t>(m0) * K;
     const _Float16* r16 = static_cast<const _Float16*>(fz.R) + static_cast<size_t>(m0) * K;
     const bool two = fz.kind == 2;
-    auto& av = fr.av;
-    auto& rv = fr.rv;
-    auto& wv = fr.wv;
-    auto& kk = fr.kk;
+    h16x8 av[kFuseOwn][2], rv[kFuseOwn][2], wv[kFuseOwn][2];
+    int kk[kFuseOwn];
 #pragma unroll
     for (int j = 0; j < kFuseOwn; ++j) {
         const int it = min(tid + 64 * NW * j, items - 1);
@@ -751,17 +741,6 @@ __device__ __forceinline__ void fused_load(const __half* A, const GemvFuse& fz, 
             }
         }
     }
-}
-
-template <class F, int MR, int NW>
-__device__ __forceinline__ void fused_finish(const GemvFuse& fz, int M, int K, int m0, int nwin, int tid, FusedRegs& fr) {
-    __shared__ float red[NW];
-    const int items = nwin * 256;
-    const bool two = fz.kind == 2;
-    auto& av = fr.av;
-    const auto& rv = fr.rv;
-    const auto& wv = fr.wv;
-    const auto& kk = fr.kk;
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < kFuseOwn; ++j) {
@@ -944,14 +923,11 @@ void gemv_resident_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int 
     bool fused = false;
     if constexpr (kFoldable<F, MR, YT, NW, TA>) fused = fz.kind != 0;
     if (fused) {
-        // the prologue's loads, then the weight bytes, then the prologue (it waits for its own
-        // loads only)
-        FusedRegs fr;
-        if constexpr (kFoldable<F, MR, YT, NW, TA>) fused_load<F, MR, NW>(A, fz, M, K, m0, nwin, tid, fr);
+        // weight bytes first, then the activations with their prologue
         load_item(gl, wl, b0); next(gl, wl);
         if constexpr (PD >= 1) { load_item(gl, wl, b1); next(gl, wl); }
         if constexpr (PD >= 2) { load_item(gl, wl, b2); next(gl, wl); }
-        if constexpr (kFoldable<F, MR, YT, NW, TA>) fused_finish<F, MR, NW>(fz, M, K, m0, nwin, tid, fr);
+        if constexpr (kFoldable<F, MR, YT, NW, TA>) stage_fused<F, MR, NW>(A, fz, M, K, m0, nwin, tid);
     } else {
         if constexpr (kF32) {
             if (tid < nwin * MR) wmax[tid] = 0u;
@@ -1122,13 +1098,6 @@ void gemv_stream_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K,
     int gl = gc, wl = 0;
     const bool active = gc < nrg;
 
-    bool fused = false;
-    if constexpr (kFoldable<F, MR, YT, NW, TA>) fused = fz.kind != 0;
-    // with a prologue its loads come first, so that it waits for them only
-    FusedRegs fr;
-    if constexpr (kFoldable<F, MR, YT, NW, TA>) {
-        if (fused) fused_load<F, MR, NW>(A, fz, M, K, m0, nwin, tid, fr);
-    }
     // the first NS - 1 items are requested before the activations are staged
 #pragma unroll
     for (int j = 0; j < NS - 1; ++j) {
@@ -1136,8 +1105,10 @@ void gemv_stream_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K,
         next(gl, wl);
     }
     const int items = nwin * MR * 256;
+    bool fused = false;
+    if constexpr (kFoldable<F, MR, YT, NW, TA>) fused = fz.kind != 0;
     if (fused) {
-        if constexpr (kFoldable<F, MR, YT, NW, TA>) fused_finish<F, MR, NW>(fz, M, K, m0, nwin, tid, fr);
+        if constexpr (kFoldable<F, MR, YT, NW, TA>) stage_fused<F, MR, NW>(A, fz, M, K, m0, nwin, tid);
     } else {
         if constexpr (kF32) {
             if (tid < nwin * MR) wmax[tid] = 0u;
