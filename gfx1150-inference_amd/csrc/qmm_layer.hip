@@ -324,7 +324,9 @@ __global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restri
 // With kRope (one query row, the decode step): Q, k_new and v_new are the projections before
 // RoPE; each wave rotates its query into LDS, the new key (position start_pos) is rotated into LDS
 // and stands in for its cache row, and the first query head of each KV head's group writes the
-// rotated key and the value into the cache row (which no wave of this launch reads).
+// rotated key and the value into the cache row.  No wave of the launch uses that row's cache
+// contents: the new key's lane takes the rotated key from LDS and its value from v_new (a load
+// of the row issued for a masked or replaced lane is discarded).
 struct DecodeRope {
     const _Float16* k_new;  // [kv_heads][head_dim]
     const _Float16* v_new;
