@@ -403,7 +403,7 @@ def run_dequant(torch, qmm, hip, gen, dev, reps=20):
     return res
 
 
-# time at the target fraction (GEMV 70 % of HBM, prefill 50 % of the dense peak)
+# Time per call at the target fraction of peak (GEMV 70 % of HBM, prefill 50 % of the dense f16 peak)
 TARGETS_US = {"8b_q8_0_layer_m1": 41.4, "8b_q4_k_m_layer_m1": 24.7, "8b_q6_k_lm_head_m1": 77.0,
               "prefill_m512_per_matrix": 47.8, "70b_q4_k_m_layer_m1": 96.9, "70b_q4_k_m_layer_m4": 97.2}
 
@@ -716,8 +716,8 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1:
-        print(f"bench.py: --gpus {args.gpus} is not supported; this build measures one GPU "
-              "(the hot path shards by weight rows, see DESIGN.md).", file=sys.stderr)
+        print(f"bench.py: --gpus {args.gpus} is not supported; only one GPU is measured "
+              "(the path would shard by weight rows, one slice per GPU).", file=sys.stderr)
         sys.exit(2)
 
     import torch
