@@ -27,7 +27,7 @@ extern "C" {
 enum qmm_status {
     QMM_OK = 0,
     QMM_ERR_INVALID_ARGUMENT = 1, /* maps to the reference's std::invalid_argument / ValueError */
-    QMM_ERR_UNSUPPORTED = 2,      /* valid request this build does not implement */
+    QMM_ERR_UNSUPPORTED = 2,      /* valid request the library does not implement */
     QMM_ERR_HIP = 3,              /* HIP runtime error; maps to std::runtime_error / RuntimeError */
     QMM_ERR_IO = 4,               /* file open / read failure (qmm_upload_file, qmm_read_file); OSError */
     QMM_ERR_OUT_OF_RANGE = 5      /* index outside the KV cache pool (std::out_of_range); IndexError */

@@ -1,6 +1,6 @@
 """CPU oracle for the GGUF quantized-matmul path (TEST INFRASTRUCTURE ONLY).
 
-This module is the checker, never the product: only ``tests/``,
+This module checks results and is never the product: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it.  The shipped path (``libqmm_gfx950.so`` and ``matmul_module``) never
 calls into it and has no CPU fallback.

@@ -1,4 +1,4 @@
-"""CPU tests that pin the oracle (oracle/gguf_oracle.py) before it is trusted as the checker.
+"""CPU tests that pin the oracle (oracle/gguf_oracle.py) before the GPU tests compare against it.
 
 What pins what:
 * layouts + dequant formulas  -> known-answer blocks packed byte-by-byte from the GGML layout
