@@ -351,11 +351,12 @@ def time_gemv(torch, qmm, hip, weights, t, n, k, M, io, reps):
     return us
 
 
-def run_small_m(torch, qmm, hip, gen, dev, Ms=(1, 4, 8, 12, 16, 17, 24, 31)):
+def run_small_m(torch, qmm, hip, gen, dev, Ms=(1, 2, 4, 5, 8, 12, 16, 17, 24, 31)):
     """Small M (prompt chunks of fewer than 32 tokens, src/inference.py:255-286) on the 70B gate
     (Q4_K 28672 x 8192) and down (Q6_K 8192 x 28672) shapes, fp16 I/O: µs per call and algorithmic
-    GB/s (weights once + activations + outputs).  M <= 16 runs the GEMV (4- or 8-row blocks), M >= 17
-    the 32-row MFMA tile."""
+    GB/s (weights once + activations + outputs).  M <= 16 runs the GEMV kernels (Q4_K: the v_dot2 GEMV
+    at M = 1, the matrix-core GEMV from M = 2; Q6_K: v_dot2 in 4- or 8-row blocks), M >= 17 the 32-row
+    MFMA tile."""
     res = {}
     for name, t, n, k, copies in (("gate_q4_k_28672x8192", Q4_K, 28672, 8192, 12),
                                   ("down_q6_k_8192x28672", Q6_K, 8192, 28672, 8)):

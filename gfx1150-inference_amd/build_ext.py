@@ -25,7 +25,7 @@ BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_NAME = "libqmm_gfx950.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 
-HIP_SOURCES = ["qmm_api.hip", "qmm_gemv.hip", "qmm_dequant.hip", "qmm_prefill.hip", "qmm_embed.hip", "qmm_upload.hip", "qmm_layer.hip",
+HIP_SOURCES = ["qmm_api.hip", "qmm_gemv.hip", "qmm_gemv_mfma.hip", "qmm_dequant.hip", "qmm_prefill.hip", "qmm_embed.hip", "qmm_upload.hip", "qmm_layer.hip",
                "qmm_host.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

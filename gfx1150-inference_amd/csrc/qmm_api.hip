@@ -16,6 +16,8 @@ namespace {
 
 thread_local std::string g_last_error;
 std::atomic<int> g_gemv_max_m{qmm::kGemvMaxMDefault};  // qmm_set_gemv_max_m
+thread_local int g_thread_gemv_max_m = 0;              // qmm_set_thread_gemv_max_m (0: the process value)
+thread_local int g_row_identity = 0;                   // qmm_set_row_identity
 
 int fail(int code, const std::string& msg) {
     g_last_error = msg;
@@ -84,9 +86,10 @@ int check_dequant_args(int t, const void* W, void* out, int out_dtype, int64_t n
     return QMM_OK;
 }
 
-// gmax: the GEMV / prefill threshold the call was issued under (qmm::gemv_max_m() read once).
+// gmax: the GEMV / prefill threshold the call was issued under (qmm::gemv_max_m() read once);
+// ident: every GEMV-range M on the kernel family of M = 1 (rows bit-identical across M).
 int gemm_impl(int t, const void* A, int a_dtype, const void* W, void* C, int c_dtype, int M, int N, int K,
-              hipStream_t stream, int gmax) {
+              hipStream_t stream, int gmax, bool ident) {
     int rc = check_gemm_args(t, A, a_dtype, W, C, c_dtype, M, N, K);
     if (rc != QMM_OK) return rc;
     if (M == 0 || N == 0) return QMM_OK;
@@ -94,7 +97,7 @@ int gemm_impl(int t, const void* A, int a_dtype, const void* W, void* C, int c_d
     if (M >= gmax && qmm::gemm_prefill_supported(t, a_dtype, c_dtype, M, N, K, A, W, C))
         e = qmm::launch_gemm_prefill(t, A, a_dtype, W, C, c_dtype, M, N, K, stream);
     else
-        e = qmm::launch_gemv(t, A, a_dtype, W, C, c_dtype, M, N, K, stream);
+        e = qmm::launch_gemv(t, A, a_dtype, W, C, c_dtype, M, N, K, stream, ident);
     if (e != hipSuccess) return hip_fail(e, "qmm_gemm kernel launch");
     return QMM_OK;
 }
@@ -185,7 +188,9 @@ int matmul_host(int t, const void* hA, const void* hB, void* hC, int M, int N, i
     if ((e = ws_ensure(ws, need)) != hipSuccess) return hip_fail(e, "workspace hipMalloc");
     if ((e = hipMemcpy(ws.buf[0], hA, sa, hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "hipMemcpy A");
     if ((e = hipMemcpy(ws.buf[1], hB, sb, hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "hipMemcpy B");
-    rc = gemm_impl(t, ws.buf[0], QMM_DTYPE_F16, ws.buf[1], ws.buf[2], QMM_DTYPE_F16, M, N, K, nullptr, qmm::gemv_max_m());
+    // the reference's host launchers: rows bit-identical across M, as its tests assert
+    rc = gemm_impl(t, ws.buf[0], QMM_DTYPE_F16, ws.buf[1], ws.buf[2], QMM_DTYPE_F16, M, N, K, nullptr, qmm::gemv_max_m(),
+                   true);
     if (rc != QMM_OK) return rc;
     if ((e = hipMemcpy(hC, ws.buf[2], sc, hipMemcpyDeviceToHost)) != hipSuccess) return hip_fail(e, "hipMemcpy C");
     return QMM_OK;
@@ -215,7 +220,9 @@ int dequant_host(int t, const void* hq, void* hout, int num_elements) {
 
 int qmm::set_last_error(int code, const std::string& msg) { return fail(code, msg); }
 
-int qmm::gemv_max_m() { return g_gemv_max_m.load(std::memory_order_relaxed); }
+int qmm::gemv_max_m() {
+    return g_thread_gemv_max_m > 0 ? g_thread_gemv_max_m : g_gemv_max_m.load(std::memory_order_relaxed);
+}
 
 extern "C" {
 
@@ -233,6 +240,22 @@ int qmm_set_gemv_max_m(int m) {
     return QMM_OK;
 }
 
+int qmm_set_thread_gemv_max_m(int m) {
+    if (m < 0 || m > qmm::kGemvMaxMLimit)
+        return fail(QMM_ERR_INVALID_ARGUMENT, "qmm_set_thread_gemv_max_m: m must be 0 or in [1, " +
+                                                  std::to_string(qmm::kGemvMaxMLimit) + "], got " + std::to_string(m) + ".");
+    g_thread_gemv_max_m = m;
+    return QMM_OK;
+}
+
+int qmm_set_row_identity(int on) {
+    if (on != 0 && on != 1) return fail(QMM_ERR_INVALID_ARGUMENT, "qmm_set_row_identity: on must be 0 or 1.");
+    g_row_identity = on;
+    return QMM_OK;
+}
+
+int qmm_row_identity(void) { return g_row_identity; }
+
 size_t qmm_weight_bytes(int ggml_type, int64_t n, int64_t k) {
     if (!gemm_type(ggml_type) || n < 0 || k < 0) return 0;
     const int qk = qmm::block_elems(ggml_type);
@@ -242,7 +265,8 @@ size_t qmm_weight_bytes(int ggml_type, int64_t n, int64_t k) {
 
 int qmm_gemm(int ggml_type, const void* A, int a_dtype, const void* W, void* C, int c_dtype, int M, int N, int K,
              void* stream) {
-    return gemm_impl(ggml_type, A, a_dtype, W, C, c_dtype, M, N, K, static_cast<hipStream_t>(stream), qmm::gemv_max_m());
+    return gemm_impl(ggml_type, A, a_dtype, W, C, c_dtype, M, N, K, static_cast<hipStream_t>(stream), qmm::gemv_max_m(),
+                     g_row_identity != 0);
 }
 
 int qmm_gemm_noalloc(int ggml_type, const void* A, int a_dtype, const void* W, void* C, int c_dtype, int M, int N, int K,
@@ -256,12 +280,12 @@ int qmm_gemm_noalloc(int ggml_type, const void* A, int a_dtype, const void* W, v
         size_t need = 0;
         e = qmm::launch_gemm_prefill_noalloc(ggml_type, A, a_dtype, W, C, c_dtype, M, N, K, s, &need);
         if (e == hipErrorOutOfMemory && need > qmm::kNoAllocScratchBytes)
-            return fail(QMM_ERR_OUT_OF_RANGE, "qmm_gemm_noalloc: M=" + std::to_string(M) + " N=" + std::to_string(N) +
+            return fail(QMM_ERR_UNSUPPORTED, "qmm_gemm_noalloc: M=" + std::to_string(M) + " N=" + std::to_string(N) +
                                                   " K=" + std::to_string(K) + " needs " + std::to_string(need) +
                                                   " bytes of scratch; the static scratch holds " +
                                                   std::to_string(qmm::kNoAllocScratchBytes) + " bytes.");
     } else {
-        e = qmm::launch_gemv(ggml_type, A, a_dtype, W, C, c_dtype, M, N, K, s);  // allocates nothing
+        e = qmm::launch_gemv(ggml_type, A, a_dtype, W, C, c_dtype, M, N, K, s, g_row_identity != 0);  // allocates nothing
     }
     if (e != hipSuccess) return hip_fail(e, "qmm_gemm_noalloc kernel launch");
     return QMM_OK;
@@ -283,7 +307,8 @@ int qmm_gemm_batch(const qmm_gemm_desc* descs, int count, void* stream) {
         if (ev && (e = hipEventRecord(static_cast<hipEvent_t>(ev), s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
         return QMM_OK;
     };
-    const int gmax = qmm::gemv_max_m();  // one threshold for the whole batch
+    const int gmax = qmm::gemv_max_m();  // one threshold (and kernel policy) for the whole batch
+    const bool ident = g_row_identity != 0;
     int i = 0;
     while (i < count) {
         // longest run starting at i that one launch can serve
@@ -305,7 +330,8 @@ int qmm_gemm_batch(const qmm_gemm_desc* descs, int count, void* stream) {
             hipError_t e = h.M >= gmax
                                ? qmm::launch_gemm_prefill_fused(h.ggml_type, h.A, h.a_dtype, h.c_dtype, h.M, h.K, W, C, N,
                                                                 j - i, s)
-                               : qmm::launch_gemv_fused(h.ggml_type, h.A, h.a_dtype, h.c_dtype, h.M, h.K, W, C, N, j - i, s);
+                               : qmm::launch_gemv_fused(h.ggml_type, h.A, h.a_dtype, h.c_dtype, h.M, h.K, W, C, N, j - i, s,
+                                                        ident);
             if (e == hipSuccess) {
                 if ((rc = record(descs[j - 1].ev_after)) != QMM_OK) return rc;
                 i = j;
@@ -313,7 +339,8 @@ int qmm_gemm_batch(const qmm_gemm_desc* descs, int count, void* stream) {
             }
             if (e != hipErrorNotSupported) return hip_fail(e, "qmm_gemm_batch fused kernel launch");
             // not fusable after all (e.g. byte-load fallback): run the first one alone
-            if ((rc = gemm_impl(h.ggml_type, h.A, h.a_dtype, h.W, h.C, h.c_dtype, h.M, h.N, h.K, s, gmax)) != QMM_OK) return rc;
+            if ((rc = gemm_impl(h.ggml_type, h.A, h.a_dtype, h.W, h.C, h.c_dtype, h.M, h.N, h.K, s, gmax, ident)) != QMM_OK)
+                return rc;
             if ((rc = record(h.ev_after)) != QMM_OK) return rc;
             ++i;
             continue;
@@ -321,7 +348,7 @@ int qmm_gemm_batch(const qmm_gemm_desc* descs, int count, void* stream) {
         const qmm_gemm_desc& d = descs[i];
         int rc = record(d.ev_before);
         if (rc != QMM_OK) return rc;
-        if ((rc = gemm_impl(d.ggml_type, d.A, d.a_dtype, d.W, d.C, d.c_dtype, d.M, d.N, d.K, s, gmax)) != QMM_OK) return rc;
+        if ((rc = gemm_impl(d.ggml_type, d.A, d.a_dtype, d.W, d.C, d.c_dtype, d.M, d.N, d.K, s, gmax, ident)) != QMM_OK) return rc;
         if ((rc = record(d.ev_after)) != QMM_OK) return rc;
         ++i;
     }
@@ -496,16 +523,20 @@ int qmm_dequantize(int ggml_type, const void* W, void* out, int out_dtype, int64
 }
 
 int qmm_matmul_q4_0_device(const void* a, const void* b, void* c, int M, int N, int K, void* s) {
-    return qmm_gemm(QMM_TYPE_Q4_0, a, QMM_DTYPE_F16, b, c, QMM_DTYPE_F16, M, N, K, s);
+    return gemm_impl(QMM_TYPE_Q4_0, a, QMM_DTYPE_F16, b, c, QMM_DTYPE_F16, M, N, K, static_cast<hipStream_t>(s),
+                     qmm::gemv_max_m(), true);
 }
 int qmm_matmul_q8_0_device(const void* a, const void* b, void* c, int M, int N, int K, void* s) {
-    return qmm_gemm(QMM_TYPE_Q8_0, a, QMM_DTYPE_F16, b, c, QMM_DTYPE_F16, M, N, K, s);
+    return gemm_impl(QMM_TYPE_Q8_0, a, QMM_DTYPE_F16, b, c, QMM_DTYPE_F16, M, N, K, static_cast<hipStream_t>(s),
+                     qmm::gemv_max_m(), true);
 }
 int qmm_matmul_q4_k_device(const void* a, const void* b, void* c, int M, int N, int K, void* s) {
-    return qmm_gemm(QMM_TYPE_Q4_K, a, QMM_DTYPE_F16, b, c, QMM_DTYPE_F16, M, N, K, s);
+    return gemm_impl(QMM_TYPE_Q4_K, a, QMM_DTYPE_F16, b, c, QMM_DTYPE_F16, M, N, K, static_cast<hipStream_t>(s),
+                     qmm::gemv_max_m(), true);
 }
 int qmm_matmul_q6_k_device(const void* a, const void* b, void* c, int M, int N, int K, void* s) {
-    return qmm_gemm(QMM_TYPE_Q6_K, a, QMM_DTYPE_F16, b, c, QMM_DTYPE_F16, M, N, K, s);
+    return gemm_impl(QMM_TYPE_Q6_K, a, QMM_DTYPE_F16, b, c, QMM_DTYPE_F16, M, N, K, static_cast<hipStream_t>(s),
+                     qmm::gemv_max_m(), true);
 }
 
 int qmm_matmul_q4_0_host(const void* a, const void* b, void* c, int M, int N, int K) {

@@ -41,35 +41,13 @@ typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
 constexpr int kGemvWindow = 4096;   // weights per row per window (64 lanes x 64)
 constexpr int kChunks = 8;          // 8-weight activation chunks per lane slot
 
-// Tuning: minimum waves per SIMD the register allocator must allow (0 = unconstrained), and
-// the rows per wave of the M = 2 kernel for large N.
-#ifndef QMM_GEMV_MIN_WAVES
-#define QMM_GEMV_MIN_WAVES 0
-#endif
-#ifndef QMM_GEMV_YT_BIG
-#define QMM_GEMV_YT_BIG 1
-#endif
-#ifndef QMM_GEMV_NW
-#define QMM_GEMV_NW 8
-#endif
-// Items of weight bytes in flight while one is multiplied (0, 1 or 2).
-#ifndef QMM_GEMV_STREAM
-#define QMM_GEMV_STREAM 1   // streamed-window kernel where its conditions hold
-#endif
-#ifndef QMM_GEMV_F16_STREAM
-#define QMM_GEMV_F16_STREAM 1
-#endif
-#ifndef QMM_GEMV_NS
-#define QMM_GEMV_NS 2       // LDS window slots per wave of the streamed kernel
-#endif
-#ifndef QMM_GEMV_DEPTH
-#define QMM_GEMV_DEPTH 0
-#endif
+// Waves per workgroup of the v_dot2 kernels.
+constexpr int kGemvNW = 8;
+// LDS window slots per wave of the streamed kernel (one window is in flight while one is multiplied).
+constexpr int kGemvNS = 2;
 // Largest M whose launches switch to 16-wave workgroups when the staged activations exceed
 // 40 KB of LDS (fewer workgroups per CU fit then; larger ones keep the waves per CU up).
-#ifndef QMM_GEMV_NW16_MAXM
-#define QMM_GEMV_NW16_MAXM 2
-#endif
+constexpr int kGemvNW16MaxM = 2;
 
 // Register-resident constants (v_and_or_b32 on gfx9 takes no literal operands).
 struct Consts {
@@ -386,7 +364,7 @@ struct GF16 {
     static constexpr int kWinBytes = 2 * kGemvWindow;  // 8192
     static constexpr int kG = 1;
     static constexpr bool kAligned = false;
-    static constexpr bool kStream = QMM_GEMV_F16_STREAM != 0;
+    static constexpr bool kStream = true;
     struct Raw {
         u32x4 w[kChunks];
     };
@@ -422,14 +400,14 @@ struct GF16 {
 // chunks 2q and 2q+1 (fp32, fixed order).
 // ------------------------------------------------------------------------------------------
 template <typename TA>
-__device__ __forceinline__ void load16_act(const TA* p, bool ok, bool vec, uint32_t h[8], float mul, float& amax);
+__device__ __forceinline__ void load16_act(const TA* p, bool ok, bool vec, uint32_t h[8], int sh, float& amax);
 
 // The loads are issued whether or not the activations exist (p is always a valid address);
-// missing ones (`ok` false) are replaced by zeros afterwards.  fp32 values are multiplied by `mul`
-// (a power of two, 1 unless the window is rescaled) before the f16 rounding; `amax` receives the
-// largest magnitude of the 16 unscaled values.
+// missing ones (`ok` false) are replaced by zeros afterwards.  fp32 values are multiplied by 2^sh
+// (0 unless the window is rescaled) before the f16 rounding; `amax` receives the largest magnitude
+// of the 16 unscaled values.
 template <>
-__device__ __forceinline__ void load16_act<float>(const float* p, bool ok, bool vec, uint32_t h[8], float mul, float& amax) {
+__device__ __forceinline__ void load16_act<float>(const float* p, bool ok, bool vec, uint32_t h[8], int sh, float& amax) {
     float x[16];
     if (vec) {
 #pragma unroll
@@ -446,7 +424,7 @@ __device__ __forceinline__ void load16_act<float>(const float* p, bool ok, bool 
     for (int i = 0; i < 16; ++i) {
         x[i] = ok ? x[i] : 0.0f;
         mx = fmaxf(mx, fabsf(x[i]));
-        x[i] *= mul;
+        x[i] = __builtin_ldexpf(x[i], sh);
     }
     amax = mx;
     // pairs (0,2), (1,3), (4,6), (5,7), ... rounded to nearest even (v_cvt_pk_f16_f32)
@@ -462,7 +440,7 @@ __device__ __forceinline__ void load16_act<float>(const float* p, bool ok, bool 
 }
 
 template <>
-__device__ __forceinline__ void load16_act<__half>(const __half* p, bool ok, bool vec, uint32_t h[8], float, float& amax) {
+__device__ __forceinline__ void load16_act<__half>(const __half* p, bool ok, bool vec, uint32_t h[8], int, float& amax) {
     amax = 0.0f;
     uint32_t w[8];
     if (vec) {
@@ -501,12 +479,12 @@ struct StageItem {
     uint32_t h[8];
     float amax;  // largest unscaled magnitude of the item (fp32 activations)
     __device__ __forceinline__ void load(const TA* __restrict__ A, int M, int K, int m0, int w, int item, bool vec,
-                                         float mul = 1.0f) {
+                                         int sh = 0) {
         const int m = item >> 8, q = (item >> 6) & 3, lane = item & 63;
         const int k = w * kGemvWindow + F::xk(lane, 2 * q);
         const bool ok = m0 + m < M && k < K;
         const TA* p = A + static_cast<size_t>(ok ? m0 + m : 0) * K + (ok ? k : 0);
-        load16_act<TA>(p, ok, vec, h, mul, amax);
+        load16_act<TA>(p, ok, vec, h, sh, amax);
     }
     __device__ __forceinline__ void store(int nslots, int slot, int item) const {
         const int m = item >> 8, q = (item >> 6) & 3, lane = item & 63;
@@ -527,18 +505,19 @@ struct StageItem {
 
 // Range of fp32 activations.  f16 holds magnitudes from 2^-14 (normal) to 65504; a window (4096 k)
 // of one activation row whose largest magnitude lies outside that range (at or above 65504, or in
-// [2^-60, 2^-14)) is staged as x * 2^-e with e = exponent(max) - 14, which brings the maximum into
-// [2^14, 2^15), and the window's group coefficients are multiplied by 2^e.  Both multiplications
-// are exact, so the products stay those of the scaled operands; every other window has e = 0 and
-// is staged and multiplied exactly as fp16 activations are.  Infinite or NaN maxima keep e = 0
-// (they propagate as in fp32 arithmetic).  The exponent depends only on the window's own values,
-// so a row's result does not depend on M.
+// [2^-126, 2^-14)) is staged as x * 2^-e with e = exponent(max) - 14, which brings the maximum into
+// [2^14, 2^15), and each group's net contribution (scale times dot sum minus offset times
+// activation sum, formed first: its two terms can leave the fp32 range where their difference
+// does not) is multiplied by 2^e.  These scalings are exact while their results are normal fp32
+// numbers.  Every other window has e = 0 and is staged and multiplied exactly as fp16 activations
+// are.  Infinite or NaN maxima keep e = 0 (they propagate as in fp32 arithmetic), and so do maxima
+// below 2^-126 (their values round to zero in f16).  The exponent depends only on the window's own
+// values, so a row's result does not depend on M.
 __device__ __forceinline__ int window_exp(uint32_t maxbits) {
     const bool big = maxbits >= 0x477FE000u && maxbits < 0x7F800000u;  // [65504, inf)
-    const bool tiny = maxbits >= 0x21800000u && maxbits < 0x38800000u;  // [2^-60, 2^-14)
+    const bool tiny = maxbits >= 0x00800000u && maxbits < 0x38800000u;  // [2^-126, 2^-14)
     return big || tiny ? static_cast<int>(maxbits >> 23) - 127 - 14 : 0;
 }
-__device__ __forceinline__ float exp2_int(int e) { return __uint_as_float(static_cast<uint32_t>(127 + e) << 23); }
 
 // (window, row) maxima of fp32 activations, in LDS: nwin * MR entries for the kernels that stage
 // every window at once (at most 17 fit the LDS), 3 * MR for the windowed kernel.
@@ -548,13 +527,13 @@ constexpr int wmax_size(int n) { return std::is_same<TA, float>::value ? n : 1; 
 
 __device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// 2^e of activation row m in staged window `w` (1 for fp16 activations).
+// e of activation row m in staged window `w` (0 for fp16 activations).
 template <int MR, typename TA>
-__device__ __forceinline__ void window_factors(const uint32_t* wmax_w, float (&pm)[MR]) {
+__device__ __forceinline__ void window_factors(const uint32_t* wmax_w, int (&pe)[MR]) {
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
-        if constexpr (std::is_same<TA, float>::value) pm[m] = exp2_int(window_exp(wmax_w[m]));
-        else pm[m] = 1.0f;
+        if constexpr (std::is_same<TA, float>::value) pe[m] = window_exp(wmax_w[m]);
+        else pe[m] = 0;
     }
 }
 
@@ -574,7 +553,7 @@ __device__ __forceinline__ void restage_out_of_range(const TA* __restrict__ A, c
             const int e = window_exp(wmax[w * MR + (item >> 8)]);
             if (e != 0) {
                 StageItem<F, MR, TA> s2;
-                s2.load(A, M, K, m0, w, item, vec, exp2_int(-e));
+                s2.load(A, M, K, m0, w, item, vec, -e);
                 s2.store(nwin, w, item);
             }
         }
@@ -593,18 +572,18 @@ __device__ __forceinline__ void store_out<__half>(__half* p, float v) {
 
 // acc[m][y] += the window's contribution of row y for activation row m.
 // FULL: every lane slot of the window is inside K (no validity masks).
-// SC: fp32 activations; pm[m] = 2^e of activation row m in this window (1 unless rescaled).
+// SC: fp32 activations; pe[m] = e of activation row m in this window (0 unless rescaled).
 template <class F, int MR, int YT, bool FULL, bool SC = false>
 __device__ __forceinline__ void mac_window(const typename F::Raw (&cur)[YT], int nslots, int slot, int lane, int kv,
-                                           const Consts& KC, float (&acc)[MR][YT], const float (&pm)[MR]) {
+                                           const Consts& KC, float (&acc)[MR][YT], const int (&pe)[MR]) {
     if constexpr (F::kType == QMM_TYPE_F16) {
         // dense weights: no group scales; activations outside K are staged as zeros.  A rescaled
-        // window (pm != 1) is summed on its own and added as pm * sum.
+        // window (pe != 0) is summed on its own and added as 2^e * sum.
         float s0[MR][YT];
 #pragma unroll
         for (int m = 0; m < MR; ++m)
 #pragma unroll
-            for (int y = 0; y < YT; ++y) s0[m][y] = !SC || pm[m] == 1.0f ? acc[m][y] : 0.0f;
+            for (int y = 0; y < YT; ++y) s0[m][y] = !SC || pe[m] == 0 ? acc[m][y] : 0.0f;
 #pragma unroll
         for (int cj = 0; cj < kChunks; ++cj) {
             u32x4 xp[MR];
@@ -628,7 +607,7 @@ __device__ __forceinline__ void mac_window(const typename F::Raw (&cur)[YT], int
 #pragma unroll
         for (int m = 0; m < MR; ++m)
 #pragma unroll
-            for (int y = 0; y < YT; ++y) acc[m][y] = !SC || pm[m] == 1.0f ? s0[m][y] : __fmaf_rn(pm[m], s0[m][y], acc[m][y]);
+            for (int y = 0; y < YT; ++y) acc[m][y] = !SC || pe[m] == 0 ? s0[m][y] : acc[m][y] + __builtin_ldexpf(s0[m][y], pe[m]);
         return;
     }
     constexpr int G = F::kG;
@@ -685,10 +664,13 @@ __device__ __forceinline__ void mac_window(const typename F::Raw (&cur)[YT], int
 #pragma unroll
             for (int y = 0; y < YT; ++y) {
                 float t = acc[m][y];
-                const float ag = SC ? a[y][g] * pm[m] : a[y][g];   // exact: pm is a power of two
-                const float bg = SC ? B[y][g] * pm[m] : B[y][g];
-                t = __fmaf_rn(ag, S[m][y], t);
-                t = __fmaf_rn(-bg, sxg, t);
+                if (SC && pe[m] != 0) {  // rescaled window: the group's net, then times 2^e
+                    const float net = __fmaf_rn(a[y][g], S[m][y], -(B[y][g] * sxg));
+                    t += __builtin_ldexpf(net, pe[m]);
+                } else {
+                    t = __fmaf_rn(a[y][g], S[m][y], t);
+                    t = __fmaf_rn(-B[y][g], sxg, t);
+                }
                 acc[m][y] = t;
             }
         }
@@ -869,11 +851,12 @@ __device__ __forceinline__ SegRef<TC> seg_of(const GemvSegs<TC>& sg, int g) {
 
 // Resident-activation kernel: the workgroup stages all windows of its MR activation rows once,
 // then every wave streams (row group, window) items (YT rows each) round-robin over the grid.
-// Three register buffers rotate statically: while item i is multiplied, items i+1 and i+2 are
-// in flight.  Row and window arithmetic is wave-uniform (scalar).  No barrier after staging.
+// One register buffer per item: an item's weight loads are issued as soon as the previous item
+// has been multiplied (the occupancy of several waves per SIMD covers their latency).  Row and
+// window arithmetic is wave-uniform (scalar).  No barrier after staging.
 // Dynamic LDS: MR * nwin * 9216 bytes.
 template <class F, int MR, int YT, int NW, typename TA, typename TC>
-__global__ __launch_bounds__(64 * NW, QMM_GEMV_MIN_WAVES)
+__global__ __launch_bounds__(64 * NW)
 void gemv_resident_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K, int a_vec, int nrg, GemvFuse fz) {
     constexpr bool kF32 = std::is_same<TA, float>::value;
     __shared__ uint32_t wmax[wmax_size<TA>(kWmaxEntries)];
@@ -918,15 +901,12 @@ void gemv_resident_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int 
     // then the LDS writes; the weight loads stay in flight through the barrier.
     constexpr int kFirst = 2;  // activation items per thread issued before the weight loads
     const int items = nwin * MR * 256;
-    constexpr int PD = QMM_GEMV_DEPTH;
-    Raw b0[YT], b1[YT], b2[YT];
+    Raw b0[YT];
     bool fused = false;
     if constexpr (kFoldable<F, MR, YT, NW, TA>) fused = fz.kind != 0;
     if (fused) {
         // weight bytes first, then the activations with their prologue
         load_item(gl, wl, b0); next(gl, wl);
-        if constexpr (PD >= 1) { load_item(gl, wl, b1); next(gl, wl); }
-        if constexpr (PD >= 2) { load_item(gl, wl, b2); next(gl, wl); }
         if constexpr (kFoldable<F, MR, YT, NW, TA>) stage_fused<F, MR, NW>(A, fz, M, K, m0, nwin, tid);
     } else {
         if constexpr (kF32) {
@@ -941,8 +921,6 @@ void gemv_resident_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int 
         }
         // issued by every wave (inactive waves re-read a valid row group) to keep counts static
         load_item(gl, wl, b0); next(gl, wl);
-        if constexpr (PD >= 1) { load_item(gl, wl, b1); next(gl, wl); }
-        if constexpr (PD >= 2) { load_item(gl, wl, b2); next(gl, wl); }
         if constexpr (kF32) lds_barrier();  // the maxima are cleared before any item joins them
 #pragma unroll
         for (int j = 0; j < kFirst; ++j) {
@@ -973,10 +951,10 @@ void gemv_resident_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int 
 
     auto compute = [&](const Raw (&b)[YT]) {
         const int kv = min(K - wc * kGemvWindow, kGemvWindow);
-        float pm[MR];
-        window_factors<MR, TA>(&wmax[kF32 ? wc * MR : 0], pm);
-        if (kv == kGemvWindow) mac_window<F, MR, YT, true, kF32>(b, nwin, wc, lane, kv, KC, acc, pm);
-        else mac_window<F, MR, YT, false, kF32>(b, nwin, wc, lane, kv, KC, acc, pm);
+        int pe[MR];
+        window_factors<MR, TA>(&wmax[kF32 ? wc * MR : 0], pe);
+        if (kv == kGemvWindow) mac_window<F, MR, YT, true, kF32>(b, nwin, wc, lane, kv, KC, acc, pe);
+        else mac_window<F, MR, YT, false, kF32>(b, nwin, wc, lane, kv, KC, acc, pe);
         if (wc == nwin - 1) {
             const SegRef<TC> sr = seg_of(sg, gc);
             reduce_store<MR, YT, TC>(acc, sr.C, M, sr.N, m0, fz.pair ? gc : (gc - sr.g0) * YT, lane, fz);
@@ -988,37 +966,13 @@ void gemv_resident_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int 
         next(gc, wc);
     };
 
-    // PD items are in flight while an item is multiplied; its buffer is refilled with the item
-    // PD + 1 ahead right after (past the wave's last item: a valid row group re-read).
+    // The next item's loads are issued right after an item's multiply (past the wave's last
+    // item: a valid row group re-read).
     const int total = ((nrg - gc + stride - 1) / stride) * nwin;
-    int i = 0;
-    if constexpr (PD == 0) {
-        while (true) {
-            compute(b0);
-            if (++i == total) break;
-            load_item(gl, wl, b0); next(gl, wl);
-        }
-    } else if constexpr (PD == 1) {
-        while (true) {
-            compute(b0);
-            if (++i == total) break;
-            load_item(gl, wl, b0); next(gl, wl);
-            compute(b1);
-            if (++i == total) break;
-            load_item(gl, wl, b1); next(gl, wl);
-        }
-    } else {
-        while (true) {
-            compute(b0);
-            if (++i == total) break;
-            load_item(gl, wl, b0); next(gl, wl);
-            compute(b1);
-            if (++i == total) break;
-            load_item(gl, wl, b1); next(gl, wl);
-            compute(b2);
-            if (++i == total) break;
-            load_item(gl, wl, b2); next(gl, wl);
-        }
+    for (int i = 0;;) {
+        compute(b0);
+        if (++i == total) break;
+        load_item(gl, wl, b0); next(gl, wl);
     }
 }
 
@@ -1050,7 +1004,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 template <class F, int MR, int YT, int NW, int NS, typename TA, typename TC>
-__global__ __launch_bounds__(64 * NW, QMM_GEMV_MIN_WAVES)
+__global__ __launch_bounds__(64 * NW)
 void gemv_stream_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K, int a_vec, int nrg, GemvFuse fz) {
     using WS = WinSlot<F>;
     constexpr bool kF32 = std::is_same<TA, float>::value;
@@ -1148,10 +1102,10 @@ void gemv_stream_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K,
         Raw b[YT];
 #pragma unroll
         for (int y = 0; y < YT; ++y) b[y] = F::load(wslots + (slot * YT + y) * WS::kBytes, lane, kv);
-        float pm[MR];
-        window_factors<MR, TA>(&wmax[kF32 ? wc * MR : 0], pm);
-        if (kv == kGemvWindow) mac_window<F, MR, YT, true, kF32>(b, nwin, wc, lane, kv, KC, acc, pm);
-        else mac_window<F, MR, YT, false, kF32>(b, nwin, wc, lane, kv, KC, acc, pm);
+        int pe[MR];
+        window_factors<MR, TA>(&wmax[kF32 ? wc * MR : 0], pe);
+        if (kv == kGemvWindow) mac_window<F, MR, YT, true, kF32>(b, nwin, wc, lane, kv, KC, acc, pe);
+        else mac_window<F, MR, YT, false, kF32>(b, nwin, wc, lane, kv, KC, acc, pe);
         if (wc == nwin - 1) {
             const SegRef<TC> sr = seg_of(sg, gc);
             reduce_store<MR, YT, TC>(acc, sr.C, M, sr.N, m0, fz.pair ? gc : (gc - sr.g0) * YT, lane, fz);
@@ -1170,7 +1124,7 @@ void gemv_stream_kernel(const TA* __restrict__ A, GemvSegs<TC> sg, int M, int K,
 // window w + 1's activations are staged into the other of two LDS slots and its weight bytes
 // loaded while window w is multiplied; one barrier per window.  Dynamic LDS: MR * 2 * 9216.
 template <class F, int MR, int YT, int NW, typename TA, typename TC>
-__global__ __launch_bounds__(64 * NW, QMM_GEMV_MIN_WAVES)
+__global__ __launch_bounds__(64 * NW)
 void gemv_window_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W, TC* __restrict__ C,
                         int M, int N, int K, int a_vec) {
     constexpr int kItems = MR * 256;
@@ -1224,7 +1178,7 @@ void gemv_window_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W,
 
     for (int w = 0; w < nwin; ++w) {
         const bool more = w + 1 < nwin;
-        float pm[MR];
+        int pe[MR];
         if constexpr (kF32) {
             const uint32_t* wm = &wmax[(w % 3) * MR];
             bool need = false;
@@ -1237,16 +1191,16 @@ void gemv_window_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W,
                     const int e = it < kItems ? window_exp(wm[it >> 8]) : 0;
                     if (e != 0) {
                         StageItem<F, MR, TA> s2;
-                        s2.load(A, M, K, m0, w, it, vec, exp2_int(-e));
+                        s2.load(A, M, K, m0, w, it, vec, -e);
                         s2.store(2, w & 1, it);
                     }
                 }
                 __syncthreads();
             }
-            window_factors<MR, TA>(wm, pm);
+            window_factors<MR, TA>(wm, pe);
             if (tid < MR) wmax[((w + 2) % 3) * MR + tid] = 0u;
         } else {
-            window_factors<MR, TA>(wmax, pm);
+            window_factors<MR, TA>(wmax, pe);
         }
         {
             // unconditional weight prefetch (the last one re-reads window w)
@@ -1263,8 +1217,8 @@ void gemv_window_kernel(const TA* __restrict__ A, const uint8_t* __restrict__ W,
         }
         {
             const int kv = min(K - w * kGemvWindow, kGemvWindow);
-            if (kv == kGemvWindow) mac_window<F, MR, YT, true, kF32>(cur, 2, w & 1, lane, kv, KC, acc, pm);
-            else mac_window<F, MR, YT, false, kF32>(cur, 2, w & 1, lane, kv, KC, acc, pm);
+            if (kv == kGemvWindow) mac_window<F, MR, YT, true, kF32>(cur, 2, w & 1, lane, kv, KC, acc, pe);
+            else mac_window<F, MR, YT, false, kF32>(cur, 2, w & 1, lane, kv, KC, acc, pe);
         }
         if (more) {
 #pragma unroll
@@ -1369,7 +1323,14 @@ hipError_t occupancy(const void* kern, int threads, size_t lds, int& blocks) {
         return hipSuccess;
     }
     if (lds > 65536) {
-        e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        // raised to the largest size the device allows beside the kernel's static LDS: the attribute
+        // belongs to the kernel, and setting it to this call's size would lower it for a later, larger
+        // call whose occupancy is already cached
+        hipFuncAttributes fa;
+        if ((e = hipFuncGetAttributes(&fa, kern)) != hipSuccess) return e;
+        int mx = 0;
+        if ((e = hipDeviceGetAttribute(&mx, hipDeviceAttributeMaxSharedMemoryPerBlock, dev)) != hipSuccess) return e;
+        e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, mx - static_cast<int>(fa.sharedSizeBytes));
         if (e != hipSuccess) return e;
     }
     int n = 0;
@@ -1434,7 +1395,6 @@ hipError_t launch_fast(const void* A, const Seg* segs, int nseg, int M, int K, b
         return hipErrorNotSupported;
     // fp32 activations: one LDS maximum per staged (window, row)
     const bool wmax_fits = !std::is_same<TA, float>::value || MR * nwin <= kWmaxEntries;
-#if QMM_GEMV_STREAM
     if constexpr (F::kStream) {
         auto try_stream = [&](auto nsc) -> bool {
             constexpr int NS = decltype(nsc)::value;
@@ -1462,9 +1422,8 @@ hipError_t launch_fast(const void* A, const Seg* segs, int nseg, int M, int K, b
         int rows = 0;
         for (int j = 0; j < nseg; ++j) rows += segs[j].N;
         const bool lane_slots = MR == 1 && nwin == 1 && rows < 16384 && !folded;
-        if (!lane_slots && try_stream(std::integral_constant<int, QMM_GEMV_NS>{})) return e;
+        if (!lane_slots && try_stream(std::integral_constant<int, kGemvNS>{})) return e;
     }
-#endif
     if (res_lds <= di.max_lds && wmax_fits) {
         const void* kern = reinterpret_cast<const void*>(&gemv_resident_kernel<F, MR, YT, NW, TA, TC>);
         int occ = 0;
@@ -1496,7 +1455,6 @@ template <class F, int NW, typename TA, typename TC>
 hipError_t dispatch_rows(const void* A, const Seg* segs, int nseg, int M, int N, int K, bool a_vec,
                          const GemvFuse& fz, hipStream_t stream) {
     // Rows per wave item by the total row count (enough items to cover the 256 CUs several times).
-    constexpr int YB = QMM_GEMV_YT_BIG;
     if (fz.pair) {
         if (M != 1) return hipErrorNotSupported;
         return launch_fast<F, 1, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
@@ -1520,7 +1478,7 @@ hipError_t dispatch_rows(const void* A, const Seg* segs, int nseg, int M, int N,
         return launch_fast<F, 1, 1, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
     }
     if (M == 2) {
-        if (N >= 8192) return launch_fast<F, 2, YB, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
+        if (N >= 8192) return launch_fast<F, 2, 1, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
         if (N >= 2048) return launch_fast<F, 2, 2, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
         return launch_fast<F, 2, 1, NW, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
     }
@@ -1563,9 +1521,9 @@ hipError_t dispatch_fast(const void* A, const Seg* segs, int nseg, int M, int K,
         if (M == 1 && !fz.pair && fz.kind == 0 && fz.ea == nullptr && nwin == 1 && N >= 16384)
             return launch_fast<F, 1, 2, 4, TA, TC>(A, segs, nseg, M, K, a_vec, fz, stream);
     }
-    if (M <= QMM_GEMV_NW16_MAXM && res_lds > 40 * 1024)
+    if (M <= kGemvNW16MaxM && res_lds > 40 * 1024)
         return dispatch_rows<F, 16, TA, TC>(A, segs, nseg, M, N, K, a_vec, fz, stream);
-    return dispatch_rows<F, QMM_GEMV_NW, TA, TC>(A, segs, nseg, M, N, K, a_vec, fz, stream);
+    return dispatch_rows<F, kGemvNW, TA, TC>(A, segs, nseg, M, N, K, a_vec, fz, stream);
 }
 
 template <int T, typename TA, typename TC>
@@ -1585,11 +1543,27 @@ bool fast_weights(int t, const void* W) {
 
 template <typename TA, typename TC>
 hipError_t dispatch_types(int t, const void* A, const Seg* segs, int nseg, int M, int K, const GemvFuse& fz,
-                          hipStream_t stream) {
+                          hipStream_t stream, bool identity) {
     const bool a_ok = (reinterpret_cast<uintptr_t>(A) & (sizeof(TA) - 1)) == 0;
     const bool a_vec = (reinterpret_cast<uintptr_t>(A) & 15u) == 0;
     bool fast = a_ok && (t != QMM_TYPE_F16 || K % 16 == 0);
     for (int j = 0; j < nseg; ++j) fast = fast && fast_weights(t, segs[j].W);
+    // the matrix-core GEMV for M >= 2 (per row it is the same for every M), and for M = 1 when rows must
+    // match larger M bit for bit; the v_dot2 kernels are faster at M = 1
+    if (fast && gemv_mfma_type(t) && (M >= 2 || identity) && fz.kind == 0 && fz.ea == nullptr && fz.pair == 0) {
+        const void* W[kMaxSegs];
+        void* C[kMaxSegs];
+        int N[kMaxSegs];
+        for (int j = 0; j < nseg; ++j) {
+            W[j] = segs[j].W;
+            C[j] = segs[j].C;
+            N[j] = segs[j].N;
+        }
+        const int a_dt = std::is_same<TA, float>::value ? QMM_DTYPE_F32 : QMM_DTYPE_F16;
+        const int c_dt = std::is_same<TC, float>::value ? QMM_DTYPE_F32 : QMM_DTYPE_F16;
+        const hipError_t e = launch_gemv_mfma(t, A, a_dt, c_dt, M, K, W, C, N, nseg, stream);
+        if (e != hipErrorNotSupported) return e;
+    }
     if (!fast) {
         if (nseg != 1 || fz.kind != 0 || fz.ea != nullptr || fz.pair != 0) return hipErrorNotSupported;
         const void* W = segs[0].W;
@@ -1615,33 +1589,34 @@ hipError_t dispatch_types(int t, const void* A, const Seg* segs, int nseg, int M
 }
 
 hipError_t dispatch_dtypes(int t, const void* A, int a_dtype, int c_dtype, const Seg* segs, int nseg, int M, int K,
-                           hipStream_t stream, const GemvFuse& fz = GemvFuse{}) {
+                           hipStream_t stream, bool identity, const GemvFuse& fz = GemvFuse{}) {
     if (a_dtype == QMM_DTYPE_F32) {
         if (fz.kind != 0 || fz.ea != nullptr || fz.pair != 0) return hipErrorNotSupported;
-        if (c_dtype == QMM_DTYPE_F32) return dispatch_types<float, float>(t, A, segs, nseg, M, K, fz, stream);
-        return dispatch_types<float, __half>(t, A, segs, nseg, M, K, fz, stream);
+        if (c_dtype == QMM_DTYPE_F32) return dispatch_types<float, float>(t, A, segs, nseg, M, K, fz, stream, identity);
+        return dispatch_types<float, __half>(t, A, segs, nseg, M, K, fz, stream, identity);
     }
     if (c_dtype == QMM_DTYPE_F32) {
         if (fz.ea != nullptr || fz.pair != 0) return hipErrorNotSupported;
-        return dispatch_types<__half, float>(t, A, segs, nseg, M, K, fz, stream);
+        return dispatch_types<__half, float>(t, A, segs, nseg, M, K, fz, stream, identity);
     }
-    return dispatch_types<__half, __half>(t, A, segs, nseg, M, K, fz, stream);
+    return dispatch_types<__half, __half>(t, A, segs, nseg, M, K, fz, stream, identity);
 }
 
 }  // namespace
 
 hipError_t launch_gemv(int ggml_type, const void* A, int a_dtype, const void* W, void* C,
-                       int c_dtype, int M, int N, int K, hipStream_t stream) {
+                       int c_dtype, int M, int N, int K, hipStream_t stream, bool identity) {
     const Seg seg{W, C, N};
-    return dispatch_dtypes(ggml_type, A, a_dtype, c_dtype, &seg, 1, M, K, stream);
+    return dispatch_dtypes(ggml_type, A, a_dtype, c_dtype, &seg, 1, M, K, stream, identity);
 }
 
 hipError_t launch_gemv_fused(int ggml_type, const void* A, int a_dtype, int c_dtype, int M, int K,
-                             const void* const* W, void* const* C, const int* N, int count, hipStream_t stream) {
+                             const void* const* W, void* const* C, const int* N, int count, hipStream_t stream,
+                             bool identity) {
     if (count < 2 || count > kMaxSegs) return hipErrorNotSupported;
     Seg segs[kMaxSegs];
     for (int j = 0; j < count; ++j) segs[j] = Seg{W[j], C[j], N[j]};
-    return dispatch_dtypes(ggml_type, A, a_dtype, c_dtype, segs, count, M, K, stream);
+    return dispatch_dtypes(ggml_type, A, a_dtype, c_dtype, segs, count, M, K, stream, identity);
 }
 
 int gemv_max_fused() { return kMaxSegs; }
@@ -1655,7 +1630,7 @@ hipError_t launch_gemv_ex(int ggml_type, const void* A, int c_dtype, int M, int 
     if (fz.kind != 0 && (K % 16 != 0 || (align & 15u) != 0)) return hipErrorNotSupported;
     Seg segs[kMaxSegs];
     for (int j = 0; j < count; ++j) segs[j] = Seg{W[j], C[j], N[j]};
-    return dispatch_dtypes(ggml_type, A, QMM_DTYPE_F16, c_dtype, segs, count, M, K, stream, fz);
+    return dispatch_dtypes(ggml_type, A, QMM_DTYPE_F16, c_dtype, segs, count, M, K, stream, false, fz);
 }
 
 }  // namespace qmm

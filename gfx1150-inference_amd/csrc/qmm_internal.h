@@ -79,18 +79,29 @@ struct GemvFuse {
 };
 
 // Kernel launchers (validated arguments; return a hipError_t from the launch).
+// GEMV kernel families: M = 1 runs the v_dot2 kernels; 2 <= M < gemv_max_m() runs the matrix-core GEMV
+// where it is faster (Q4_K), else the v_dot2 kernels.  identity: every M on the family of M = 1's
+// choice for identity (the matrix-core GEMV for Q4_K), so that row m of any M is bit-identical to the
+// M = 1 call, the reference's invariant (tests/test_phase5_scale.py:274-310, 360-379).
 hipError_t launch_gemv(int ggml_type, const void* A, int a_dtype, const void* W, void* C,
-                       int c_dtype, int M, int N, int K, hipStream_t stream);
+                       int c_dtype, int M, int N, int K, hipStream_t stream, bool identity);
 // Several weight matrices (same type and K) times the same activations in one launch; returns
 // hipErrorNotSupported when the fused path does not apply (the caller then launches each).
 hipError_t launch_gemv_fused(int ggml_type, const void* A, int a_dtype, int c_dtype, int M, int K,
-                             const void* const* W, void* const* C, const int* N, int count, hipStream_t stream);
+                             const void* const* W, void* const* C, const int* N, int count, hipStream_t stream,
+                             bool identity);
 // GEMV of up to gemv_max_fused() matrices sharing fp16 activations A [M, K] (M < gemv_max_m()), with
 // work folded in (`fz`); hipErrorNotSupported when the shapes or alignments need a kernel without
 // the folding (the caller then runs the separate kernels).
 hipError_t launch_gemv_ex(int ggml_type, const void* A, int c_dtype, int M, int K, const void* const* W, void* const* C,
                           const int* N, int count, const GemvFuse& fz, hipStream_t stream);
 int gemv_max_fused();
+// Matrix-core GEMV (qmm_gemv_mfma.hip) for the GEMV family's M: Q4_K and Q6_K weights, `count` (1..4)
+// matrices sharing the activations; hipErrorNotSupported when the shape is outside it (then no row of
+// any M of that shape takes it, so rows stay bit-identical across M).
+bool gemv_mfma_type(int ggml_type);
+hipError_t launch_gemv_mfma(int ggml_type, const void* A, int a_dtype, int c_dtype, int M, int K, const void* const* W,
+                            void* const* C, const int* N, int count, hipStream_t stream);
 hipError_t launch_gemm_prefill(int ggml_type, const void* A, int a_dtype, const void* W, void* C,
                                int c_dtype, int M, int N, int K, hipStream_t stream);
 bool gemm_prefill_supported(int ggml_type, int a_dtype, int c_dtype, int M, int N, int K,

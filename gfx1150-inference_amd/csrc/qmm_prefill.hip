@@ -37,33 +37,18 @@
 
 #include "qmm_device.h"
 
-#ifndef QMM_PF_WIDE
-#define QMM_PF_WIDE 1
-#endif
-#ifndef QMM_PF_WIDE_VALU
-#define QMM_PF_WIDE_VALU 4  // VALU operations per MFMA round of the 256 x 256 tile's schedule
-#endif
-// The wide tile is used while its tiles cover at least 1 / QMM_PF_WIDE_MIN of the CUs (K is
-// split over workgroups below that).
-#ifndef QMM_PF_WIDE_MIN
-#define QMM_PF_WIDE_MIN 2
-#endif
-// Largest M that runs the 32-row tile (one 32-row tile per weight slice when M <= 32).
-#ifndef QMM_PF_SMALL_MAXM
-#define QMM_PF_SMALL_MAXM 32
-#endif
-#ifndef QMM_PF_LDS_EPILOGUE
-#define QMM_PF_LDS_EPILOGUE 1
-#endif
-#ifndef QMM_PF_VEC_STORE
-#define QMM_PF_VEC_STORE 1
-#endif
-#ifndef QMM_PF_SMALL_FILL
-#define QMM_PF_SMALL_FILL 1
-#endif
-
 namespace qmm {
 namespace {
+
+// VALU operations per MFMA round of the 256 x 256 tile's schedule.
+constexpr int kWideValu = 4;
+// The wide tile is used while its tiles cover at least 1 / kWideMin of the CUs (K is split over
+// workgroups below that).
+constexpr int kWideMin = 2;
+// Largest M that runs the 32-row tile (one 32-row tile per weight slice when M <= 32).
+constexpr int kSmallMaxM = 32;
+// Workgroups of the 32-row tile per CU that its grid is split to fill.
+constexpr int kSmallFill = 1;
 
 constexpr int kBM = 128;        // activation rows per workgroup tile
 constexpr int kBN = 256;        // weight rows per workgroup tile (32 per wave)
@@ -485,7 +470,7 @@ __device__ __forceinline__ void store_quad(TC* __restrict__ C, float* __restrict
                                            int ldc, int m, int n, const float (&vs)[4]) {
     if (ksplit > 1) {
         float* dst = part + (static_cast<size_t>(kz) * M + m) * N + n;
-        if (QMM_PF_VEC_STORE && n + 3 < N && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+        if (n + 3 < N && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
             *reinterpret_cast<float4*>(dst) = make_float4(vs[0], vs[1], vs[2], vs[3]);
             return;
         }
@@ -496,7 +481,7 @@ __device__ __forceinline__ void store_quad(TC* __restrict__ C, float* __restrict
     }
     TC* dst = C + static_cast<size_t>(m) * ldc + n;
     if constexpr (sizeof(TC) == 4) {
-        if (QMM_PF_VEC_STORE && n + 3 < N && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+        if (n + 3 < N && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
             *reinterpret_cast<float4*>(dst) = make_float4(vs[0], vs[1], vs[2], vs[3]);
             return;
         }
@@ -504,7 +489,7 @@ __device__ __forceinline__ void store_quad(TC* __restrict__ C, float* __restrict
         for (int e = 0; e < 4; ++e)
             if (n + e < N) reinterpret_cast<float*>(dst)[e] = vs[e];
     } else {
-        if (QMM_PF_VEC_STORE && n + 3 < N && (reinterpret_cast<uintptr_t>(dst) & 7u) == 0) {
+        if (n + 3 < N && (reinterpret_cast<uintptr_t>(dst) & 7u) == 0) {
             *reinterpret_cast<uint2*>(dst) = make_uint2(float_to_half_bits(vs[0]) | (float_to_half_bits(vs[1]) << 16),
                                                         float_to_half_bits(vs[2]) | (float_to_half_bits(vs[3]) << 16));
             return;
@@ -708,7 +693,6 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
         cur = nxt;
     }
 
-#if QMM_PF_LDS_EPILOGUE
     // Output tile through LDS (both activation stages: 256 x kH x BM bytes), so that every store
     // instruction writes whole row segments: fp16 rows of 512 bytes (fp16 C), or fp32 rows of
     // 1 KiB (fp32 C; with 256-k steps only, where they fit).  Without a K split only: the split's
@@ -780,7 +764,6 @@ void prefill_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, fl
         }
         return;
     }
-#endif
 
     // D element v of tile i: weight row n = n0 + 32wv + 8(v/4) + 4h + v%4, activation row
     // m = m0 + 32i + l32.
@@ -993,7 +976,7 @@ void prefill_wide_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> s
                     __builtin_memcpy(&bw, wf[B][nb], 16);
                     acc[nb][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bw, af[B][i], acc[nb][i], 0, 0, 0);
                 }
-            interleave_wide<QMM_PF_WIDE_VALU>();
+            interleave_wide<kWideValu>();
             __builtin_amdgcn_sched_barrier(0);
         };
         for_each_index(sub, std::make_integer_sequence<int, kQ>{});
@@ -1007,7 +990,6 @@ void prefill_wide_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> s
     }
     if (t < nsteps) step(std::integral_constant<int, 0>{}, t);
 
-#if QMM_PF_LDS_EPILOGUE
     if constexpr (sizeof(TC) == 2) {
         if (ksplit == 1) {
             // fp16 tile through LDS, so that every store instruction writes whole row segments:
@@ -1058,7 +1040,6 @@ void prefill_wide_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> s
             return;
         }
     }
-#endif
 
     // D element v of tile (nb, i): weight row n = n0 + 64wv + 32nb + 8(v/4) + 4h + v%4,
     // activation row m = m0 + 32i + l32.
@@ -1103,10 +1084,12 @@ __global__ __launch_bounds__(256) void to_f16_kernel(const TA* __restrict__ A, _
 }
 
 // fp32 activations [M, K] -> f16 [M, lda], one workgroup per row.  A row whose largest magnitude
-// lies outside the f16 range (at or above 65504, or in [2^-60, 2^-14)) is rounded as x * 2^-e with
-// e = exponent(max) - 14 (its maximum lands in [2^14, 2^15)), and rs[m] = 2^e multiplies the row's
-// outputs; both scalings are exact.  Other rows are rounded unchanged and rs[m] = 1.  Infinite or
-// NaN values keep e = 0 and propagate.
+// lies outside the f16 range (at or above 65504, or in [2^-126, 2^-14)) is rounded as x * 2^-e
+// with e = exponent(max) - 14 (its maximum lands in [2^14, 2^15)), and rs[m] = 2^e (a subnormal
+// fp32 number below 2^-126) multiplies the row's outputs: a product of the scaled row is the
+// original one times 2^-e, and both scalings are exact while their results are normal fp32
+// numbers.  Other rows are rounded unchanged and rs[m] = 1.  Infinite or NaN values keep e = 0
+// and propagate, and so does a row whose maximum is below 2^-126 (it rounds to zero in f16).
 __global__ __launch_bounds__(256) void to_f16_rows_kernel(const float* __restrict__ A, _Float16* __restrict__ out,
                                                           float* __restrict__ rs, int K, int lda) {
     __shared__ float red[4];
@@ -1153,10 +1136,9 @@ __global__ __launch_bounds__(256) void to_f16_rows_kernel(const float* __restric
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const uint32_t mb = __float_as_uint(mx);
     const bool big = mb >= 0x477FE000u && mb < 0x7F800000u;
-    const bool tiny = mb >= 0x21800000u && mb < 0x38800000u;
+    const bool tiny = mb >= 0x00800000u && mb < 0x38800000u;
     const int e = big || tiny ? static_cast<int>(mb >> 23) - 127 - 14 : 0;
-    const float down = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
-    if (tid == 0) rs[m] = __uint_as_float(static_cast<uint32_t>(127 + e) << 23);
+    if (tid == 0) rs[m] = __builtin_ldexpf(1.0f, e);
     if (cached) {
 #pragma unroll
         for (int i = 0; i < kU; ++i) {
@@ -1165,7 +1147,7 @@ __global__ __launch_bounds__(256) void to_f16_rows_kernel(const float* __restric
             const float x[8] = {va[i].x, va[i].y, va[i].z, va[i].w, vb[i].x, vb[i].y, vb[i].z, vb[i].w};
             _Float16 v[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = static_cast<_Float16>(x[j] * down);
+            for (int j = 0; j < 8; ++j) v[j] = static_cast<_Float16>(__builtin_ldexpf(x[j], -e));
             __builtin_memcpy(out + static_cast<size_t>(m) * lda + k, v, 16);
         }
         return;
@@ -1183,7 +1165,7 @@ __global__ __launch_bounds__(256) void to_f16_rows_kernel(const float* __restric
         }
         _Float16 v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = static_cast<_Float16>(x[j] * down);
+        for (int j = 0; j < 8; ++j) v[j] = static_cast<_Float16>(__builtin_ldexpf(x[j], -e));
         __builtin_memcpy(out + static_cast<size_t>(m) * lda + k, v, 16);
     }
 }
@@ -1329,16 +1311,11 @@ hipError_t cu_count(int& cus) {
 // CUs without splitting K (one workgroup per CU; a split costs a partial-sum pass).  Its element
 // offsets are 32-bit.
 bool use_wide(int M, int64_t wide_tiles_n, int K, int cus) {
-#if QMM_PF_WIDE
     const int64_t pad256 = (static_cast<int64_t>(M) + kWBM - 1) / kWBM * kWBM;
     const int64_t pad128 = (static_cast<int64_t>(M) + kBM - 1) / kBM * kBM;
     const int64_t lda = (static_cast<int64_t>(K) + kWBK - 1) / kWBK * kWBK;
     const int64_t tiles = (pad256 / kWBM) * wide_tiles_n;
-    return M >= kWBM && pad256 <= pad128 + 64 && QMM_PF_WIDE_MIN * tiles >= cus && static_cast<int64_t>(M) * lda < (int64_t{1} << 31);
-#else
-    (void)M, (void)wide_tiles_n, (void)K, (void)cus;
-    return false;
-#endif
+    return M >= kWBM && pad256 <= pad128 + 64 && kWideMin * tiles >= cus && static_cast<int64_t>(M) * lda < (int64_t{1} << 31);
 }
 
 struct PfSeg {
@@ -1460,8 +1437,8 @@ hipError_t launch_p(const void* A, const PfSeg* segs, int nseg, int M, int K, hi
         n_total += segs[i].N;
     }
     const int steps = (K + BK - 1) / BK;
-    // the small tile's workgroups fit QMM_PF_SMALL_FILL to a CU (its grid is split to fill them)
-    const PfPlan plan = plan_prefill(Sh::kWide, tiles_m, tiles_n, steps, BK, cus, Tile == kTileSmall ? QMM_PF_SMALL_FILL : 1);
+    // the small tile's grid is split to fill kSmallFill of its workgroups per CU
+    const PfPlan plan = plan_prefill(Sh::kWide, tiles_m, tiles_n, steps, BK, cus, Tile == kTileSmall ? kSmallFill : 1);
 
     // the tail launch's segments: rows from n-tile ns on, as column ranges of the callers' C
     PfSeg main_segs[kPfMaxSegs], tail_segs[kPfMaxSegs];
@@ -1532,7 +1509,7 @@ hipError_t launch_family(const void* A, const PfSeg* segs, int nseg, int M, int 
     int64_t wide_tiles_n = 0;
     for (int i = 0; i < nseg; ++i) wide_tiles_n += (segs[i].N + kWBN - 1) / kWBN;
     if (use_wide(M, wide_tiles_n, K, cus)) return launch_p<PF<kWH>, TA, TC, kTileWide>(A, segs, nseg, M, K, stream, ext);
-    if (M <= QMM_PF_SMALL_MAXM) return launch_p<PF<HN>, TA, TC, kTileSmall>(A, segs, nseg, M, K, stream, ext);
+    if (M <= kSmallMaxM) return launch_p<PF<HN>, TA, TC, kTileSmall>(A, segs, nseg, M, K, stream, ext);
     return launch_p<PF<HN>, TA, TC, kTileStd>(A, segs, nseg, M, K, stream, ext);
 }
 
@@ -1587,37 +1564,48 @@ int prefill_max_fused() { return kPfMaxSegs; }
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 namespace {
-std::mutex g_scratch_mutex;
-std::unordered_map<int, void*> g_scratch_ptr;
-
-hipError_t scratch_address(void** out) {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return e;
-    std::lock_guard<std::mutex> lock(g_scratch_mutex);
-    auto it = g_scratch_ptr.find(dev);
-    if (it != g_scratch_ptr.end()) {
-        *out = it->second;
-        return hipSuccess;
-    }
+// Per device: the scratch address, and an event recorded after the last eager call that used the
+// scratch, with that call's stream.  An eager call on another stream waits for the event first, so
+// calls on different streams take turns on the array instead of racing.  Calls under stream
+// capture neither wait nor record (the caller orders graph replays against other work).
+struct ScratchDev {
     void* ptr = nullptr;
-    if ((e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch))) != hipSuccess) return e;
-    if (ptr == nullptr) return hipErrorInvalidSymbol;
-    g_scratch_ptr.emplace(dev, ptr);
-    *out = ptr;
-    return hipSuccess;
-}
+    hipEvent_t done = nullptr;
+    hipStream_t last = nullptr;
+    bool pending = false;
+};
+std::mutex g_scratch_mutex;
+std::unordered_map<int, ScratchDev> g_scratch;
 }  // namespace
 
 hipError_t launch_gemm_prefill_noalloc(int ggml_type, const void* A, int a_dtype, const void* W, void* C, int c_dtype,
                                        int M, int N, int K, hipStream_t stream, size_t* need) {
     *need = 0;
-    PfWs ext{nullptr, kNoAllocScratchBytes, 0};
-    hipError_t e = scratch_address(&ext.buf);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);  // held through the launches: calls take turns
+    ScratchDev& sd = g_scratch[dev];
+    if (sd.ptr == nullptr) {
+        void* ptr = nullptr;
+        if ((e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch))) != hipSuccess) return e;
+        if (ptr == nullptr) return hipErrorInvalidSymbol;
+        if ((e = hipEventCreateWithFlags(&sd.done, hipEventDisableTiming)) != hipSuccess) return e;
+        sd.ptr = ptr;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if ((e = hipStreamIsCapturing(stream, &cs)) != hipSuccess) return e;
+    const bool eager = cs == hipStreamCaptureStatusNone;
+    if (eager && sd.pending && stream != sd.last && (e = hipStreamWaitEvent(stream, sd.done, 0)) != hipSuccess) return e;
+    PfWs ext{sd.ptr, kNoAllocScratchBytes, 0};
     const PfSeg seg{W, C, N, N};
     e = dispatch_dtypes(ggml_type, A, a_dtype, c_dtype, &seg, 1, M, K, stream, &ext);
     *need = ext.need;
+    if (e == hipSuccess && eager && ext.need > 0) {
+        if ((e = hipEventRecord(sd.done, stream)) != hipSuccess) return e;
+        sd.last = stream;
+        sd.pending = true;
+    }
     return e;
 }
 

@@ -98,6 +98,9 @@ _SIGNATURES = {
     "qmm_version": (_i, []),
     "qmm_gemv_max_m": (_i, []),
     "qmm_set_gemv_max_m": (_i, [_i]),
+    "qmm_set_thread_gemv_max_m": (_i, [_i]),
+    "qmm_set_row_identity": (_i, [_i]),
+    "qmm_row_identity": (_i, []),
     "qmm_weight_bytes": (ctypes.c_size_t, [_i, _i64, _i64]),
     "qmm_gemm": (_i, [_i, _vp, _i, _vp, _vp, _i, _i, _i, _i, _vp]),
     "qmm_gemm_noalloc": (_i, [_i, _vp, _i, _vp, _vp, _i, _i, _i, _i, _vp]),
@@ -177,9 +180,42 @@ def gemv_max_m() -> int:
 
 
 def set_gemv_max_m(m: int) -> None:
-    """Moves the GEMV / prefill threshold: M < m runs the GEMV family (rows bit-identical to the
-    M = 1 call); the default is 17."""
+    """Moves the GEMV / prefill threshold for the process: M < m runs the GEMV kernels; the
+    default is 17."""
     check(_lib.qmm_set_gemv_max_m(int(m)))
+
+
+def set_thread_gemv_max_m(m: int) -> None:
+    """The calling thread's GEMV / prefill threshold (0: the process value again)."""
+    check(_lib.qmm_set_thread_gemv_max_m(int(m)))
+
+
+def row_identity() -> bool:
+    return bool(_lib.qmm_row_identity())
+
+
+def set_row_identity(on: bool) -> None:
+    """Calling thread's row-identity mode: when on, every GEMV-size M runs the kernels of M >= 2,
+    so that row m of any M < gemv_max_m() is bit-identical to the M = 1 call (the reference's
+    invariant); when off (the default), Q4_K's M = 1 takes the faster v_dot2 GEMV."""
+    check(_lib.qmm_set_row_identity(1 if on else 0))
+
+
+class row_identity_mode:
+    """Context manager: row-identity mode on (or off) for the calling thread, restored on exit."""
+
+    def __init__(self, on: bool = True):
+        self._on = bool(on)
+        self._prev = False
+
+    def __enter__(self):
+        self._prev = row_identity()
+        set_row_identity(self._on)
+        return self
+
+    def __exit__(self, *exc):
+        set_row_identity(self._prev)
+        return False
 
 
 def _torch():

@@ -63,9 +63,14 @@ size_t qmm_weight_bytes(int ggml_type, int64_t n, int64_t k);
  * --------------------------------------------------------------------------------- */
 
 /* C[M,N] (c_dtype) = A[M,K] (a_dtype) @ dequant(W)[N,K]^T with fp32 accumulation.
- * M < qmm_gemv_max_m() (17) runs the bandwidth-bound GEMV family, whose row m result is
- * bit-identical for every such M; larger M runs the f16-MFMA prefill GEMM (a 32-row tile up
- * to M = 32), whose rows agree with the M = 1 call within the prefill accuracy bound.
+ * M < qmm_gemv_max_m() (17) runs the bandwidth-bound GEMV kernels; larger M runs the f16-MFMA
+ * prefill GEMM (a 32-row tile up to M = 32), whose rows agree with the M = 1 call within the
+ * prefill accuracy bound.  Among GEMV sizes, Q4_K takes a matrix-core GEMV for M >= 2 and the
+ * v_dot2 GEMV at M = 1 (the faster at each size): rows of every M in [2, gemv_max_m()) are
+ * bit-identical to one another, and agree with M = 1 within the accuracy bound of either.  With
+ * qmm_set_row_identity(1) M = 1 runs the matrix-core GEMV too, so that every GEMV-size row is
+ * bit-identical to the M = 1 call, as in the reference.  The other formats run one GEMV family
+ * for every M (bit-identical rows in both modes).
  * Generalises launch_matmul_q{4_0,8_0,4_k,6_k}_device (reference
  * src/kernels/dequantize.h:98-132, dispatch at dequantize.hip:778/896/1014/1132). */
 int qmm_gemm(int ggml_type, const void* A, int a_dtype, const void* W, void* C, int c_dtype,
@@ -76,8 +81,11 @@ int qmm_gemm(int ggml_type, const void* A, int a_dtype, const void* W, void* C, 
  * Same arguments, kernels and results as qmm_gemm.  The prefill sizes' workspace (f16 copy of
  * fp32 or unaligned activations, split-K partial tiles) is a static per-device scratch array of
  * qmm_noalloc_scratch_bytes() bytes, held by every GPU the library runs on until the process
- * ends; a call needing more returns QMM_ERR_OUT_OF_RANGE and launches nothing.  All calls on one
- * GPU share that array: calls that overlap on one GPU (other streams, other threads) race. */
+ * ends; a call needing more returns QMM_ERR_UNSUPPORTED and launches nothing.  All calls on one
+ * GPU share that array.  Eager calls take turns on it: a call on another stream than the previous
+ * one that used the array waits for that call's kernels (hipStreamWaitEvent on a per-device event
+ * created by the first call).  Calls under stream capture are not ordered that way: replays of a
+ * captured call that overlap other calls on the same GPU race, and the caller orders them. */
 int qmm_gemm_noalloc(int ggml_type, const void* A, int a_dtype, const void* W, void* C, int c_dtype,
                      int M, int N, int K, void* stream);
 size_t qmm_noalloc_scratch_bytes(void);
@@ -138,6 +146,22 @@ int qmm_gemv_max_m(void);
  * read the threshold once (a qmm_gemm_batch call for all its descriptors); changing it while
  * other threads issue calls changes which family their later calls take. */
 int qmm_set_gemv_max_m(int m);
+
+/* Per-thread threshold for calls issued by the calling thread (1 <= m <= 65536), or 0 to use the
+ * process value again; QMM_ERR_INVALID_ARGUMENT otherwise.  No counterpart in the reference: lets
+ * one caller keep bit-identical rows beyond M = 16 without moving the threshold for every other
+ * caller.  qmm_gemv_max_m() reports the calling thread's effective threshold. */
+int qmm_set_thread_gemv_max_m(int m);
+
+/* Row-identity mode of the calling thread (0 or 1; QMM_ERR_INVALID_ARGUMENT otherwise); 0 by
+ * default.  No counterpart in the reference, whose kernels keep every row of every GEMV-size M
+ * bit-identical to the M = 1 call (its tests assert it, tests/test_phase5_scale.py:274-310).
+ * With 1, qmm_gemm, qmm_gemm_noalloc and qmm_gemm_batch run every M < qmm_gemv_max_m() on the
+ * kernel family of M >= 2, so that rows match the M = 1 call bit for bit (Q4_K's M = 1 then runs
+ * the matrix-core GEMV, a few microseconds slower than the v_dot2 GEMV on large matrices).  The
+ * reference-API launchers (qmm_matmul_q*_device / _host) always run in this mode. */
+int qmm_set_row_identity(int on);
+int qmm_row_identity(void);
 
 /* Per-type device launchers with the reference's argument meaning: fp16 A [M,K],
  * packed B [N,K], fp16 C [M,N], all device pointers, on `stream`.

@@ -52,6 +52,41 @@ def test_gemv_threshold_setting():
     assert qmm.gemv_max_m() == before
 
 
+def test_thread_threshold_and_row_identity_settings():
+    """qmm_set_thread_gemv_max_m overrides the threshold for the calling thread (0 restores the
+    process value); qmm_set_row_identity takes 0 or 1; both reject other values unchanged and
+    leave other threads alone (host logic only, no kernel runs)."""
+    import threading
+    base = qmm.gemv_max_m()
+    assert not qmm.row_identity()
+    try:
+        qmm.set_thread_gemv_max_m(300)
+        qmm.set_row_identity(True)
+        for bad in (-1, 65537):
+            with pytest.raises(ValueError, match="qmm_set_thread_gemv_max_m"):
+                qmm.set_thread_gemv_max_m(bad)
+        with pytest.raises(ValueError, match="qmm_set_row_identity"):
+            qmm.check(qmm.lib().qmm_set_row_identity(2))
+        assert qmm.gemv_max_m() == 300 and qmm.row_identity()
+        seen = []
+        th = threading.Thread(target=lambda: seen.append((qmm.gemv_max_m(), qmm.row_identity())))
+        th.start()
+        th.join()
+        assert seen == [(base, False)]
+        qmm.set_gemv_max_m(40)  # the process value moves; this thread keeps its own
+        assert qmm.gemv_max_m() == 300
+        qmm.set_thread_gemv_max_m(0)
+        assert qmm.gemv_max_m() == 40
+    finally:
+        qmm.set_thread_gemv_max_m(0)
+        qmm.set_row_identity(False)
+        qmm.set_gemv_max_m(base)
+    assert qmm.gemv_max_m() == base and not qmm.row_identity()
+    with qmm.row_identity_mode():
+        assert qmm.row_identity()
+    assert not qmm.row_identity()
+
+
 @pytest.mark.parametrize("t,n,k,expected", [
     (qmm.GGML_Q4_0, 4096, 4096, 9_437_184),
     (qmm.GGML_Q8_0, 4096, 4096, 17_825_792),

@@ -6,8 +6,9 @@ Bars (tolerances are written into each check):
 * GEMV (M < qmm_gemv_max_m): max_i|y_i - y64_i| / max_i|y64_i| <= 1e-3 against fp64 on the
   exact weights, and the reference tests' own absolute tolerances against the reference
   formula (fp16-rounded weights, fp32 matmul);
-* row results bit-identical for every M in the GEMV range (the reference's invariant,
-  tests/test_phase5_scale.py:274-310, 371-379);
+* row results bit-identical for every M in the GEMV range in row-identity mode (the
+  reference's invariant, tests/test_phase5_scale.py:274-310, 371-379), and for every M >= 2 in
+  the default mode (Q4_K's M = 1 then runs the v_dot2 GEMV, within the GEMV bar);
 * full 8B / 70B shapes: sampled rows against fp64, linearity in x.
 """
 
@@ -193,7 +194,7 @@ GEMV_SHAPES = {
     O.GGML_Q4_0: [(512, 4096), (300, 2304), (64, 256), (257, 14336)],
     O.GGML_Q8_0: [(512, 4096), (300, 2304), (64, 256), (257, 14336)],
     O.GGML_Q4_K: [(512, 4096), (300, 2304), (96, 256)],
-    O.GGML_Q6_K: [(512, 4096), (257, 6144), (96, 512)],          # 512: fallback (K % 2048 != 0)
+    O.GGML_Q6_K: [(512, 4096), (257, 6144), (96, 512)],
 }
 
 
@@ -227,15 +228,61 @@ def test_gemv_dtypes(dev, t, a_dtype, c_dtype):
 def test_gemv_rows_bit_identical_across_m(dev, t):
     import qmm
     rng = np.random.default_rng(601 + t)
-    for N, K in GEMV_SHAPES[t][:2] + GEMV_SHAPES[t][-1:]:
+    with qmm.row_identity_mode():
+        for N, K in GEMV_SHAPES[t][:2] + GEMV_SHAPES[t][-1:]:
+            raw = O.synth_weights(t, N, K, rng)
+            Mmax = min(qmm.gemv_max_m() - 1, 31)
+            x = rng.standard_normal((Mmax, K)).astype(np.float32)
+            single = np.stack([gemm(t, x[m:m + 1], raw, N, K, dev)[0] for m in range(Mmax)])
+            # 4-row blocks (M % 8 in 1..4) and 8-row blocks (M % 8 == 0 or >= 5) of the v_dot2
+            # kernels; one 16-row pass of the matrix-core GEMV
+            for M in sorted({2, 3, 4, 5, 7, 8, 9, 12, 13, 16, Mmax}):
+                y = gemm(t, x[:M], raw, N, K, dev)
+                np.testing.assert_array_equal(y, single[:M], err_msg=f"{O.TYPE_NAMES[t]} M={M} N={N} K={K}")
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_default_mode_rows_bit_identical_for_m_from_2(dev, t):
+    """Default mode: every M >= 2 of the GEMV range gives each row bit for bit the same result
+    (Q4_K: the matrix-core GEMV); M = 1 (Q4_K: the v_dot2 GEMV) agrees with them within the GEMV
+    bar, and is bit-identical to them for the formats that run one family."""
+    import qmm
+    assert not qmm.row_identity()
+    rng = np.random.default_rng(651 + t)
+    for N, K in GEMV_SHAPES[t][:2]:
         raw = O.synth_weights(t, N, K, rng)
-        Mmax = min(qmm.gemv_max_m() - 1, 31)
-        x = rng.standard_normal((Mmax, K)).astype(np.float32)
-        single = np.stack([gemm(t, x[m:m + 1], raw, N, K, dev)[0] for m in range(Mmax)])
-        # 4-row blocks (M % 8 in 1..4) and 8-row blocks (M % 8 == 0 or >= 5)
-        for M in sorted({2, 3, 4, 5, 7, 8, 9, 12, 13, 16, Mmax}):
-            y = gemm(t, x[:M], raw, N, K, dev)
-            np.testing.assert_array_equal(y, single[:M], err_msg=f"{O.TYPE_NAMES[t]} M={M} N={N} K={K}")
+        x = rng.standard_normal((16, K)).astype(np.float32)
+        y16 = gemm(t, x, raw, N, K, dev)
+        for M in (2, 3, 5, 8, 13):
+            np.testing.assert_array_equal(gemm(t, x[:M], raw, N, K, dev), y16[:M],
+                                          err_msg=f"{O.TYPE_NAMES[t]} M={M} N={N} K={K}")
+        y1 = np.stack([gemm(t, x[m:m + 1], raw, N, K, dev)[0] for m in range(16)])
+        y64 = O.matmul_f64(t, x, raw, N, K)
+        assert O.max_rel_err(y1, y64) <= GEMV_TOL and O.max_rel_err(y16, y64) <= GEMV_TOL
+        if t != O.GGML_Q4_K:
+            np.testing.assert_array_equal(y1, y16, err_msg=f"{O.TYPE_NAMES[t]} N={N} K={K}")
+
+
+def test_row_identity_and_thread_threshold_are_per_thread(dev):
+    """qmm_set_row_identity and qmm_set_thread_gemv_max_m change the calling thread only."""
+    import threading
+    import qmm
+    base = qmm.gemv_max_m()
+    seen = {}
+
+    def other():
+        seen["identity"], seen["gmax"] = qmm.row_identity(), qmm.gemv_max_m()
+    with qmm.row_identity_mode():
+        qmm.set_thread_gemv_max_m(200)
+        try:
+            assert qmm.row_identity() and qmm.gemv_max_m() == 200
+            th = threading.Thread(target=other)
+            th.start()
+            th.join()
+        finally:
+            qmm.set_thread_gemv_max_m(0)
+    assert seen == {"identity": False, "gmax": base}
+    assert not qmm.row_identity() and qmm.gemv_max_m() == base
 
 
 @pytest.mark.parametrize("t", TYPES)
@@ -249,15 +296,24 @@ def test_raised_threshold_keeps_every_m_bit_identical(dev, t):
     N, K = 96, 4096
     raw = O.synth_weights(t, N, K, rng)
     x = rng.standard_normal((100, K)).astype(np.float32)
-    single = np.stack([gemm(t, x[m:m + 1], raw, N, K, dev)[0] for m in range(100)])
     before = qmm.gemv_max_m()
     try:
         qmm.set_gemv_max_m(4096)
-        for M in (40, 100):
-            np.testing.assert_array_equal(gemm(t, x[:M], raw, N, K, dev), single[:M],
-                                          err_msg=f"{O.TYPE_NAMES[t]} M={M}")
+        with qmm.row_identity_mode():
+            single = np.stack([gemm(t, x[m:m + 1], raw, N, K, dev)[0] for m in range(100)])
+            for M in (40, 100):
+                np.testing.assert_array_equal(gemm(t, x[:M], raw, N, K, dev), single[:M],
+                                              err_msg=f"{O.TYPE_NAMES[t]} M={M}")
     finally:
         qmm.set_gemv_max_m(before)
+    # the same through the calling thread's own threshold, the process value untouched
+    qmm.set_thread_gemv_max_m(4096)
+    try:
+        with qmm.row_identity_mode():
+            np.testing.assert_array_equal(gemm(t, x[:40], raw, N, K, dev), single[:40])
+    finally:
+        qmm.set_thread_gemv_max_m(0)
+    assert qmm.gemv_max_m() == before
     y = gemm(t, x[:40], raw, N, K, dev)
     assert O.max_rel_err(y, single[:40]) <= 1e-2
 
@@ -278,10 +334,11 @@ def test_gemv_rows_bit_identical_across_m_windowed_f16_io(dev, t):
         C = qmm.gemm(t, torch.from_numpy(np.ascontiguousarray(a)).to(dev), W, N, K, out_dtype=torch.float16)
         torch.cuda.synchronize()
         return C.cpu().numpy()
-    single = np.concatenate([run(x[m:m + 1]) for m in range(16)])
-    for M in (5, 8, 13, 16):
-        np.testing.assert_array_equal(run(x[:M]).view(np.uint16), single[:M].view(np.uint16),
-                                      err_msg=f"{O.TYPE_NAMES[t]} M={M}")
+    with qmm.row_identity_mode():
+        single = np.concatenate([run(x[m:m + 1]) for m in range(16)])
+        for M in (5, 8, 13, 16):
+            np.testing.assert_array_equal(run(x[:M]).view(np.uint16), single[:M].view(np.uint16),
+                                          err_msg=f"{O.TYPE_NAMES[t]} M={M}")
 
 
 @pytest.mark.parametrize("t", TYPES)
@@ -302,9 +359,11 @@ def test_gemv_rows_bit_identical_across_m_long_k(dev, t):
             C = qmm.gemm(t, torch.from_numpy(np.ascontiguousarray(a)).to(dev), W, N, K, out_dtype=torch.float32)
             torch.cuda.synchronize()
             return C.cpu().numpy()
-        single = np.concatenate([run(x[m:m + 1]) for m in range(8)])
-        for M in (2, 3, 4, 5, 8):
-            np.testing.assert_array_equal(run(x[:M]), single[:M], err_msg=f"{O.TYPE_NAMES[t]} M={M} {dt.__name__}")
+        with qmm.row_identity_mode():
+            single = np.concatenate([run(x[m:m + 1]) for m in range(8)])
+            for M in (2, 3, 4, 5, 8):
+                np.testing.assert_array_equal(run(x[:M]), single[:M],
+                                              err_msg=f"{O.TYPE_NAMES[t]} M={M} {dt.__name__}")
 
 
 @pytest.mark.parametrize("t", TYPES)
