@@ -1548,9 +1548,8 @@ hipError_t dispatch_types(int t, const void* A, const Seg* segs, int nseg, int M
     const bool a_vec = (reinterpret_cast<uintptr_t>(A) & 15u) == 0;
     bool fast = a_ok && (t != QMM_TYPE_F16 || K % 16 == 0);
     for (int j = 0; j < nseg; ++j) fast = fast && fast_weights(t, segs[j].W);
-    // the matrix-core GEMV for M >= 2 (per row it is the same for every M), and for M = 1 when rows must
-    // match larger M bit for bit; the v_dot2 kernels are faster at M = 1
-    if (fast && gemv_mfma_type(t) && (M >= 2 || identity) && fz.kind == 0 && fz.ea == nullptr && fz.pair == 0) {
+    // the matrix-core GEMV from the format's smallest M (its rows are the same for every M it serves)
+    if (fast && M >= gemv_mfma_min_m(t, identity) && fz.kind == 0 && fz.ea == nullptr && fz.pair == 0) {
         const void* W[kMaxSegs];
         void* C[kMaxSegs];
         int N[kMaxSegs];

@@ -25,12 +25,15 @@
 //     instruction sequence whatever M, the row group's place and the grid; MFMA rows are
 //     independent, so row m of any M is bit-identical to the M = 1 call (the reference's
 //     prefill-vs-M=1 invariant, tests/test_phase5_scale.py:274-310).
-//   * Activations (16 rows per pass) are staged once per workgroup into LDS in natural k order
-//     (8-k pieces with the pair order of the decoded codes), fp32 rounded to f16 with a power-of-two
-//     rescale of any (row, 4096-k window) outside f16's range.
-//   * Weights stream through an LDS ring of NB (3 or 4) chunks of 16 rows x 8 super-blocks, copied
-//     by the whole workgroup with direct global -> LDS 16-byte loads (each instruction reads whole
-//     row segments); NB - 1 chunks are in flight while one is multiplied, across row groups.
+//   * Weights stream through an LDS ring of NB (3 or 4) chunks of 16 rows x 8 super-blocks (a window of
+//     K), copied by the whole workgroup with direct global -> LDS 16-byte loads (each instruction reads
+//     whole row segments); NB - 1 chunks are in flight while one is multiplied.
+//   * Windows are the outer loop over a batch of up to 4 row groups: a wave holds the activation
+//     operands of its super-block of the window in registers (up to 16 rows per pass) and applies them
+//     to every row group of the batch, whose accumulators stay in registers.  fp16 activations reach
+//     registers through a per-wave LDS area filled by the same direct loads one window ahead; fp32
+//     activations are loaded directly and rounded to f16, with a power-of-two rescale of any
+//     (row, super-block) outside f16's range.  The work of a pass hardly depends on its row count.
 #include <climits>
 #include <mutex>
 #include <string>
@@ -50,10 +53,7 @@ typedef float mf4 __attribute__((ext_vector_type(4)));
 constexpr int kSlots = 8;       // waves per workgroup = K slots of a row group
 constexpr int kRows = 16;       // weight rows per row group
 constexpr int kMRows = 16;      // activation rows per pass
-constexpr int kWinK = 4096;     // fp32 rescale window
-constexpr int kMaxWin = 16;     // K <= 65536 for fp32 activations
 
-constexpr size_t kStaticLds = 2 * kMRows * kMaxWin * 4;  // the kernels' static LDS at most (fp32 window maxima)
 
 __device__ __forceinline__ uint32_t mkeep(uint32_t v) {
     __asm__("" : "+v"(v));
@@ -249,151 +249,131 @@ struct MQ6K {
 };
 
 // ------------------------------------------------------------------------------------------------
-// LDS of a workgroup (dynamic), per staged activation row m (row stride rs bytes, rs % 128 = 16 or 80
-// so that the rows' fragments spread over the banks):
-//   [0, 2K)            activations, natural k order, each 8-k piece in pair order (0,2,1,3,4,6,5,7)
-//   [2K, 2K + 64 nsb)  per (super-block, quarter) 8 halves: group sums / 32 as f16 hi and lo
-// then the slot partials: 2 buffers x 8 waves x 64 lanes x 16 bytes.
+// LDS of a workgroup (dynamic):
+//   ring  NB weight chunks of Chunk<F>::kBytes;
+//   act   fp16 activations only: per wave, the pass's rows of the wave's super-block of the current
+//         window, lrows rows x kActRP 16-byte pieces (the 512 bytes of a row, then one padding piece,
+//         so that consecutive rows start 4 banks apart);
+//   red   slot partials of a batch: kBG row groups x 8 waves x 16 qa lanes x 16 bytes.
 // ------------------------------------------------------------------------------------------------
 extern __shared__ __attribute__((aligned(16))) uint8_t mlds[];
 
-template <class F>
-__host__ __device__ constexpr int row_stride(int K) { return 2 * K + (F::kSums ? 64 * (K / 256) : 0) + 16; }
-// slot partials of a pass of `lrows` activation rows: 2 buffers x 8 waves x 16 lanes per quarter
-__host__ __device__ constexpr int red_bytes(int lrows) { return 2 * kSlots * 16 * ((lrows + 3) / 4) * 16; }
+constexpr int kBG = 4;     // row groups per batch: their accumulators stay in registers across the windows
+constexpr int kActP = 32;  // 16-byte pieces of one super-block of one fp16 activation row
+constexpr int kActRP = 33;
+
+__host__ __device__ constexpr int act_bytes(int lrows) { return kSlots * lrows * kActRP * 16; }
+__host__ __device__ constexpr int red_bytes(int lrows) { return kBG * kSlots * 16 * ((lrows + 3) / 4) * 16; }
 
 __device__ __forceinline__ int win_exp(uint32_t maxbits) {
-    // (row, window) maximum at or above 65504, or in [2^-126, 2^-14): scale by 2^-e with
+    // (row, super-block) maximum at or above 65504, or in [2^-126, 2^-14): scale by 2^-e with
     // e = exponent(max) - 14 (brings the maximum into [2^14, 2^15))
     const bool big = maxbits >= 0x477FE000u && maxbits < 0x7F800000u;
     const bool tiny = maxbits >= 0x00800000u && maxbits < 0x38800000u;
     return big || tiny ? static_cast<int>(maxbits >> 23) - 127 - 14 : 0;
 }
 
-template <typename TA>
-__device__ __forceinline__ void load_group(const TA* p, bool vec, float x[16]);
-template <>
-__device__ __forceinline__ void load_group<float>(const float* p, bool vec, float x[16]) {
-    if (vec) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float4 v = reinterpret_cast<const float4*>(p)[i];
-            x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) x[i] = p[i];
-    }
-}
-template <>
-__device__ __forceinline__ void load_group<__half>(const __half* p, bool vec, float x[16]) {
-    _Float16 h[16];
-    if (vec) {
-        __builtin_memcpy(h, p, 32);
-    } else {
-        const uint16_t* s = reinterpret_cast<const uint16_t*>(p);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const uint16_t b = s[i];
-            __builtin_memcpy(&h[i], &b, 2);
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = static_cast<float>(h[i]);
+// Activation operands of one super-block for lane (n, c): the A operand of each MFMA step (8 k in the
+// pair order of the decoded codes) and, for formats with group sums, the sums operand.
+struct AOps {
+    mh8 a[8];
+    mh8 s;
+};
+
+// (x0, x1, .., x7) -> (x0, x2, x1, x3, x4, x6, x5, x7)
+__device__ __forceinline__ mh8 pair_order(mu4 v) {
+    mu4 r;
+    r.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);
+    r.y = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);
+    r.z = __builtin_amdgcn_perm(v.w, v.z, 0x05040100u);
+    r.w = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);
+    mh8 h;
+    __builtin_memcpy(&h, &r, 16);
+    return h;
 }
 
-// Stages activation rows m0 .. m0 + mr - 1 into LDS, 16 k per item (fp32: after the (row, window)
-// maxima are known; `wexp` holds e per (row, window)).
-// Writes staging item `it` (16 consecutive activations x of one row, rows staged as in stage_rows).
-template <class F, typename TA>
-__device__ __forceinline__ void stage_item(int it, int per_row, int K, int rs, bool ok, const float (&x)[16], const int* wexp) {
-    {
-        const int m = it / per_row, k = 16 * (it - m * per_row);
-        const int e = std::is_same<TA, float>::value ? wexp[m * kMaxWin + k / kWinK] : 0;
-        _Float16 h[16];
+// Group sums of the 8 fragments (Q4_K: steps 0..3 and 4..7 are the lane's two 32-k groups), summed in a
+// fixed order and held as f16 hi + lo * 2^-11 of sum / 32 (exact power-of-two scalings; the remainder
+// scaled by 2^11 stays a normal f16, and the B operand's halves carry the 2^-11).
+template <class F>
+__device__ __forceinline__ void group_sums(AOps& ao) {
+    if constexpr (F::kSums) {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const h2 one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+        _Float16 hi[2], lo[2];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float v = ok ? x[i] : 0.0f;
-            h[i] = static_cast<_Float16>(std::is_same<TA, float>::value ? __builtin_ldexpf(v, -e) : v);
-        }
-        uint8_t* row = mlds + m * rs;
+        for (int g = 0; g < 2; ++g) {
+            float s = 0.0f;
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const mh8 v{h[8 * q], h[8 * q + 2], h[8 * q + 1], h[8 * q + 3], h[8 * q + 4], h[8 * q + 6], h[8 * q + 5],
-                        h[8 * q + 7]};
-            *reinterpret_cast<mh8*>(row + 2 * (k + 8 * q)) = v;
-        }
-        if constexpr (!F::kSums) return;
-        // group sums in a fixed order, stored as f16 hi + lo of sum / 32 (exact power-of-two scaling;
-        // |sum / 32| stays inside f16's range)
-        float s = 0.0f;
+            for (int t = 4 * g; t < 4 * g + 4; ++t) {
+                const mh8 v = ao.a[t];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) s += static_cast<float>(h[i]);
-        bool store = true;
-        int j = (k & 255) >> 4;
-        if constexpr (F::kGroupK == 32) {
-            // a 32-k group is two items of adjacent lanes (items come in pairs: per_row and the
-            // stride are even); the first half's lane adds the second's sum
-            const float o = __shfl_xor(s, 1, 64);
-            store = (it & 1) == 0;
-            s = s + o;
-            j >>= 1;
-        }
-        if (store) {
-            const int sb = k >> 8;
-            const float v = s * 0.03125f;
-            const _Float16 hi = static_cast<_Float16>(v);
-            // the remainder scaled by 2^11 stays a normal f16 (its B halves carry the 2^-11)
-            const _Float16 lo = static_cast<_Float16>((v - static_cast<float>(hi)) * 2048.0f);
-            _Float16* f = reinterpret_cast<_Float16*>(row + 2 * K + 64 * sb + 16 * F::gq(j));
-            f[F::hpos(j)] = hi;
-            f[F::lpos(j)] = lo;
-            if constexpr (F::kGroupK == 32) {
-                if ((j & 1) == 0) {  // halves 4..7 of the quarter's fragment are unused: zero
-                    f[4] = static_cast<_Float16>(0.0f);
-                    f[5] = static_cast<_Float16>(0.0f);
-                    f[6] = static_cast<_Float16>(0.0f);
-                    f[7] = static_cast<_Float16>(0.0f);
-                }
+                for (int i = 0; i < 4; ++i) s = __builtin_amdgcn_fdot2(h2{v[2 * i], v[2 * i + 1]}, one, s, false);
             }
+            const float x = s * 0.03125f;
+            hi[g] = static_cast<_Float16>(x);
+            lo[g] = static_cast<_Float16>((x - static_cast<float>(hi[g])) * 2048.0f);
+        }
+        const _Float16 z = static_cast<_Float16>(0.0f);
+        ao.s = mh8{hi[0], hi[1], lo[0], lo[1], z, z, z, z};
+    }
+}
+
+// fp16 activations of the current window from this wave's LDS area (row n of the pass; lanes of rows
+// past the pass read row 0: their MFMA output rows are never stored, and MFMA rows are independent).
+template <class F>
+__device__ __forceinline__ void read_act(const uint8_t* wact, int n, int c, int mr, AOps& ao) {
+    const uint8_t* row = wact + (n < mr ? n : 0) * kActRP * 16;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) ao.a[t] = pair_order(*reinterpret_cast<const mu4*>(row + 2 * F::k0(c, t)));
+    group_sums<F>(ao);
+}
+
+// Activations straight from memory (fp32, or fp16 not 16-byte aligned): row n of the pass, super-block
+// sb.  fp32 rows are rounded to f16 after scaling by 2^-e, e from the maximum over the row's super-block
+// (the four lane quarters of row n together hold it), and e is returned (0 for fp16).
+template <class F, typename TA>
+__device__ __forceinline__ int load_act(const TA* __restrict__ A, int K, int row, int sb, int c, bool vec, AOps& ao) {
+    const TA* p = A + static_cast<size_t>(row) * K + 256 * sb;
+    float x[8][8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const TA* q = p + F::k0(c, t);
+        if constexpr (std::is_same<TA, float>::value) {
+            if (vec) {
+                const float4 u = reinterpret_cast<const float4*>(q)[0], v = reinterpret_cast<const float4*>(q)[1];
+                x[t][0] = u.x; x[t][1] = u.y; x[t][2] = u.z; x[t][3] = u.w;
+                x[t][4] = v.x; x[t][5] = v.y; x[t][6] = v.z; x[t][7] = v.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) x[t][i] = q[i];
+            }
+        } else {
+            const uint16_t* s = reinterpret_cast<const uint16_t*>(q);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[t][i] = half_bits_to_float(s[i]);
         }
     }
-}
-
-// Stages activation rows m0 .. m0 + mr - 1 into LDS, 16 k per item, items first, first + nthreads, ...
-// (fp32: after the (row, window) maxima are known; `wexp` holds e per (row, window)).
-template <class F, typename TA>
-__device__ __forceinline__ void stage_rows(const TA* __restrict__ A, int M, int K, int m0, int mr, bool vec, const int* wexp,
-                                           int first, int nthreads) {
-    const int rs = row_stride<F>(K);
-    const int per_row = K / 16;
-    const int items = mr * per_row;
-    for (int it = first; it < items; it += nthreads) {
-        const int m = it / per_row, k = 16 * (it - m * per_row);
-        const bool ok = m0 + m < M;
-        float x[16];
-        load_group<TA>(A + static_cast<size_t>(ok ? m0 + m : 0) * K + k, vec, x);
-        stage_item<F, TA>(it, per_row, K, rs, ok, x, wexp);
+    int e = 0;
+    if constexpr (std::is_same<TA, float>::value) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(x[t][i]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        e = win_exp(__float_as_uint(mx));
     }
-}
-
-// The first kEarly staging items of each thread (fp16 activations) are loaded before the weight chunks
-// are requested, by loads the compiler does not track, and waited for with an explicit count that
-// leaves the chunk requests in flight.
-constexpr int kEarly = 4;
-__device__ __forceinline__ mu4 ldg_untracked(const void* p) {
-    mu4 v;
-    __asm__ volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
-    return v;
-}
-template <int N>
-__device__ __forceinline__ void vm_wait_for(mu4 (&v)[kEarly][2]) {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __asm__ volatile("s_waitcnt vmcnt(%8)"
-                     : "+v"(v[0][0]), "+v"(v[0][1]), "+v"(v[1][0]), "+v"(v[1][1]), "+v"(v[2][0]), "+v"(v[2][1]),
-                       "+v"(v[3][0]), "+v"(v[3][1])
-                     : "n"(N)
-                     : "memory");
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        _Float16 h[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) h[i] = static_cast<_Float16>(__builtin_ldexpf(x[t][i], -e));
+        ao.a[t] = mh8{h[0], h[2], h[1], h[3], h[4], h[6], h[5], h[7]};
+    }
+    group_sums<F>(ao);
+    return e;
 }
 
 template <typename TC>
@@ -431,7 +411,8 @@ __device__ __forceinline__ void mstore<__half>(__half* p, float v) { *reinterpre
 
 // Direct global -> LDS load of 16 bytes per lane (global_load_lds_dwordx4): lane l's bytes land at
 // LDS address m0 + 16 l.  The compiler does not track these loads; they are waited for with explicit
-// vmcnt counts.
+// vmcnt counts (vector memory operations complete in issue order, so waiting until at most N remain
+// outstanding completes every operation issued before the last N).
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds_m0) {
     __asm__ volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_m0) : "memory", "m0");
 }
@@ -440,7 +421,29 @@ __device__ __forceinline__ void vm_wait() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+// vm_wait with a wave-uniform count; counts above 15 wait for 15 (more than needed).
+__device__ __forceinline__ void vm_wait_rt(int n) {
+    switch (n) {
+        case 0: vm_wait<0>(); break;
+        case 1: vm_wait<1>(); break;
+        case 2: vm_wait<2>(); break;
+        case 3: vm_wait<3>(); break;
+        case 4: vm_wait<4>(); break;
+        case 5: vm_wait<5>(); break;
+        case 6: vm_wait<6>(); break;
+        case 7: vm_wait<7>(); break;
+        case 8: vm_wait<8>(); break;
+        case 9: vm_wait<9>(); break;
+        case 10: vm_wait<10>(); break;
+        case 11: vm_wait<11>(); break;
+        case 12: vm_wait<12>(); break;
+        case 13: vm_wait<13>(); break;
+        case 14: vm_wait<14>(); break;
+        default: vm_wait<15>(); break;
+    }
+}
 __device__ __forceinline__ void lds_sync() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ __forceinline__ void lds_reads_done() { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // Weight chunk of a row group: 16 rows x 8 super-blocks (one per slot), copied row by row into an LDS
 // ring slot of 16 x kRP 16-byte pieces (kRP = the chunk row's pieces, plus one unused piece where that
@@ -453,18 +456,25 @@ struct Chunk {
     static constexpr int kInstr = (2 * kRP + 63) / 64;                  // DMA instructions per wave
 };
 
-// R: accumulated values per lane (min(rows of the pass, 4) for one lane quarter holding rows;
-// 4 for passes of more than 4 rows, where quarter c holds rows 4c .. 4c + 3).  NB: ring slots.
+// A pass of lrows (<= 16) activation rows over the workgroup's row groups.  K is cut into windows of 8
+// super-blocks; window j's super-block 8 j + w belongs to wave w (its slot).  Row groups are taken in
+// batches of kBG: for each window, every row group of the batch multiplies its chunk (16 rows x the
+// window's 8 super-blocks) by the window's activations, which each wave holds in registers for its own
+// super-block, so the activations are read once per batch and window whatever the number of rows.
+// Accumulators of the batch stay in registers; at the batch's end the 8 slot partials of each row group
+// are added in slot order through LDS.  A row's arithmetic (slot w adds its super-blocks in order, then
+// the slots are added in order) does not depend on M, the batch or the grid.
 // Per chunk step: wave w waits for its own copies of the chunk, one barrier (all copies landed; every
 // wave is done with the slot refilled next), then it requests chunk i + NB - 1 into that slot and
-// multiplies super-block w of chunk i for the 16 rows from LDS.
+// multiplies super-block w of chunk i for the 16 rows from LDS.  Chunks are requested in the order they
+// are multiplied: batch, window, row group.
+// R: accumulated values per lane (min(rows of the pass, 4) for one lane quarter holding rows;
+// 4 for passes of more than 4 rows, where quarter c holds rows 4c .. 4c + 3).  NB: ring slots.
 template <class F, int R, int NB, typename TA, typename TC>
 __global__ __launch_bounds__(64 * kSlots) void gemv_mfma_kernel(const TA* __restrict__ A, MSegs<TC> sg, int M, int K,
                                                                  int nrg, int a_vec, int lrows) {
     using CK = Chunk<F>;
     constexpr bool kF32 = std::is_same<TA, float>::value;
-    __shared__ int wexp[kF32 ? kMRows * kMaxWin : 1];
-    __shared__ uint32_t wmax[kF32 ? kMRows * kMaxWin : 1];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -472,17 +482,21 @@ __global__ __launch_bounds__(64 * kSlots) void gemv_mfma_kernel(const TA* __rest
     const int m0 = blockIdx.y * lrows;
     const int mr = min(lrows, M - m0);
     const int nsb = K >> 8;
-    const int cpr = (nsb + kSlots - 1) / kSlots;  // chunks per row group
+    const int nwin = (nsb + kSlots - 1) / kSlots;
     const int mine = (nrg - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
-    const int total = mine * cpr;
     const int row_bytes = nsb * F::kBlockBytes;
-    const int rs = row_stride<F>(K);
     const bool vec = a_vec != 0;
-    uint8_t* ring = mlds + lrows * rs;
-    uint8_t* red = ring + NB * CK::kBytes;
+    // activations through this wave's LDS area (fp16, 16-byte aligned), else straight from memory
+    const bool staged = !kF32 && vec;
+    uint8_t* ring = mlds;
+    uint8_t* wact = ring + NB * CK::kBytes + w * lrows * kActRP * 16;
+    uint8_t* red = ring + NB * CK::kBytes + (kF32 ? 0 : act_bytes(lrows));
     const uint32_t ring_m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring));
+    const uint32_t wact_m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(wact));
+    const int qa = (lrows + 3) >> 2;  // lane quarters with partial-sum space
+    const int qrows = (mr + 3) >> 2;  // lane quarters holding output rows
 
-    // Per-lane constants of the copies: instruction k moves this lane's piece q = 64 k + lane of the
+    // Per-lane constants of the chunk copies: instruction k moves this lane's piece q = 64 k + lane of the
     // wave's two rows (row r = q / kRP, piece pc of it; the row's padding piece repeats its last piece).
     int lane_off[CK::kInstr];
     bool lane_r1[CK::kInstr];
@@ -492,27 +506,23 @@ __global__ __launch_bounds__(64 * kSlots) void gemv_mfma_kernel(const TA* __rest
         lane_r1[k] = q >= CK::kRP;
         lane_off[k] = 16 * min(q - (lane_r1[k] ? CK::kRP : 0), CK::kP - 1);
     }
-    // Issue cursor: row group ili (of this workgroup), chunk ich, ring slot islot; the wave's two
-    // source rows (row 2w + 1 clamped to the segment's last row: then d1 = 0).
-    int ili = 0, ich = 0, islot = 0;
-    const uint8_t* src0 = nullptr;
-    int d1 = 0;
-    auto rg_rows = [&](int li) {
-        const int g = static_cast<int>(blockIdx.x) + li * static_cast<int>(gridDim.x);
+    // Issue cursor: batch start ib0 (row groups of this workgroup), its size ibs, window ij, row group iq
+    // of the batch, ring slot islot.
+    int ib0 = 0, ibs = min(kBG, mine), ij = 0, iq = 0, islot = 0;
+    // Requests the cursor's chunk into its slot and advances the cursor (past the workgroup's last chunk
+    // it stays there: the tail requests re-read valid bytes, so every wave issues the same loads).
+    auto issue = [&]() {
+        const int g = static_cast<int>(blockIdx.x) + (ib0 + iq) * static_cast<int>(gridDim.x);
         const uint8_t* W;
         TC* Cs;
         int N, g0;
         seg_pick(sg, g, W, Cs, N, g0);
+        // the wave's two source rows (row 2w + 1 clamped to the segment's last row: then d1 = 0)
         const int r0 = min((g - g0) * kRows + 2 * w, N - 1);
         const int r1 = min(r0 + 1, N - 1);
-        src0 = W + static_cast<size_t>(r0) * row_bytes;
-        d1 = (r1 - r0) * row_bytes;
-    };
-    rg_rows(0);
-    // Requests the cursor's chunk into its slot and advances the cursor (past the workgroup's last chunk
-    // it stays there: the tail requests re-read valid bytes, so every wave issues the same loads).
-    auto issue = [&]() {
-        const int cb = ich * kSlots * F::kBlockBytes;
+        const uint8_t* src0 = W + static_cast<size_t>(r0) * row_bytes;
+        const int d1 = (r1 - r0) * row_bytes;
+        const int cb = ij * kSlots * F::kBlockBytes;
         const uint32_t dst = ring_m0 + static_cast<uint32_t>(islot * CK::kBytes + 2 * w * CK::kRP * 16);
 #pragma unroll
         for (int k = 0; k < CK::kInstr; ++k) {
@@ -520,179 +530,152 @@ __global__ __launch_bounds__(64 * kSlots) void gemv_mfma_kernel(const TA* __rest
             if (64 * k + 64 <= 2 * CK::kRP || 64 * k + lane < 2 * CK::kRP) dma16(src0 + off, dst + 64 * 16 * k);
         }
         islot = islot + 1 == NB ? 0 : islot + 1;
-        if (ich + 1 < cpr) {
-            ++ich;
-        } else if (ili + 1 < mine) {
-            ich = 0;
-            rg_rows(++ili);
+        if (iq + 1 < ibs) {
+            ++iq;
+        } else if (ij + 1 < nwin) {
+            iq = 0;
+            ++ij;
+        } else if (ib0 + ibs < mine) {
+            ib0 += ibs;
+            ibs = min(kBG, mine - ib0);
+            iq = 0;
+            ij = 0;
+        }
+    };
+    // Requests window j's activations (fp16, staged) into this wave's area: the pass's rows of super-block
+    // 8 j + w, lane piece q = 64 i + lane of instruction i (row q / kActRP; the padding piece repeats the
+    // row's last piece).
+    const int act_instr = (mr * kActRP + 63) / 64;
+    auto issue_act = [&](int j) {
+        const int sb = min(kSlots * j + w, nsb - 1);
+        const TA* base = A + static_cast<size_t>(m0) * K + 256 * sb;
+        for (int i = 0; i < act_instr; ++i) {
+            const int q = 64 * i + lane;
+            const int r = q / kActRP;
+            const int pc = min(q - r * kActRP, kActP - 1);
+            if (q < mr * kActRP) dma16(base + static_cast<size_t>(r) * K + 8 * pc, wact_m0 + 64 * 16 * i);
         }
     };
 
-    // fp16 activations: the first items' loads go out first, then the first NB - 1 chunk requests
-    const int per_row = K / 16;
-    const int items = mr * per_row;
-    const bool early = !kF32 && vec;
-    mu4 ev[kEarly][2];
-    if (early) {
-#pragma unroll
-        for (int e = 0; e < kEarly; ++e) {
-            const int it = min(tid + e * 64 * kSlots, items - 1);
-            const int m = it / per_row, k = 16 * (it - m * per_row);
-            const TA* p = A + static_cast<size_t>(m0 + m) * K + k;
-            ev[e][0] = ldg_untracked(p);
-            ev[e][1] = ldg_untracked(p + 8);
-        }
-    }
+    if (staged) issue_act(0);
 #pragma unroll
     for (int u = 0; u < NB - 1; ++u) issue();
+    int act_after = (NB - 1) * CK::kInstr;  // vector memory operations issued after the pending activation copy
 
-    // staging (fp32: window maxima first)
-    if constexpr (kF32) {
-        const int nwin = (K + kWinK - 1) / kWinK;
-        for (int i = tid; i < kMRows * kMaxWin; i += 64 * kSlots) wmax[i] = 0u;
-        __syncthreads();
-        const int per_row = K / 16;
-        for (int it = tid; it < mr * per_row; it += 64 * kSlots) {
-            const int m = it / per_row, k = 16 * (it - m * per_row);
-            float x[16];
-            load_group<float>(A + static_cast<size_t>(m0 + m) * K + k, vec, x);
-            float mx = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(x[i]));
-            atomicMax(&wmax[m * kMaxWin + k / kWinK], __float_as_uint(mx));
-        }
-        __syncthreads();
-        for (int i = tid; i < kMRows * kMaxWin; i += 64 * kSlots) {
-            const int m = i / kMaxWin, wi = i - m * kMaxWin;
-            wexp[i] = (m < mr && wi < nwin) ? win_exp(wmax[i]) : 0;
-        }
-        __syncthreads();
-    }
-    if (early) {
-        vm_wait_for<(NB - 1) * CK::kInstr>(ev);  // the early items have landed; the chunks may still fly
-#pragma unroll
-        for (int e = 0; e < kEarly; ++e) {
-            const int it = tid + e * 64 * kSlots;
-            if (it < items) {
-                _Float16 h[16];
-                __builtin_memcpy(h, &ev[e][0], 16);
-                __builtin_memcpy(h + 8, &ev[e][1], 16);
-                float x[16];
-#pragma unroll
-                for (int i = 0; i < 16; ++i) x[i] = static_cast<float>(h[i]);
-                stage_item<F, TA>(it, per_row, K, rs, true, x, wexp);
-            }
-        }
-        stage_rows<F, TA>(A, M, K, m0, mr, vec, wexp, tid + kEarly * 64 * kSlots, 64 * kSlots);
-    } else {
-        stage_rows<F, TA>(A, M, K, m0, mr, vec, wexp, tid, 64 * kSlots);
-    }
-
-    // activation row read by this lane: rows past the pass read row 0 (their MFMA output rows are never
-    // stored; MFMA rows are independent)
-    const uint8_t* abase = mlds + (n < mr ? n : 0) * rs;
     const uint32_t mg = mkeep(0x64006400u);
-    const int qrows = (mr + 3) >> 2;  // lane quarters holding output rows
-    const int qa = (lrows + 3) >> 2;  // lane quarters with partial-sum space
+    float acc[kBG][R];
+    AOps ao;
+    int eo[R];  // fp32: e of output rows 4c + r in the current window
+#pragma unroll
+    for (int r = 0; r < R; ++r) eo[r] = 0;
+    int cslot = 0;
 
-    float y[R];
+    for (int b0 = 0; b0 < mine; b0 += kBG) {
+        const int bs = min(kBG, mine - b0);
 #pragma unroll
-    for (int r = 0; r < R; ++r) y[r] = 0.0f;
-
-    // Adds the 8 slot partials of the workgroup's li-th row group (written before the last barrier) in
-    // slot order and stores its outputs (wave li % 8).
-    auto reduce_store = [&](int li) {
-        if (w != (li & (kSlots - 1)) || c >= qrows) return;
-        const uint8_t* rb = red + (li & 1) * (kSlots * 16 * qa * 16);
-        mf4 v[kSlots];
+        for (int q = 0; q < kBG; ++q)
 #pragma unroll
-        for (int q = 0; q < kSlots; ++q) v[q] = *reinterpret_cast<const mf4*>(rb + (q * 16 * qa + lane) * 16);
-        mf4 sum = v[0];
-#pragma unroll
-        for (int q = 1; q < kSlots; ++q)
-#pragma unroll
-            for (int r = 0; r < R; ++r) sum[r] += v[q][r];
-        const int g = static_cast<int>(blockIdx.x) + li * static_cast<int>(gridDim.x);
-        const uint8_t* W;
-        TC* Cp;
-        int N, g0;
-        seg_pick(sg, g, W, Cp, N, g0);
-        const int row = (g - g0) * kRows + n;
-        if (row < N) {
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int m = 4 * c + r;
-                if (m < mr) mstore<TC>(Cp + static_cast<size_t>(m0 + m) * N + row, sum[r]);
-            }
-        }
-    };
-
-    int cli = 0, cch = 0, cslot = 0;  // compute cursor
-    for (int i = 0; i < total; ++i) {
-        // this wave's copies of chunk i have landed (chunks i + 1 .. i + NB - 2 may still be in flight)
-        vm_wait<(NB - 2) * CK::kInstr>();
-        lds_sync();
-        if (cch == 0 && cli > 0) reduce_store(cli - 1);
-        issue();
-        const int li = cli, ch = cch;
-        const int sbr = ch * kSlots + w;
-        const bool take = sbr < nsb;
-        const int sb = min(sbr, nsb - 1);
-        const typename F::Raw raw = F::load(ring + cslot * CK::kBytes + n * CK::kRP * 16 + w * F::kBlockBytes, c);
-        const typename F::Pre p = F::prep(raw, c);
-        mf4 T = {0.0f, 0.0f, 0.0f, 0.0f};
-        mf4 T2 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const mh8 af = *reinterpret_cast<const mh8*>(abase + 2 * (256 * sb + F::k0(c, t)));
-            mh8 bw[F::kChains];
-            F::steps(raw, p, t, mg, bw);
-            T = mfma16(af, bw[0], T);
-            if constexpr (F::kChains == 2) T2 = mfma16(af, bw[1], T2);
-        }
-        mf4 U = {0.0f, 0.0f, 0.0f, 0.0f};
-        if constexpr (F::kSums) {
-            const mh8 as = *reinterpret_cast<const mh8*>(abase + 2 * K + 64 * sb + 16 * c);
-            U = mfma16(as, p.bu, U);
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float tv = T[r];
-            if constexpr (F::kChains == 2) tv = __fmaf_rn(16.0f, T2[r], tv);
-            const float uv = U[r];
-            float yn;
-            const int e = kF32 ? wexp[min(4 * c + r, kMRows - 1) * kMaxWin + (sb >> 4)] : 0;
-            if (kF32 && e != 0) {
-                // rescaled window: the super-block's net d T - dmin U first (its two terms can
-                // leave the fp32 range where their difference does not), then times 2^e
-                const float net = F::kSums ? __fmaf_rn(p.d, tv, -(p.c2 * uv)) : p.d * tv;
-                yn = y[r] + __builtin_ldexpf(net, e);
+            for (int r = 0; r < R; ++r) acc[q][r] = 0.0f;
+        for (int j = 0; j < nwin; ++j) {
+            const int sbr = kSlots * j + w;
+            const bool take = sbr < nsb;
+            if (staged) {
+                if (nwin > 1 || b0 == 0) {
+                    vm_wait_rt(act_after);  // window j's activations have landed
+                    read_act<F>(wact, n, c, mr, ao);
+                    if (nwin > 1) {
+                        lds_reads_done();  // the area is refilled with the next window's activations
+                        issue_act(j + 1 < nwin ? j + 1 : 0);
+                        act_after = 0;
+                    }
+                }
             } else {
-                const float yd = __fmaf_rn(p.d, tv, y[r]);
-                yn = F::kSums ? __fmaf_rn(-p.c2, uv, yd) : yd;
-            }
-            y[r] = take ? yn : y[r];
-        }
-        if (ch == cpr - 1) {
-            // row group done: this slot's partial goes to LDS; added after the next barrier
-            if (c < qrows) {
-                mf4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+                const int e = load_act<F, TA>(A, K, m0 + (n < mr ? n : 0), min(sbr, nsb - 1), c, vec, ao);
 #pragma unroll
-                for (int r = 0; r < R; ++r) v[r] = y[r];
-                *reinterpret_cast<mf4*>(red + (li & 1) * (kSlots * 16 * qa * 16) + (w * 16 * qa + lane) * 16) = v;
+                for (int r = 0; r < R; ++r) eo[r] = __shfl(e, 4 * c + r, 64);
             }
 #pragma unroll
-            for (int r = 0; r < R; ++r) y[r] = 0.0f;
+            for (int q = 0; q < kBG; ++q) {
+                if (q < bs) {
+                    // this wave's copies of the chunk have landed (the next NB - 2 may still be in flight)
+                    vm_wait<(NB - 2) * CK::kInstr>();
+                    lds_sync();
+                    issue();
+                    act_after += CK::kInstr;
+                    const typename F::Raw raw =
+                        F::load(ring + cslot * CK::kBytes + n * CK::kRP * 16 + w * F::kBlockBytes, c);
+                    const typename F::Pre p = F::prep(raw, c);
+                    mf4 T = {0.0f, 0.0f, 0.0f, 0.0f};
+                    mf4 T2 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        mh8 bw[F::kChains];
+                        F::steps(raw, p, t, mg, bw);
+                        T = mfma16(ao.a[t], bw[0], T);
+                        if constexpr (F::kChains == 2) T2 = mfma16(ao.a[t], bw[1], T2);
+                    }
+                    mf4 U = {0.0f, 0.0f, 0.0f, 0.0f};
+                    if constexpr (F::kSums) U = mfma16(ao.s, p.bu, U);
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        float tv = T[r];
+                        if constexpr (F::kChains == 2) tv = __fmaf_rn(16.0f, T2[r], tv);
+                        const float uv = U[r];
+                        float yn;
+                        if (kF32 && eo[r] != 0) {
+                            // rescaled activations: the super-block's net d T - dmin U first (its two terms
+                            // can leave the fp32 range where their difference does not), then times 2^e
+                            const float net = F::kSums ? __fmaf_rn(p.d, tv, -(p.c2 * uv)) : p.d * tv;
+                            yn = acc[q][r] + __builtin_ldexpf(net, eo[r]);
+                        } else {
+                            const float yd = __fmaf_rn(p.d, tv, acc[q][r]);
+                            yn = F::kSums ? __fmaf_rn(-p.c2, uv, yd) : yd;
+                        }
+                        acc[q][r] = take ? yn : acc[q][r];
+                    }
+                    cslot = cslot + 1 == NB ? 0 : cslot + 1;
+                }
+            }
         }
-        cslot = cslot + 1 == NB ? 0 : cslot + 1;
-        if (++cch == cpr) {
-            cch = 0;
-            ++cli;
+        // batch done: slot partials to LDS, one barrier, then wave q adds row group b0 + q's partials in
+        // slot order and stores its outputs (the area is next written after at least one more barrier)
+        if (c < qrows) {
+#pragma unroll
+            for (int q = 0; q < kBG; ++q) {
+                if (q < bs) {
+                    mf4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int r = 0; r < R; ++r) v[r] = acc[q][r];
+                    *reinterpret_cast<mf4*>(red + ((q * kSlots + w) * 16 * qa + lane) * 16) = v;
+                }
+            }
+        }
+        lds_sync();
+        if (w < bs && c < qrows) {
+            mf4 v[kSlots];
+#pragma unroll
+            for (int s = 0; s < kSlots; ++s) v[s] = *reinterpret_cast<const mf4*>(red + ((w * kSlots + s) * 16 * qa + lane) * 16);
+            mf4 sum = v[0];
+#pragma unroll
+            for (int s = 1; s < kSlots; ++s)
+#pragma unroll
+                for (int r = 0; r < R; ++r) sum[r] += v[s][r];
+            const int g = static_cast<int>(blockIdx.x) + (b0 + w) * static_cast<int>(gridDim.x);
+            const uint8_t* W;
+            TC* Cp;
+            int N, g0;
+            seg_pick(sg, g, W, Cp, N, g0);
+            const int row = (g - g0) * kRows + n;
+            if (row < N) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int m = 4 * c + r;
+                    if (m < mr) mstore<TC>(Cp + static_cast<size_t>(m0 + m) * N + row, sum[r]);
+                }
+            }
         }
     }
     vm_wait<0>();  // the tail requests land before the wave ends
-    lds_sync();
-    reduce_store(mine - 1);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -761,22 +744,21 @@ hipError_t mocc(const void* kern, size_t lds, int& blocks) {
 }
 
 
-template <class F>
-size_t mlds_bytes(int lrows, int K, int nb) {
-    return static_cast<size_t>(lrows) * row_stride<F>(K) + static_cast<size_t>(nb) * Chunk<F>::kBytes + red_bytes(lrows);
+template <class F, typename TA>
+size_t mlds_bytes(int lrows, int nb) {
+    return static_cast<size_t>(nb) * Chunk<F>::kBytes + (std::is_same<TA, float>::value ? 0 : act_bytes(lrows)) +
+           red_bytes(lrows);
 }
 
 // Activation rows per pass: up to 16, as many as the LDS holds beside a ring of nb weight chunks (rows
-// of a pass share every weight byte loaded; each further pass streams the weights again).  0 when not
-// even one row fits.
-template <class F>
-int pass_rows(int M, int K, int nb, size_t max_lds) {
-    max_lds -= kStaticLds;
+// of a pass share every weight byte loaded; each further pass streams the weights again), balanced over
+// the passes.  0 when not even one row fits.
+template <class F, typename TA>
+int pass_rows(int M, int nb, size_t max_lds) {
     int best = 0;
     for (int r = 1; r <= min(M, kMRows); ++r)
-        if (mlds_bytes<F>(r, K, nb) <= max_lds) best = r;
+        if (mlds_bytes<F, TA>(r, nb) <= max_lds) best = r;
     if (best == 0) return 0;
-    // balance the passes: the fewest rows per pass that keep the same pass count
     const int passes = (M + best - 1) / best;
     return (M + passes - 1) / passes;
 }
@@ -789,7 +771,7 @@ const void* mkern() {
 template <class F, int R, int NB, typename TA, typename TC>
 hipError_t mlaunch(const void* A, const MSegs<TC>& sg, int nrg, int M, int K, bool a_vec, int lrows, int occ, int cus,
                    hipStream_t stream) {
-    const size_t lds = mlds_bytes<F>(lrows, K, NB);
+    const size_t lds = mlds_bytes<F, TA>(lrows, NB);
     const int fill = max(1, occ * cus);
     const dim3 grid(min(nrg, fill), (M + lrows - 1) / lrows);
     hipLaunchKernelGGL((gemv_mfma_kernel<F, R, NB, TA, TC>), grid, dim3(64 * kSlots), lds, stream,
@@ -802,15 +784,15 @@ hipError_t mlaunch_ring(const void* A, const MSegs<TC>& sg, int nrg, int M, int 
                         hipStream_t stream) {
     // ring of 3 or 4 chunks: fewer passes first, then more chunks in flight per CU (workgroups per CU
     // times ring depth - 1), then the shallower ring
-    const int lr3 = pass_rows<F>(M, K, 3, di.max_lds), lr4 = pass_rows<F>(M, K, 4, di.max_lds);
+    const int lr3 = pass_rows<F, TA>(M, 3, di.max_lds), lr4 = pass_rows<F, TA>(M, 4, di.max_lds);
     if (lr3 == 0) return hipErrorNotSupported;
     hipError_t e;
     int occ3 = 0, occ4 = 0;
-    if ((e = mocc(mkern<F, R, 3, TA, TC>(), mlds_bytes<F>(lr3, K, 3), occ3)) != hipSuccess) return e;
+    if ((e = mocc(mkern<F, R, 3, TA, TC>(), mlds_bytes<F, TA>(lr3, 3), occ3)) != hipSuccess) return e;
     const int p3 = (M + lr3 - 1) / lr3;
     bool use4 = false;
     if (lr4 > 0) {
-        if ((e = mocc(mkern<F, R, 4, TA, TC>(), mlds_bytes<F>(lr4, K, 4), occ4)) != hipSuccess) return e;
+        if ((e = mocc(mkern<F, R, 4, TA, TC>(), mlds_bytes<F, TA>(lr4, 4), occ4)) != hipSuccess) return e;
         const int p4 = (M + lr4 - 1) / lr4;
         use4 = p4 < p3 || (p4 == p3 && 3 * occ4 > 2 * occ3);
     }
@@ -842,7 +824,7 @@ hipError_t mdispatch(const void* A, const void* const* W, void* const* C, const 
     if (e != hipSuccess) return e;
     const bool a_vec = (reinterpret_cast<uintptr_t>(A) & 15u) == 0;
     // R by the rows of a pass: a ring of 3 bounds them from above (a ring of 4 holds no more)
-    const int lrows = pass_rows<F>(M, K, 3, di.max_lds);
+    const int lrows = pass_rows<F, TA>(M, 3, di.max_lds);
     if (lrows == 0) return hipErrorNotSupported;
     if (lrows <= 1) return mlaunch_ring<F, 1, TA, TC>(A, sg, nrg, M, K, a_vec, di, stream);
     if (lrows <= 2) return mlaunch_ring<F, 2, TA, TC>(A, sg, nrg, M, K, a_vec, di, stream);
@@ -862,13 +844,20 @@ hipError_t mdtypes(int a_dtype, int c_dtype, const void* A, const void* const* W
 
 }  // namespace
 
-// Q4_K takes the matrix-core GEMV.  Q6_K is not dispatched here: the v_dot2 kernels are faster for it
-// at every measured shape (its activations and 26 KiB weight chunks leave one workgroup per CU).
-bool gemv_mfma_type(int ggml_type) { return ggml_type == QMM_TYPE_Q4_K; }
+// Where the matrix-core GEMV runs.  Q4_K: from M = 2 (the v_dot2 GEMV is faster at M = 1; 70B gate
+// 28672 x 8192: 26 against 30 us), and at M = 1 too in row-identity mode.  Q6_K: from M = 3 (70B down
+// 8192 x 28672: 58 us at M = 1..8 against 41, 42, 72 and 98 us for v_dot2 at M = 1, 2, 4, 8: its decode
+// takes two MFMA chains and twice the VALU work of Q4_K); row-identity mode keeps Q6_K on v_dot2 for
+// every M, so that its M = 1 calls (decode) keep the faster kernel.
+int gemv_mfma_min_m(int ggml_type, bool identity) {
+    if (ggml_type == QMM_TYPE_Q4_K) return identity ? 1 : 2;
+    if (ggml_type == QMM_TYPE_Q6_K) return identity ? INT_MAX : 3;
+    return INT_MAX;
+}
 
 hipError_t launch_gemv_mfma(int ggml_type, const void* A, int a_dtype, int c_dtype, int M, int K, const void* const* W,
                             void* const* C, const int* N, int count, hipStream_t stream) {
-    if (count < 1 || count > 4 || M < 1 || K < 256 || K % 256 != 0 || K > kMaxWin * kWinK) return hipErrorNotSupported;
+    if (count < 1 || count > 4 || M < 1 || K < 256 || K % 256 != 0) return hipErrorNotSupported;
     for (int j = 0; j < count; ++j)
         if (N[j] < 1 || (reinterpret_cast<uintptr_t>(W[j]) & 15u) != 0) return hipErrorNotSupported;
     // the weight chunks are copied in 16-byte pieces: rows must be whole pieces

@@ -98,8 +98,9 @@ hipError_t launch_gemv_ex(int ggml_type, const void* A, int c_dtype, int M, int 
 int gemv_max_fused();
 // Matrix-core GEMV (qmm_gemv_mfma.hip) for the GEMV family's M: Q4_K and Q6_K weights, `count` (1..4)
 // matrices sharing the activations; hipErrorNotSupported when the shape is outside it (then no row of
-// any M of that shape takes it, so rows stay bit-identical across M).
-bool gemv_mfma_type(int ggml_type);
+// any M of that shape takes it, so rows stay bit-identical across M).  gemv_mfma_min_m: the smallest M
+// that runs it for the format (INT_MAX: none), in row-identity mode or not.
+int gemv_mfma_min_m(int ggml_type, bool identity);
 hipError_t launch_gemv_mfma(int ggml_type, const void* A, int a_dtype, int c_dtype, int M, int K, const void* const* W,
                             void* const* C, const int* N, int count, hipStream_t stream);
 hipError_t launch_gemm_prefill(int ggml_type, const void* A, int a_dtype, const void* W, void* C,

@@ -195,9 +195,10 @@ def row_identity() -> bool:
 
 
 def set_row_identity(on: bool) -> None:
-    """Calling thread's row-identity mode: when on, every GEMV-size M runs the kernels of M >= 2,
-    so that row m of any M < gemv_max_m() is bit-identical to the M = 1 call (the reference's
-    invariant); when off (the default), Q4_K's M = 1 takes the faster v_dot2 GEMV."""
+    """Calling thread's row-identity mode: when on, every GEMV-size M of a format runs one kernel
+    family (Q4_K the matrix-core GEMV, the other formats v_dot2), so that row m of any
+    M < gemv_max_m() is bit-identical to the M = 1 call (the reference's invariant); when off (the
+    default), each M takes the faster family (Q4_K matrix-core from M = 2, Q6_K from M = 3)."""
     check(_lib.qmm_set_row_identity(1 if on else 0))
 
 

@@ -65,12 +65,13 @@ size_t qmm_weight_bytes(int ggml_type, int64_t n, int64_t k);
 /* C[M,N] (c_dtype) = A[M,K] (a_dtype) @ dequant(W)[N,K]^T with fp32 accumulation.
  * M < qmm_gemv_max_m() (17) runs the bandwidth-bound GEMV kernels; larger M runs the f16-MFMA
  * prefill GEMM (a 32-row tile up to M = 32), whose rows agree with the M = 1 call within the
- * prefill accuracy bound.  Among GEMV sizes, Q4_K takes a matrix-core GEMV for M >= 2 and the
- * v_dot2 GEMV at M = 1 (the faster at each size): rows of every M in [2, gemv_max_m()) are
- * bit-identical to one another, and agree with M = 1 within the accuracy bound of either.  With
- * qmm_set_row_identity(1) M = 1 runs the matrix-core GEMV too, so that every GEMV-size row is
- * bit-identical to the M = 1 call, as in the reference.  The other formats run one GEMV family
- * for every M (bit-identical rows in both modes).
+ * prefill accuracy bound.  Among GEMV sizes each format takes the faster of two kernel families:
+ * Q4_K the matrix-core GEMV from M = 2, Q6_K from M = 3 (16-byte aligned weights, K a multiple of
+ * 2048), and the v_dot2 GEMV below that and for the other formats.  Rows are bit-identical for
+ * every M within one family, and the two families agree within the GEMV accuracy bound.  With
+ * qmm_set_row_identity(1) every GEMV-size M runs one family (Q4_K the matrix-core GEMV, the other
+ * formats the v_dot2 GEMV), so that every row is bit-identical to the M = 1 call, as in the
+ * reference.
  * Generalises launch_matmul_q{4_0,8_0,4_k,6_k}_device (reference
  * src/kernels/dequantize.h:98-132, dispatch at dequantize.hip:778/896/1014/1132). */
 int qmm_gemm(int ggml_type, const void* A, int a_dtype, const void* W, void* C, int c_dtype,
@@ -156,10 +157,11 @@ int qmm_set_thread_gemv_max_m(int m);
 /* Row-identity mode of the calling thread (0 or 1; QMM_ERR_INVALID_ARGUMENT otherwise); 0 by
  * default.  No counterpart in the reference, whose kernels keep every row of every GEMV-size M
  * bit-identical to the M = 1 call (its tests assert it, tests/test_phase5_scale.py:274-310).
- * With 1, qmm_gemm, qmm_gemm_noalloc and qmm_gemm_batch run every M < qmm_gemv_max_m() on the
- * kernel family of M >= 2, so that rows match the M = 1 call bit for bit (Q4_K's M = 1 then runs
- * the matrix-core GEMV, a few microseconds slower than the v_dot2 GEMV on large matrices).  The
- * reference-API launchers (qmm_matmul_q*_device / _host) always run in this mode. */
+ * With 1, qmm_gemm, qmm_gemm_noalloc and qmm_gemm_batch run every M < qmm_gemv_max_m() of a
+ * format on one kernel family, so that rows match the M = 1 call bit for bit: Q4_K on the
+ * matrix-core GEMV (its M = 1 a few microseconds slower than the v_dot2 GEMV on large matrices),
+ * Q6_K and the other formats on the v_dot2 GEMV (Q6_K's M >= 3 then slower than the matrix-core
+ * GEMV).  The reference-API launchers (qmm_matmul_q*_device / _host) always run in this mode. */
 int qmm_set_row_identity(int on);
 int qmm_row_identity(void);
 

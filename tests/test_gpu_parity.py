@@ -7,8 +7,9 @@ Bars (tolerances are written into each check):
   exact weights, and the reference tests' own absolute tolerances against the reference
   formula (fp16-rounded weights, fp32 matmul);
 * row results bit-identical for every M in the GEMV range in row-identity mode (the
-  reference's invariant, tests/test_phase5_scale.py:274-310, 371-379), and for every M >= 2 in
-  the default mode (Q4_K's M = 1 then runs the v_dot2 GEMV, within the GEMV bar);
+  reference's invariant, tests/test_phase5_scale.py:274-310, 371-379), and within each kernel
+  family in the default mode (Q4_K from M = 2 and Q6_K from M = 3 run the matrix-core GEMV, smaller
+  M the v_dot2 GEMV; the families agree within the GEMV bar);
 * full 8B / 70B shapes: sampled rows against fp64, linearity in x.
 """
 
@@ -241,25 +242,36 @@ def test_gemv_rows_bit_identical_across_m(dev, t):
                 np.testing.assert_array_equal(y, single[:M], err_msg=f"{O.TYPE_NAMES[t]} M={M} N={N} K={K}")
 
 
+def mfma_min_m(t, K):
+    """Smallest M that runs the matrix-core GEMV in the default mode (99: none)."""
+    if t == O.GGML_Q4_K:
+        return 2
+    if t == O.GGML_Q6_K and K % 2048 == 0:
+        return 3
+    return 99
+
+
 @pytest.mark.parametrize("t", TYPES)
-def test_default_mode_rows_bit_identical_for_m_from_2(dev, t):
-    """Default mode: every M >= 2 of the GEMV range gives each row bit for bit the same result
-    (Q4_K: the matrix-core GEMV); M = 1 (Q4_K: the v_dot2 GEMV) agrees with them within the GEMV
-    bar, and is bit-identical to them for the formats that run one family."""
+def test_default_mode_rows_bit_identical_within_each_family(dev, t):
+    """Default mode: every M from the format's matrix-core threshold on (Q4_K 2, Q6_K 3) gives each
+    row bit for bit the same result, and so does every M below it (the v_dot2 GEMV); the two families
+    agree within the GEMV bar.  Formats without the matrix-core path run one family for every M."""
     import qmm
     assert not qmm.row_identity()
     rng = np.random.default_rng(651 + t)
-    for N, K in GEMV_SHAPES[t][:2]:
+    for N, K in GEMV_SHAPES[t]:
         raw = O.synth_weights(t, N, K, rng)
         x = rng.standard_normal((16, K)).astype(np.float32)
+        thr = mfma_min_m(t, K)
         y16 = gemm(t, x, raw, N, K, dev)
-        for M in (2, 3, 5, 8, 13):
-            np.testing.assert_array_equal(gemm(t, x[:M], raw, N, K, dev), y16[:M],
-                                          err_msg=f"{O.TYPE_NAMES[t]} M={M} N={N} K={K}")
         y1 = np.stack([gemm(t, x[m:m + 1], raw, N, K, dev)[0] for m in range(16)])
+        for M in (2, 3, 5, 8, 13):
+            want = y16 if M >= thr else y1
+            np.testing.assert_array_equal(gemm(t, x[:M], raw, N, K, dev), want[:M],
+                                          err_msg=f"{O.TYPE_NAMES[t]} M={M} N={N} K={K}")
         y64 = O.matmul_f64(t, x, raw, N, K)
         assert O.max_rel_err(y1, y64) <= GEMV_TOL and O.max_rel_err(y16, y64) <= GEMV_TOL
-        if t != O.GGML_Q4_K:
+        if thr > 16:
             np.testing.assert_array_equal(y1, y16, err_msg=f"{O.TYPE_NAMES[t]} N={N} K={K}")
 
 
@@ -488,6 +500,7 @@ FULL_SHAPES = [
     ("8b_q6_k_lm_head", O.GGML_Q6_K, 128256, 4096),
     ("8b_q4_k_gate_up_rows", O.GGML_Q4_K, 28672, 4096),
     ("70b_q4_k_gate", O.GGML_Q4_K, 28672, 8192),
+    ("70b_q4_k_q_o", O.GGML_Q4_K, 8192, 8192),
     ("70b_q4_k_kv", O.GGML_Q4_K, 1024, 8192),
     ("70b_q6_k_down", O.GGML_Q6_K, 8192, 28672),
     ("4k_q4_0", O.GGML_Q4_0, 4096, 4096),
@@ -495,7 +508,7 @@ FULL_SHAPES = [
 
 
 @pytest.mark.parametrize("name,t,N,K", FULL_SHAPES)
-@pytest.mark.parametrize("M", [1, 4])
+@pytest.mark.parametrize("M", [1, 4, 16])
 def test_full_size_sampled_rows_and_linearity(dev, name, t, N, K, M):
     import torch
     import qmm
