@@ -267,12 +267,23 @@ int qmm_forward_layer_host(const qmm_layer_config* cfg, const qmm_layer_weights*
             return bad(std::string(names[i]) + " has an unsupported ggml_type or a K its blocks do not divide.");
         ops.push_back({wp[i], nullptr, b});
     }
+    // optional fp16 biases (host vectors) follow the weights
+    const void* bp[4] = {w->bq, w->bk, w->bv, w->bo};
+    const int bn[4] = {q_dim, kv_dim, kv_dim, hidden};
+    int bias_op[4] = {-1, -1, -1, -1};
+    for (int i = 0; i < 4; ++i) {
+        if (bp[i] == nullptr) continue;
+        bias_op[i] = static_cast<int>(ops.size());
+        ops.push_back({bp[i], nullptr, h2(bn[i])});
+    }
     return staged(ops, [&] {
         qmm_layer_weights d = *w;
         d.attn_norm = ops[2].dev;
         d.ffn_norm = ops[3].dev;
         const void** dst[7] = {&d.wq, &d.wk, &d.wv, &d.wo, &d.wgate, &d.wup, &d.wdown};
         for (int i = 0; i < 7; ++i) *dst[i] = ops[4 + i].dev;
+        const void** bdst[4] = {&d.bq, &d.bk, &d.bv, &d.bo};
+        for (int i = 0; i < 4; ++i) *bdst[i] = bias_op[i] >= 0 ? ops[bias_op[i]].dev : nullptr;
         return qmm_forward_layer(cfg, &d, ops[0].dev, ops[1].dev, layer_idx, seq_len, pos_offset, nullptr);
     });
 }

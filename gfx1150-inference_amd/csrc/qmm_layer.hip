@@ -22,6 +22,7 @@
 //   * Layer: q/k/v and gate/up each run as one fused projection launch (qmm_gemm_batch), all
 //     kernels on the caller's stream with no host synchronisation; activations live in a
 //     grow-only per-(device, stream) workspace.
+#include <algorithm>
 #include <cmath>
 #include <mutex>
 #include <string>
@@ -142,6 +143,15 @@ __global__ __launch_bounds__(256) void residual_add_kernel(const _Float16* __res
 }
 
 // out = half(silu(g) * u), silu(g) = g / (1 + exp(-g)).
+// y[r, i] = f16(f32(y[r, i]) + f32(b[i])) over `rows` rows of n values: a projection's bias added in
+// fp32 to its fp16 output and rounded once (reference src/layer.py:274-282, 344-346).
+__global__ __launch_bounds__(256) void bias_add_kernel(_Float16* __restrict__ y, const _Float16* __restrict__ b, int n,
+                                                       int64_t total) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < total; i += stride)
+        y[i] = static_cast<_Float16>(static_cast<float>(y[i]) + static_cast<float>(b[i % n]));
+}
+
 __global__ __launch_bounds__(256) void swiglu_kernel(const _Float16* __restrict__ g, const _Float16* __restrict__ u,
                                                     _Float16* __restrict__ out, int64_t n) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
@@ -791,6 +801,14 @@ hipError_t launch_residual_add(const void* x, const void* r, void* out, int64_t 
     return hipGetLastError();
 }
 
+hipError_t launch_bias_add(void* y, const void* b, int rows, int n, hipStream_t stream) {
+    const int64_t total = static_cast<int64_t>(rows) * n;
+    const int blocks = static_cast<int>(std::min<int64_t>((total + 255) / 256, 4096));
+    hipLaunchKernelGGL(bias_add_kernel, dim3(blocks), dim3(256), 0, stream, static_cast<_Float16*>(y),
+                       static_cast<const _Float16*>(b), n, total);
+    return hipGetLastError();
+}
+
 hipError_t launch_swiglu(const void* g, const void* u, void* out, int64_t n, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
     const int64_t items = (n & 7) == 0 ? n / 8 : n;
@@ -1100,6 +1118,15 @@ LayerStatus forward_layer(const qmm_layer_config& cfg, const qmm_layer_weights& 
             return fail(e, "rmsnorm");
         if ((st = gemms(qkv + done, 3 - done)).code != QMM_OK) return st;
     }
+    // optional q / k / v biases, added to the projections before the rotation
+    {
+        const void* const bias[3] = {w.bq, w.bk, w.bv};
+        const size_t at[3] = {o_q, o_k, o_v};
+        const int bn[3] = {qd, kvd, kvd};
+        for (int i = 0; i < 3; ++i)
+            if (bias[i] != nullptr && (e = launch_bias_add(ws + at[i], bias[i], seq_len, bn[i], stream)) != hipSuccess)
+                return fail(e, "q/k/v bias");
+    }
     // 3.-4. RoPE on q and k (k and v land in the cache at their positions), attention over the
     // cache; in decode the rotation and the cache write run inside the attention kernel
     const float scale = cfg.scale != 0.0f ? cfg.scale : 1.0f / std::sqrt(static_cast<float>(D));
@@ -1118,6 +1145,8 @@ LayerStatus forward_layer(const qmm_layer_config& cfg, const qmm_layer_weights& 
     // 5. output projection
     const qmm_gemm_desc o = desc(w.wo_type, ws + o_att, w.wo, ws + o_proj, seq_len, hid, qd);
     if ((st = gemms(&o, 1)).code != QMM_OK) return st;
+    if (w.bo != nullptr && (e = launch_bias_add(ws + o_proj, w.bo, seq_len, hid, stream)) != hipSuccess)
+        return fail(e, "output bias");
     // 6.-7. residual + pre-FFN RMSNorm, gate, up (one launch per weight type)
     const qmm_gemm_desc gu[2] = {desc(w.wgate_type, ws + o_norm, w.wgate, ws + o_g, seq_len, inter, hid),
                                  desc(w.wup_type, ws + o_norm, w.wup, ws + o_u, seq_len, inter, hid)};

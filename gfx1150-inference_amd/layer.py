@@ -161,6 +161,31 @@ def layer_weights_struct(layer_weights: Dict[str, Tuple[object, object]], prefix
                 raise ValueError(f"{name}.weight view holds {_nbytes(view)} bytes, N={N} K={K} need {need}")
         setattr(w, field, view.data_ptr())
         setattr(w, field + "_type", int(info.ggml_type))
+    # Optional projection biases (reference src/layer.py:274-282, 344-346), passed as fp16 vectors: an
+    # F32 bias is rounded to fp16 first, as the reference's norm_weight_fp16 does (layer.py:161-167).
+    # The converted copies are kept on the struct for the duration of the call.
+    import torch
+
+    keep = []
+    for field, name, n in (("bq", "attn_q", None if config is None else config.num_heads * config.head_dim),
+                           ("bk", "attn_k", None if config is None else config.num_kv_heads * config.head_dim),
+                           ("bv", "attn_v", None if config is None else config.num_kv_heads * config.head_dim),
+                           ("bo", "attn_output", None if config is None else config.hidden_size)):
+        entry = layer_weights.get(f"{prefix}{name}.bias")
+        if entry is None:
+            continue
+        view = entry[1]
+        if view.dtype == torch.float32:
+            view = view.to(torch.float16)
+        elif view.dtype != torch.float16:
+            raise ValueError(f"Unsupported bias dtype for {name}.bias: {view.dtype}")
+        if config is not None:
+            on_device(name + ".bias", view)
+            if view.numel() != n:
+                raise ValueError(f"{name}.bias has {view.numel()} values, the projection has {n} outputs")
+        keep.append(view)
+        setattr(w, field, view.data_ptr())
+    w._keep = keep
     return w
 
 
@@ -194,8 +219,9 @@ class TransformerLayer:
                                 or tuple(out.shape) != tuple(x.shape)):
             raise ValueError("out must be a contiguous fp16 tensor of hidden_states' shape on its device")
         y = torch.empty_like(x) if out is None else out
-        w = layer_weights_struct(layer_weights, f"blk.{layer_idx}.", self.cfg, x.device)
         s = torch.cuda.current_stream(x.device) if stream is None else stream
+        with torch.cuda.stream(s):  # bias conversions are ordered before the layer's kernels
+            w = layer_weights_struct(layer_weights, f"blk.{layer_idx}.", self.cfg, x.device)
         qmm.check(qmm.lib().qmm_forward_layer(self._c, w, x.data_ptr(), y.data_ptr(), layer_idx, x.shape[0], pos_offset,
                                               s.cuda_stream))
         return y, None

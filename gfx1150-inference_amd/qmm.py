@@ -84,7 +84,8 @@ class LayerWeights(ctypes.Structure):
 
     _fields_ = [("attn_norm", _vp), ("attn_norm_dtype", _i), ("wq", _vp), ("wq_type", _i), ("wk", _vp), ("wk_type", _i),
                 ("wv", _vp), ("wv_type", _i), ("wo", _vp), ("wo_type", _i), ("ffn_norm", _vp), ("ffn_norm_dtype", _i),
-                ("wgate", _vp), ("wgate_type", _i), ("wup", _vp), ("wup_type", _i), ("wdown", _vp), ("wdown_type", _i)]
+                ("wgate", _vp), ("wgate_type", _i), ("wup", _vp), ("wup_type", _i), ("wdown", _vp), ("wdown_type", _i),
+                ("bq", _vp), ("bk", _vp), ("bv", _vp), ("bo", _vp)]
 
 
 class GemmDesc(ctypes.Structure):

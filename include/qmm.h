@@ -276,6 +276,14 @@ typedef struct qmm_layer_weights {
     int wup_type;
     const void* wdown;
     int wdown_type;
+    /* Optional fp16 biases (NULL = none): q [num_heads * head_dim], k and v [num_kv_heads * head_dim],
+     * attention output [hidden_size].  Each is added in fp32 to its projection's fp16 output, which
+     * is rounded to fp16 once more, as the reference's layer does (src/layer.py:274-282, 344-346;
+     * an F32 GGUF bias is rounded to fp16 first, layer.py:161-167). */
+    const void* bq;
+    const void* bk;
+    const void* bv;
+    const void* bo;
 } qmm_layer_weights;
 
 /* x_out [seq_len, hidden] = one Llama layer on x_in (fp16, device): RMSNorm, q/k/v (one fused

@@ -106,24 +106,33 @@ def project(x, w_deq_f16):
     return _f16(np.asarray(x, np.float16).astype(np.float32) @ np.asarray(w_deq_f16, np.float16).astype(np.float32).T)
 
 
+def add_bias(y, b):
+    """fp16 projection output plus an optional fp16 bias, added in fp32 and rounded to fp16
+    (reference src/layer.py:274-282, 344-346)."""
+    if b is None:
+        return y
+    return _f16(np.asarray(y, np.float16).astype(np.float32) + np.asarray(b, np.float16).astype(np.float32))
+
+
 def layer_forward(x, w, cfg, k_cache, v_cache, pos_offset):
     """One layer on fp16 activations x [seq, hidden]; w maps 'attn_norm', 'ffn_norm' (fp16 [hidden])
-    and 'q', 'k', 'v', 'o', 'gate', 'up', 'down' (fp16 dequantized [N, K]); k_cache / v_cache
+    and 'q', 'k', 'v', 'o', 'gate', 'up', 'down' (fp16 dequantized [N, K]), and optionally the fp16
+    biases 'bq', 'bk', 'bv', 'bo' (reference src/layer.py:274-282, 344-346); k_cache / v_cache
     (fp16 [max_seq, kv_heads, d]) receive this call's rotated keys and values at pos_offset."""
     seq = x.shape[0]
     H, kvh, d = cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"]
     eps, base, neox = cfg["rms_norm_eps"], cfg["rope_freq_base"], cfg["rope_neox"]
     nx = rmsnorm(x, w["attn_norm"], eps)
-    q = project(nx, w["q"]).reshape(seq, H, d)
-    k = project(nx, w["k"]).reshape(seq, kvh, d)
-    v = project(nx, w["v"]).reshape(seq, kvh, d)
+    q = add_bias(project(nx, w["q"]), w.get("bq")).reshape(seq, H, d)
+    k = add_bias(project(nx, w["k"]), w.get("bk")).reshape(seq, kvh, d)
+    v = add_bias(project(nx, w["v"]), w.get("bv")).reshape(seq, kvh, d)
     q = rope(q, pos_offset, base, neox)
     k = rope(k, pos_offset, base, neox)
     k_cache[pos_offset:pos_offset + seq] = k
     v_cache[pos_offset:pos_offset + seq] = v
     att = gqa_attention(q, k_cache[:pos_offset + seq], v_cache[:pos_offset + seq], pos_offset,
                         cfg.get("scale", 0.0) or 1.0 / math.sqrt(d), True)
-    proj = project(att.reshape(seq, H * d), w["o"])
+    proj = add_bias(project(att.reshape(seq, H * d), w["o"]), w.get("bo"))
     h, nh = rmsnorm_residual(x, proj, w["ffn_norm"], eps)
     act = swiglu(project(nh, w["gate"]), project(nh, w["up"]))
     return residual_add(h, project(act, w["down"]))

@@ -297,6 +297,57 @@ def test_forward_layer_prefill_then_decode(dev, prefill, neox, up_type):
         qmm.check(lib.qmm_kv_cache_free())
 
 
+@pytest.mark.parametrize("prefill", [6, 24])
+def test_forward_layer_with_biases(dev, prefill):
+    """q / k / v / output biases (reference src/layer.py:274-282, 344-346): each added in fp32 to
+    its fp16 projection and rounded once, before the rotation and the residual; a prefill (GEMV
+    rows, or the MFMA projections from 17 rows) then a decode step, against the oracle."""
+    import torch
+    import qmm
+    r = np.random.default_rng(80 + prefill)
+    hidden, inter, heads, kvh, d = 256, 512, 8, 2, 32
+    types = {"q": O.GGML_Q4_K, "k": O.GGML_Q4_K, "v": O.GGML_Q6_K, "o": O.GGML_Q8_0, "gate": O.GGML_Q4_K,
+             "up": O.GGML_Q4_K, "down": O.GGML_Q6_K}
+    packed, deq = make_layer(r, hidden, inter, heads, kvh, d, types)
+    for bn, n in (("bq", heads * d), ("bk", kvh * d), ("bv", kvh * d), ("bo", hidden)):
+        deq[bn] = (0.5 * r.standard_normal(n)).astype(np.float16)
+    dev_w = {n: t16(raw, dev) for n, (t, raw) in packed.items()}
+    dev_b = {n: t16(deq[n], dev) for n in ("attn_norm", "ffn_norm", "bq", "bk", "bv", "bo")}
+    w = qmm.LayerWeights()
+    w.attn_norm, w.attn_norm_dtype = dev_b["attn_norm"].data_ptr(), qmm.DTYPE_F16
+    w.ffn_norm, w.ffn_norm_dtype = dev_b["ffn_norm"].data_ptr(), qmm.DTYPE_F16
+    for f, n in (("wq", "q"), ("wk", "k"), ("wv", "v"), ("wo", "o"), ("wgate", "gate"), ("wup", "up"), ("wdown", "down")):
+        setattr(w, f, dev_w[n].data_ptr())
+        setattr(w, f + "_type", packed[n][0])
+    for f in ("bq", "bk", "bv", "bo"):
+        setattr(w, f, dev_b[f].data_ptr())
+    c = qmm.LayerConfig()
+    c.hidden_size, c.intermediate_size, c.num_heads, c.num_kv_heads, c.head_dim = hidden, inter, heads, kvh, d
+    c.rms_norm_eps, c.rope_freq_base, c.rope_neox, c.scale = 1e-5, 10000.0, 0, 0.0
+    cfg = {"num_heads": heads, "num_kv_heads": kvh, "head_dim": d, "rms_norm_eps": 1e-5, "rope_freq_base": 10000.0,
+           "rope_neox": False}
+    x = (r.standard_normal((prefill + 1, hidden)) * 0.5).astype(np.float16)
+    kc, vc = np.zeros((64, kvh, d), np.float16), np.zeros((64, kvh, d), np.float16)
+    want_pre = L.layer_forward(x[:prefill], deq, cfg, kc, vc, 0)
+    want_dec = L.layer_forward(x[prefill:], deq, cfg, kc, vc, prefill)
+    # without the biases the result is measurably different (the test would notice them dropped)
+    kc0, vc0 = np.zeros_like(kc), np.zeros_like(vc)
+    nobias = {k: v for k, v in deq.items() if k not in ("bq", "bk", "bv", "bo")}
+    assert maxerr(L.layer_forward(x[:prefill], nobias, cfg, kc0, vc0, 0), want_pre) > 5e-2
+    lib = qmm.lib()
+    qmm.check(lib.qmm_kv_cache_init(1, 64, kvh, d))
+    try:
+        X = t16(x, dev)
+        Y = torch.empty_like(X)
+        qmm.check(lib.qmm_forward_layer(c, w, X.data_ptr(), Y.data_ptr(), 0, prefill, 0, stream()))
+        qmm.check(lib.qmm_forward_layer(c, w, X[prefill:].data_ptr(), Y[prefill:].data_ptr(), 0, 1, prefill, stream()))
+        y = host(Y)
+        assert maxerr(y[:prefill], want_pre) < (1e-2 if prefill >= qmm.gemv_max_m() else 5e-3)
+        assert maxerr(y[prefill:], want_dec) < 5e-3
+    finally:
+        qmm.check(lib.qmm_kv_cache_free())
+
+
 def test_transformer_layer_over_resident_weights(dev, tmp_path):
     import torch
     import gguf
@@ -315,6 +366,11 @@ def test_transformer_layer_over_resident_weights(dev, tmp_path):
                ("blk.0.ffn_norm.weight", (hidden,), gguf.GGMLType.F16, deq["ffn_norm"].tobytes())]
     for n, (t, raw) in packed.items():
         tensors.append((f"blk.0.{names[n]}.weight", (shapes[n][1], shapes[n][0]), gguf.GGMLType(t), raw.tobytes()))
+    # F32 q and output biases (rounded to fp16 on the way in, as the reference's norm_weight_fp16)
+    for bn, tname, n in (("bq", "attn_q", heads * d), ("bo", "attn_output", hidden)):
+        b32 = (0.5 * r.standard_normal(n)).astype(np.float32)
+        deq[bn] = b32.astype(np.float16)
+        tensors.append((f"blk.0.{tname}.bias", (n,), gguf.GGMLType.F32, b32.tobytes()))
     V = gguf.GGUFValueType
     meta = {"general.architecture": (V.STRING, "llama"), "llama.block_count": (V.UINT32, 1),
             "llama.embedding_length": (V.UINT32, hidden), "llama.feed_forward_length": (V.UINT32, inter),

@@ -162,3 +162,23 @@ def test_layer_decode_after_prefill_matches_longer_prefill():
     last = L.layer_forward(x[4:], w, cfg, kc2, vc2, 4)
     assert np.max(np.abs(first.astype(np.float32) - full[:4].astype(np.float32))) < 2e-3
     assert np.max(np.abs(last.astype(np.float32) - full[4:].astype(np.float32))) < 2e-3
+
+
+def test_add_bias_rounds_once_after_an_fp32_add():
+    """add_bias (reference src/layer.py:274-282): fp32 sum of the fp16 output and the fp16 bias,
+    rounded to fp16 once.  1 + 2^-11 and 3 + 2^-10 are ties (half an fp16 ulp): they round to
+    even (1 and 3); -y cancels exactly; no bias leaves y unchanged; on random values the result is
+    the exact sum rounded once (every fp32 sum of two fp16 values here is exact)."""
+    y = np.array([[1.0, 3.0, -2.5, 65504.0]], np.float16)
+    assert L.add_bias(y, None) is y
+    b = np.array([2.0 ** -11, 2.0 ** -10, 2.5, -65504.0], np.float16)
+    out = L.add_bias(y, b)
+    assert out.dtype == np.float16
+    assert out[0, 0] == np.float16(1.0)
+    assert out[0, 1] == np.float16(3.0)
+    assert out[0, 2] == 0.0 and out[0, 3] == 0.0
+    r = rng(11)
+    y = r.standard_normal((3, 40)).astype(np.float16)
+    b = r.standard_normal(40).astype(np.float16)
+    want = (y.astype(np.float64) + b.astype(np.float64)).astype(np.float16)  # exact sum, one rounding
+    assert np.array_equal(L.add_bias(y, b), want)
