@@ -180,6 +180,16 @@ def test_cpp_shim_header_compiles(tmp_path):
     assert r.returncode == 0, r.stderr
 
 
+def test_cpp_caller_links_and_loads():
+    """The C++ caller of qmm_launchers.hpp (built by build(), tests/cpp/Makefile) resolves every
+    symbol it uses from libqmm_gfx950.so at load time; without arguments it prints its usage and
+    exits with 2 before any HIP call."""
+    exe = os.path.join(REPO, "tests", "cpp", "_build", "launchers_caller")
+    assert os.path.exists(exe), "run __graft_entry__.build() (make -C tests/cpp)"
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=60, env={**os.environ, "LD_BIND_NOW": "1"})
+    assert r.returncode == 2 and "usage" in r.stderr, (r.returncode, r.stderr)
+
+
 def test_c_header_is_plain_c(tmp_path):
     src = tmp_path / "use_c.c"
     src.write_text('#include "qmm.h"\nint f(void) { return qmm_version(); }\n')
