@@ -252,18 +252,17 @@ struct MQ6K {
 // LDS of a workgroup (dynamic):
 //   ring  NB weight chunks of Chunk<F>::kBytes;
 //   act   fp16 activations only: per wave, the pass's rows of the wave's super-block of the current
-//         window, lrows rows x kActRP 16-byte pieces (the 512 bytes of a row, then one padding piece,
-//         so that consecutive rows start 4 banks apart);
-//   red   slot partials of a batch: kBG row groups x 8 waves x 16 qa lanes x 16 bytes.
+//         window, lrows rows x 32 16-byte pieces (the 512 bytes of a row), piece p of row r at slot
+//         p ^ r, so that the 16 rows' pieces p fall in different banks;
+//   red   slot partials of a batch: bg (up to kBG) row groups x 8 waves x 16 qa lanes x 16 bytes.
 // ------------------------------------------------------------------------------------------------
 extern __shared__ __attribute__((aligned(16))) uint8_t mlds[];
 
-constexpr int kBG = 4;     // row groups per batch: their accumulators stay in registers across the windows
+constexpr int kBG = 4;     // row groups per batch at most: their accumulators stay in registers across the windows
 constexpr int kActP = 32;  // 16-byte pieces of one super-block of one fp16 activation row
-constexpr int kActRP = 33;
 
-__host__ __device__ constexpr int act_bytes(int lrows) { return kSlots * lrows * kActRP * 16; }
-__host__ __device__ constexpr int red_bytes(int lrows) { return kBG * kSlots * 16 * ((lrows + 3) / 4) * 16; }
+__host__ __device__ constexpr int act_bytes(int lrows) { return kSlots * lrows * kActP * 16; }
+__host__ __device__ constexpr int red_bytes(int lrows, int bg) { return bg * kSlots * 16 * ((lrows + 3) / 4) * 16; }
 
 __device__ __forceinline__ int win_exp(uint32_t maxbits) {
     // (row, super-block) maximum at or above 65504, or in [2^-126, 2^-14): scale by 2^-e with
@@ -323,9 +322,11 @@ __device__ __forceinline__ void group_sums(AOps& ao) {
 // past the pass read row 0: their MFMA output rows are never stored, and MFMA rows are independent).
 template <class F>
 __device__ __forceinline__ void read_act(const uint8_t* wact, int n, int c, int mr, AOps& ao) {
-    const uint8_t* row = wact + (n < mr ? n : 0) * kActRP * 16;
+    const int r = n < mr ? n : 0;
+    const uint8_t* row = wact + r * kActP * 16;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) ao.a[t] = pair_order(*reinterpret_cast<const mu4*>(row + 2 * F::k0(c, t)));
+    for (int t = 0; t < 8; ++t)
+        ao.a[t] = pair_order(*reinterpret_cast<const mu4*>(row + 16 * ((F::k0(c, t) >> 3) ^ r)));
     group_sums<F>(ao);
 }
 
@@ -472,7 +473,7 @@ struct Chunk {
 // 4 for passes of more than 4 rows, where quarter c holds rows 4c .. 4c + 3).  NB: ring slots.
 template <class F, int R, int NB, typename TA, typename TC>
 __global__ __launch_bounds__(64 * kSlots) void gemv_mfma_kernel(const TA* __restrict__ A, MSegs<TC> sg, int M, int K,
-                                                                 int nrg, int a_vec, int lrows) {
+                                                                 int nrg, int a_vec, int lrows, int bg) {
     using CK = Chunk<F>;
     constexpr bool kF32 = std::is_same<TA, float>::value;
     const int tid = threadIdx.x;
@@ -489,7 +490,7 @@ __global__ __launch_bounds__(64 * kSlots) void gemv_mfma_kernel(const TA* __rest
     // activations through this wave's LDS area (fp16, 16-byte aligned), else straight from memory
     const bool staged = !kF32 && vec;
     uint8_t* ring = mlds;
-    uint8_t* wact = ring + NB * CK::kBytes + w * lrows * kActRP * 16;
+    uint8_t* wact = ring + NB * CK::kBytes + w * lrows * kActP * 16;
     uint8_t* red = ring + NB * CK::kBytes + (kF32 ? 0 : act_bytes(lrows));
     const uint32_t ring_m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring));
     const uint32_t wact_m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(wact));
@@ -508,7 +509,7 @@ __global__ __launch_bounds__(64 * kSlots) void gemv_mfma_kernel(const TA* __rest
     }
     // Issue cursor: batch start ib0 (row groups of this workgroup), its size ibs, window ij, row group iq
     // of the batch, ring slot islot.
-    int ib0 = 0, ibs = min(kBG, mine), ij = 0, iq = 0, islot = 0;
+    int ib0 = 0, ibs = min(bg, mine), ij = 0, iq = 0, islot = 0;
     // Requests the cursor's chunk into its slot and advances the cursor (past the workgroup's last chunk
     // it stays there: the tail requests re-read valid bytes, so every wave issues the same loads).
     auto issue = [&]() {
@@ -537,23 +538,23 @@ __global__ __launch_bounds__(64 * kSlots) void gemv_mfma_kernel(const TA* __rest
             ++ij;
         } else if (ib0 + ibs < mine) {
             ib0 += ibs;
-            ibs = min(kBG, mine - ib0);
+            ibs = min(bg, mine - ib0);
             iq = 0;
             ij = 0;
         }
     };
     // Requests window j's activations (fp16, staged) into this wave's area: the pass's rows of super-block
-    // 8 j + w, lane piece q = 64 i + lane of instruction i (row q / kActRP; the padding piece repeats the
-    // row's last piece).
-    const int act_instr = (mr * kActRP + 63) / 64;
+    // 8 j + w; lane slot q = 64 i + lane of instruction i is row q / 32, slot q % 32, which holds the
+    // row's piece (q % 32) ^ row.
+    const int act_instr = (mr * kActP + 63) / 64;
     auto issue_act = [&](int j) {
         const int sb = min(kSlots * j + w, nsb - 1);
         const TA* base = A + static_cast<size_t>(m0) * K + 256 * sb;
         for (int i = 0; i < act_instr; ++i) {
             const int q = 64 * i + lane;
-            const int r = q / kActRP;
-            const int pc = min(q - r * kActRP, kActP - 1);
-            if (q < mr * kActRP) dma16(base + static_cast<size_t>(r) * K + 8 * pc, wact_m0 + 64 * 16 * i);
+            const int r = q >> 5;
+            const int pc = (q & (kActP - 1)) ^ r;
+            if (q < mr * kActP) dma16(base + static_cast<size_t>(r) * K + 8 * pc, wact_m0 + 64 * 16 * i);
         }
     };
 
@@ -570,8 +571,8 @@ __global__ __launch_bounds__(64 * kSlots) void gemv_mfma_kernel(const TA* __rest
     for (int r = 0; r < R; ++r) eo[r] = 0;
     int cslot = 0;
 
-    for (int b0 = 0; b0 < mine; b0 += kBG) {
-        const int bs = min(kBG, mine - b0);
+    for (int b0 = 0; b0 < mine; b0 += bg) {
+        const int bs = min(bg, mine - b0);
 #pragma unroll
         for (int q = 0; q < kBG; ++q)
 #pragma unroll
@@ -745,22 +746,30 @@ hipError_t mocc(const void* kern, size_t lds, int& blocks) {
 
 
 template <class F, typename TA>
-size_t mlds_bytes(int lrows, int nb) {
+size_t mlds_bytes(int lrows, int nb, int bg) {
     return static_cast<size_t>(nb) * Chunk<F>::kBytes + (std::is_same<TA, float>::value ? 0 : act_bytes(lrows)) +
-           red_bytes(lrows);
+           red_bytes(lrows, bg);
 }
 
-// Activation rows per pass: up to 16, as many as the LDS holds beside a ring of nb weight chunks (rows
-// of a pass share every weight byte loaded; each further pass streams the weights again), balanced over
-// the passes.  0 when not even one row fits.
+// Launch plan for a ring of nb chunks: activation rows per pass (up to 16, as many as the LDS holds
+// beside the ring: rows of a pass share every weight byte loaded, each further pass streams the weights
+// again; balanced over the passes) and row groups per batch (4, or fewer where that lets a pass hold more
+// rows).  rows == 0 when not even one row fits.
+struct MPlan {
+    int rows = 0, bg = 0, passes = 0;
+};
 template <class F, typename TA>
-int pass_rows(int M, int nb, size_t max_lds) {
-    int best = 0;
-    for (int r = 1; r <= min(M, kMRows); ++r)
-        if (mlds_bytes<F, TA>(r, nb) <= max_lds) best = r;
-    if (best == 0) return 0;
-    const int passes = (M + best - 1) / best;
-    return (M + passes - 1) / passes;
+MPlan mplan(int M, int nb, size_t max_lds) {
+    MPlan best;
+    for (int bg = kBG; bg >= 1; bg >>= 1) {
+        int r = 0;
+        for (int t = 1; t <= min(M, kMRows); ++t)
+            if (mlds_bytes<F, TA>(t, nb, bg) <= max_lds) r = t;
+        if (r == 0) continue;
+        const int passes = (M + r - 1) / r;
+        if (best.rows == 0 || passes < best.passes) best = MPlan{(M + passes - 1) / passes, bg, passes};
+    }
+    return best;
 }
 
 template <class F, int R, int NB, typename TA, typename TC>
@@ -769,13 +778,13 @@ const void* mkern() {
 }
 
 template <class F, int R, int NB, typename TA, typename TC>
-hipError_t mlaunch(const void* A, const MSegs<TC>& sg, int nrg, int M, int K, bool a_vec, int lrows, int occ, int cus,
-                   hipStream_t stream) {
-    const size_t lds = mlds_bytes<F, TA>(lrows, NB);
+hipError_t mlaunch(const void* A, const MSegs<TC>& sg, int nrg, int M, int K, bool a_vec, const MPlan& pl, int occ,
+                   int cus, hipStream_t stream) {
+    const size_t lds = mlds_bytes<F, TA>(pl.rows, NB, pl.bg);
     const int fill = max(1, occ * cus);
-    const dim3 grid(min(nrg, fill), (M + lrows - 1) / lrows);
+    const dim3 grid(min(nrg, fill), pl.passes);
     hipLaunchKernelGGL((gemv_mfma_kernel<F, R, NB, TA, TC>), grid, dim3(64 * kSlots), lds, stream,
-                       static_cast<const TA*>(A), sg, M, K, nrg, a_vec ? 1 : 0, lrows);
+                       static_cast<const TA*>(A), sg, M, K, nrg, a_vec ? 1 : 0, pl.rows, pl.bg);
     return hipGetLastError();
 }
 
@@ -784,20 +793,18 @@ hipError_t mlaunch_ring(const void* A, const MSegs<TC>& sg, int nrg, int M, int 
                         hipStream_t stream) {
     // ring of 3 or 4 chunks: fewer passes first, then more chunks in flight per CU (workgroups per CU
     // times ring depth - 1), then the shallower ring
-    const int lr3 = pass_rows<F, TA>(M, 3, di.max_lds), lr4 = pass_rows<F, TA>(M, 4, di.max_lds);
-    if (lr3 == 0) return hipErrorNotSupported;
+    const MPlan p3 = mplan<F, TA>(M, 3, di.max_lds), p4 = mplan<F, TA>(M, 4, di.max_lds);
+    if (p3.rows == 0) return hipErrorNotSupported;
     hipError_t e;
     int occ3 = 0, occ4 = 0;
-    if ((e = mocc(mkern<F, R, 3, TA, TC>(), mlds_bytes<F, TA>(lr3, 3), occ3)) != hipSuccess) return e;
-    const int p3 = (M + lr3 - 1) / lr3;
+    if ((e = mocc(mkern<F, R, 3, TA, TC>(), mlds_bytes<F, TA>(p3.rows, 3, p3.bg), occ3)) != hipSuccess) return e;
     bool use4 = false;
-    if (lr4 > 0) {
-        if ((e = mocc(mkern<F, R, 4, TA, TC>(), mlds_bytes<F, TA>(lr4, 4), occ4)) != hipSuccess) return e;
-        const int p4 = (M + lr4 - 1) / lr4;
-        use4 = p4 < p3 || (p4 == p3 && 3 * occ4 > 2 * occ3);
+    if (p4.rows > 0) {
+        if ((e = mocc(mkern<F, R, 4, TA, TC>(), mlds_bytes<F, TA>(p4.rows, 4, p4.bg), occ4)) != hipSuccess) return e;
+        use4 = p4.passes < p3.passes || (p4.passes == p3.passes && p4.bg >= p3.bg && 3 * occ4 > 2 * occ3);
     }
-    if (use4) return mlaunch<F, R, 4, TA, TC>(A, sg, nrg, M, K, a_vec, lr4, occ4, di.cus, stream);
-    return mlaunch<F, R, 3, TA, TC>(A, sg, nrg, M, K, a_vec, lr3, occ3, di.cus, stream);
+    if (use4) return mlaunch<F, R, 4, TA, TC>(A, sg, nrg, M, K, a_vec, p4, occ4, di.cus, stream);
+    return mlaunch<F, R, 3, TA, TC>(A, sg, nrg, M, K, a_vec, p3, occ3, di.cus, stream);
 }
 
 template <class F, typename TA, typename TC>
@@ -824,7 +831,7 @@ hipError_t mdispatch(const void* A, const void* const* W, void* const* C, const 
     if (e != hipSuccess) return e;
     const bool a_vec = (reinterpret_cast<uintptr_t>(A) & 15u) == 0;
     // R by the rows of a pass: a ring of 3 bounds them from above (a ring of 4 holds no more)
-    const int lrows = pass_rows<F, TA>(M, 3, di.max_lds);
+    const int lrows = mplan<F, TA>(M, 3, di.max_lds).rows;
     if (lrows == 0) return hipErrorNotSupported;
     if (lrows <= 1) return mlaunch_ring<F, 1, TA, TC>(A, sg, nrg, M, K, a_vec, di, stream);
     if (lrows <= 2) return mlaunch_ring<F, 2, TA, TC>(A, sg, nrg, M, K, a_vec, di, stream);
