@@ -293,34 +293,38 @@ def run_prefill(torch, qmm, hip, gen, dev, steps, warmup):
         res[key] = {"us": round(us, 2), "TFLOP/s": round(tf, 1), "frac_f16_peak": round(tf / F16_DENSE_PEAK_TFLOPS, 4)}
         log(f"prefill M=512 {key}: {us:.1f} us, {tf:.1f} TFLOP/s (reference point, dense f16 weights)")
         del w, x32, w16, x16
-    # gate and up as one qmm_gemm_batch call: the two descriptors share the fp16 activations and
-    # run as one launch whose 2 x 14336 output rows fill the GPU with 256 x 256 tiles
+    # gate and up as one qmm_gemm_batch call: the two descriptors share the activations and run as
+    # one launch whose 2 x 14336 output rows fill the GPU with 256 x 256 tiles; fp16 activations and
+    # outputs, then fp32 ones (one f16 conversion pass of the shared activations per call)
     n, k = 14336, 4096
     ws = [make_weight(torch, Q4_K, n, k, gen, dev) for _ in range(2)]
-    x = torch.randn((M, k), device=dev, generator=gen).half()
-    cs = [torch.empty((M, n), device=dev, dtype=torch.float16) for _ in range(2)]
-    arr = (qmm.GemmDesc * 2)()
-    for d, w, c in zip(arr, ws, cs):
-        d.ggml_type, d.A, d.a_dtype, d.W, d.C, d.c_dtype = Q4_K, x.data_ptr(), qmm.DTYPE_F16, w.data_ptr(), c.data_ptr(), qmm.DTYPE_F16
-        d.M, d.N, d.K = M, n, k
-        d.ev_before = d.ev_after = None
-    for _ in range(warmup):
-        qmm.check(qmm.lib().qmm_gemm_batch(arr, 2, stream))
-    torch.cuda.synchronize()
-    a, b = hip.event(), hip.event()
-    hip.record(a, stream)
-    for _ in range(steps):
-        qmm.check(qmm.lib().qmm_gemm_batch(arr, 2, stream))
-    hip.record(b, stream)
-    torch.cuda.synchronize()
-    us = hip.elapsed_ms(a, b) * 1e3 / steps
-    hip.destroy(a)
-    hip.destroy(b)
-    tf = 2.0 * 2 * M * n * k / (us * 1e-6) / 1e12
-    key = "gate_up_fused_q4_k_2x14336x4096_af16"
-    res[key] = {"us": round(us, 2), "TFLOP/s": round(tf, 1), "frac_f16_peak": round(tf / F16_DENSE_PEAK_TFLOPS, 4)}
-    log(f"prefill M=512 {key}: {us:.1f} us, {tf:.1f} TFLOP/s ({tf / F16_DENSE_PEAK_TFLOPS * 100:.1f}% of f16 peak)")
-    del ws, x, cs
+    x32 = torch.randn((M, k), device=dev, generator=gen)
+    for adt, x in (("f16", x32.half()), ("f32", x32)):
+        dt = qmm.DTYPE_F16 if adt == "f16" else qmm.DTYPE_F32
+        cs = [torch.empty((M, n), device=dev, dtype=x.dtype) for _ in range(2)]
+        arr = (qmm.GemmDesc * 2)()
+        for d, w, c in zip(arr, ws, cs):
+            d.ggml_type, d.A, d.a_dtype, d.W, d.C, d.c_dtype = Q4_K, x.data_ptr(), dt, w.data_ptr(), c.data_ptr(), dt
+            d.M, d.N, d.K = M, n, k
+            d.ev_before = d.ev_after = None
+        for _ in range(warmup):
+            qmm.check(qmm.lib().qmm_gemm_batch(arr, 2, stream))
+        torch.cuda.synchronize()
+        a, b = hip.event(), hip.event()
+        hip.record(a, stream)
+        for _ in range(steps):
+            qmm.check(qmm.lib().qmm_gemm_batch(arr, 2, stream))
+        hip.record(b, stream)
+        torch.cuda.synchronize()
+        us = hip.elapsed_ms(a, b) * 1e3 / steps
+        hip.destroy(a)
+        hip.destroy(b)
+        tf = 2.0 * 2 * M * n * k / (us * 1e-6) / 1e12
+        key = f"gate_up_fused_q4_k_2x14336x4096_a{adt}"
+        res[key] = {"us": round(us, 2), "TFLOP/s": round(tf, 1), "frac_f16_peak": round(tf / F16_DENSE_PEAK_TFLOPS, 4)}
+        log(f"prefill M=512 {key}: {us:.1f} us, {tf:.1f} TFLOP/s ({tf / F16_DENSE_PEAK_TFLOPS * 100:.1f}% of f16 peak)")
+        del cs
+    del ws, x32
     return res
 
 
