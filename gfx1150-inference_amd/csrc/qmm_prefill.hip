@@ -1040,6 +1040,56 @@ void prefill_wide_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> s
             return;
         }
     }
+    if constexpr (sizeof(TC) == 4) {
+        if (ksplit == 1) {
+            // fp32 tile through LDS in two passes of 128 rows (128 KiB each: a pass's rows 0..63 in
+            // the first activation stage, 64..127 in the second, 1 KiB per row, 16-byte chunks
+            // XOR-swizzled by row), then each wave stores 32 rows, one 1 KiB row segment per
+            // instruction.
+            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // trailing stage copies have landed
+            uint8_t* const st0 = reinterpret_cast<uint8_t*>(sA0);
+            uint8_t* const st1 = reinterpret_cast<uint8_t*>(sA1);
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                __syncthreads();  // the stages are idle: past the last step (p = 0), or pass 0 is stored
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) {
+                    const int i = 4 * p + ii;
+                    const int r = 32 * ii + l32;  // row within the pass; tile row 128p + r
+                    const float sm = sg.rs != nullptr && m0 + 128 * p + r < M ? sg.rs[m0 + 128 * p + r] : 1.0f;
+                    uint8_t* const row = (r < 64 ? st0 : st1) + (r & 63) * 1024;
+#pragma unroll
+                    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            const int n = 64 * wv + 32 * nb + 8 * g + 4 * h;  // tile-local, multiple of 4
+                            *reinterpret_cast<float4*>(row + (((n >> 2) ^ (r & 31)) << 4)) =
+                                make_float4(acc[nb][i][4 * g] * sm, acc[nb][i][4 * g + 1] * sm,
+                                            acc[nb][i][4 * g + 2] * sm, acc[nb][i][4 * g + 3] * sm);
+                        }
+                }
+                __syncthreads();
+#pragma unroll 4
+                for (int k = 0; k < 32; ++k) {
+                    const int r = 32 * wv + k;
+                    const uint8_t* row = (r < 64 ? st0 : st1) + (r & 63) * 1024;
+                    const float4 v = *reinterpret_cast<const float4*>(row + ((lane ^ (r & 31)) << 4));
+                    const int gm = m0 + 128 * p + r, gn = n0 + 4 * lane;  // columns 4 lane .. + 3
+                    if (gm >= M || gn >= N) continue;
+                    float* dst = reinterpret_cast<float*>(C) + static_cast<size_t>(gm) * ldc + gn;
+                    if (gn + 3 < N && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+                        *reinterpret_cast<float4*>(dst) = v;
+                    } else {
+                        const float vf[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (gn + e < N) dst[e] = vf[e];
+                    }
+                }
+            }
+            return;
+        }
+    }
 
     // D element v of tile (nb, i): weight row n = n0 + 64wv + 32nb + 8(v/4) + 4h + v%4,
     // activation row m = m0 + 32i + l32.

@@ -8,9 +8,10 @@ type and is checked against the oracle:
   within max_i|y_i - y64_i| / max_i|y64_i| <= 1e-3 of the fp64 product on the exact weights
   (the bar includes the fp16 rounding of the outputs, at most 2^-11 relative), and every
   output bit-identical to the matrix's single qmm_gemm call;
-* the 8B prefill's fused gate/up (2 x 14336 x 4096 Q4_K, M = 512, fp16 in and out: 224 tiles
-  of 256 x 256): sampled output columns within 1e-3 of the fp64 product of the kernel's f16
-  operands (oracle.matmul_f16_operands; the bar is the fp16 output rounding plus fp32
+* the 8B prefill's fused gate/up (2 x 14336 x 4096 Q4_K, M = 512, 224 tiles of 256 x 256), with
+  fp16 activations and outputs and with fp32 activations and outputs: sampled output columns
+  within 1e-3 of the fp64 product of the kernel's f16 operands (oracle.matmul_f16_operands;
+  the bar is the fp16 rounding of the outputs or of the fp32 activations plus fp32
   accumulation) and within 1e-2 of fp64 on the exact weights.
 """
 
@@ -85,15 +86,17 @@ def test_70b_fused_gemv_launch(dev, name, M):
         assert O.max_rel_err(y.float().numpy().astype(np.float64)[:, rows], y64) <= GEMV_TOL, (name, M, n)
 
 
-def test_8b_prefill_fused_gate_up_launch(dev):
+@pytest.mark.parametrize("adt", ["f16", "f32"])
+def test_8b_prefill_fused_gate_up_launch(dev, adt):
     import torch
     t, M, N, K = O.GGML_Q4_K, 512, 14336, 4096
     rng = np.random.default_rng(1400)
-    x = rng.standard_normal((M, K)).astype(np.float16)
+    print(f"8B prefill fused gate+up a{adt}", flush=True)
+    x = rng.standard_normal((M, K)).astype(np.float16 if adt == "f16" else np.float32)
     A = to_dev(x, dev)
     raws = [O.synth_weights(t, N, K, rng) for _ in range(2)]
     Ws = [to_dev(r, dev) for r in raws]
-    Cs = [torch.empty((M, N), device=dev, dtype=torch.float16) for _ in range(2)]
+    Cs = [torch.empty((M, N), device=dev, dtype=A.dtype) for _ in range(2)]
     batch([(t, A, w, c, N, K) for w, c in zip(Ws, Cs)])
     cols = np.unique(np.concatenate([[0, N - 1, 255, 256], rng.choice(N, size=36, replace=False)]))
     xa = x.astype(np.float32)

@@ -101,10 +101,10 @@ def test_gemv_fp32_beyond_f16_range(dev, t, K):
 
 
 @pytest.mark.parametrize("t", [O.GGML_Q4_K, O.GGML_Q6_K, O.GGML_Q8_0])
-@pytest.mark.parametrize("M", [48, 20])  # 128-row and 32-row tiles
+@pytest.mark.parametrize("M", [256, 48, 20])  # 256-row (wide, 128 tiles), 128-row and 32-row tiles
 def test_prefill_fp32_beyond_f16_range(dev, t, M):
     rng = np.random.default_rng(7 + t + M)
-    N, K = 256, 4096
+    N, K = (32768, 256) if M >= 256 else (256, 4096)
     w, w64 = weights(t, N, K, rng)
     x = rng.standard_normal((M, K)).astype(np.float32)
     x[0] *= 1e6

@@ -55,10 +55,12 @@ def shapes(t):
 
 def wide_shapes(t):
     # The 256 x 256 tile serves M >= 256 when its tiles cover at least half the CUs (>= 128 tiles):
-    # exact tiles, ragged M / N with a K tail, and a K long enough to split over workgroups.
+    # exact tiles, ragged M / N with a K tail, a K long enough to split over workgroups, and
+    # fp32 outputs with N % 4 == 2 (rows whose 16-byte column groups straddle the row end or
+    # start 8 bytes off a 16-byte boundary, stored element by element).
     if t in (O.GGML_Q4_K, O.GGML_Q6_K):
-        return [(256, 32768, 256), (400, 16428, 1280), (256, 32768, 4096)]
-    return [(256, 32768, 128), (448, 16420, 544), (256, 32768, 4096)]
+        return [(256, 32768, 256), (400, 16428, 1280), (256, 32768, 4096), (450, 32770, 256)]
+    return [(256, 32768, 128), (448, 16420, 544), (256, 32768, 4096), (450, 32770, 96)]
 
 
 def sampled_cols(rng, N):
