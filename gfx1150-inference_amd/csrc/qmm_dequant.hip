@@ -4,11 +4,14 @@
 //
 // Replaces dequantize_{q4_0,q8_0,q4_k,q6_k}_kernel (reference src/kernels/dequantize.hip:68-88,
 // 213-229, 335-371, 508-544), which run one thread per block with byte loads and strided stores.
-// Here 16 lanes share a unit of 256 weights (a Q4_K / Q6_K super-block, eight Q4_0 / Q8_0
-// blocks): lane j produces weights 16j..16j+15 of the unit, read with at most two 16-byte loads
-// (its half of a Q4_K qs chunk and the super-block header; its Q6_K ql and qh slices; its Q8_0 /
-// Q4_0 block's codes), and writes them as contiguous 16-byte stores, so a wave reads four units'
-// packed bytes and writes 2 KiB (fp16) of contiguous output.  HBM-bound: packed bytes in, output out.
+// Here 16 lanes share a unit of 256 weights (a Q4_K super-block, eight Q4_0 / Q8_0 blocks): lane j
+// produces weights 16j..16j+15 of the unit, read with at most two 16-byte loads (its half of a
+// Q4_K qs chunk and the super-block header; its Q8_0 / Q4_0 block's codes), and writes them as
+// contiguous 16-byte stores, so a wave reads four units' packed bytes and writes 2 KiB (fp16) of
+// contiguous output.  Q6_K has a kernel of its own (eight lanes per super-block, below).
+// HBM-bound: packed bytes in, output out.
+#include <type_traits>
+
 #include "qmm_device.h"
 
 namespace qmm {
@@ -39,39 +42,6 @@ __device__ __forceinline__ void unit_weights(const uint8_t* __restrict__ W, int6
         const int sh = 4 * (s & 1);
 #pragma unroll
         for (int i = 0; i < 16; ++i) w[i] = __fmaf_rn(a, static_cast<float>((byte_of(q, i) >> sh) & 15u), -b);
-    } else if constexpr (T == QMM_TYPE_Q6_K) {
-        // half n = j/8, quarter t = (j/2)%4, column half h = j%2: weights 128n + 32t + 16h + i
-        const uint8_t* blk = W + u * kBytesQ6_K;
-        const int n = j >> 3, t = (j >> 1) & 3, h = j & 1;
-        // A block 2 bytes past a 4-byte boundary (every other one) is read with 4-aligned loads
-        // from 2 bytes lower, plus the dword after each slice, and shifted back (v_alignbyte):
-        // 16-byte loads at such addresses made this kernel 10 % slower.  Never below W: the
-        // first unit keeps its loads as they are.
-        const int f = u > 0 && (reinterpret_cast<uintptr_t>(blk) & 3) == 2 ? 2 : 0;
-        const uint8_t* pl = blk + 64 * n + 32 * (t & 1) + 16 * h;
-        const uint8_t* ph = blk + 128 + 32 * n + 16 * h;
-        u32x4d ql = ld16(pl - f), qh = ld16(ph - f);
-        uint32_t tl, th;
-        __builtin_memcpy(&tl, pl + 12 + f, 4);  // f = 2: the dword after the slice; f = 0: unused
-        __builtin_memcpy(&th, ph + 12 + f, 4);
-        {
-            const u32x4d a = ql, b = qh;
-            ql[0] = __builtin_amdgcn_alignbyte(a[1], a[0], f);
-            ql[1] = __builtin_amdgcn_alignbyte(a[2], a[1], f);
-            ql[2] = __builtin_amdgcn_alignbyte(a[3], a[2], f);
-            ql[3] = __builtin_amdgcn_alignbyte(tl, a[3], f);
-            qh[0] = __builtin_amdgcn_alignbyte(b[1], b[0], f);
-            qh[1] = __builtin_amdgcn_alignbyte(b[2], b[1], f);
-            qh[2] = __builtin_amdgcn_alignbyte(b[3], b[2], f);
-            qh[3] = __builtin_amdgcn_alignbyte(th, b[3], f);
-        }
-        const float d = half_bits_to_float(blk[208] | (static_cast<uint32_t>(blk[209]) << 8));
-        const float a = d * static_cast<float>(static_cast<int8_t>(blk[192 + 8 * n + h + 2 * t]));
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int q = static_cast<int>(((byte_of(ql, i) >> (4 * (t >> 1))) & 15u) | (((byte_of(qh, i) >> (2 * t)) & 3u) << 4)) - 32;
-            w[i] = a * static_cast<float>(q);
-        }
     } else if constexpr (T == QMM_TYPE_Q8_0) {
         const uint8_t* blk = W + (8 * u + (j >> 1)) * kBytesQ8_0;
         const u32x4d q = ld16(blk + 2 + 16 * (j & 1));
@@ -120,21 +90,87 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
     }
 }
 
+// Q6_K, eight lanes per super-block: lane (hf, h) of super-block u produces weights
+// 128 hf + 32 t + 8 h + (0..7) for the four groups t, so that one 8-byte slice of ql at
+// 64 hf + 8 h (groups 0 and 2), one at 64 hf + 32 + 8 h (groups 1 and 3) and one of qh at
+// 128 + 32 hf + 8 h (all four) serve 32 weights, with the half's eight sub-scales and d: five loads
+// per 32 weights, four 16-byte stores of 8 consecutive outputs.  A super-block with an odd index
+// starts 2 bytes past a 4-byte boundary: its slices are read as 12 bytes from the boundary below
+// (f = 2) and shifted back (v_alignbyte); 12-byte reads stay inside the block for either f.
+template <int OUT>
+__global__ __launch_bounds__(256) void dequant_q6k_kernel(const uint8_t* __restrict__ W, void* __restrict__ out,
+                                                          int64_t n) {
+    const int64_t lid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t u = lid >> 3;
+    if (256 * u >= n) return;  // n % 256 == 0
+    const int hf = static_cast<int>(lid >> 2) & 1, h = static_cast<int>(lid) & 3;
+    const uint8_t* blk = W + u * kBytesQ6_K;
+    // never below W: the first block keeps its loads as they lie
+    const int f = u > 0 && (reinterpret_cast<uintptr_t>(blk) & 3) == 2 ? 2 : 0;
+    auto ld8 = [&](const uint8_t* p) {  // 8 bytes at p
+        uint32_t v[3];
+        __builtin_memcpy(v, p - f, 12);
+        return make_uint2(__builtin_amdgcn_alignbyte(v[1], v[0], f), __builtin_amdgcn_alignbyte(v[2], v[1], f));
+    };
+    const uint2 qa = ld8(blk + 64 * hf + 8 * h);       // ql[l], l = 8h..8h+7: groups 0 (low), 2 (high)
+    const uint2 qb = ld8(blk + 64 * hf + 32 + 8 * h);  // ql[l + 32]: groups 1, 3
+    const uint2 qh = ld8(blk + 128 + 32 * hf + 8 * h);
+    uint32_t sv[3];  // sub-scales 8 hf .. 8 hf + 7 at bytes 4 - f ..
+    __builtin_memcpy(sv, blk + 188 + 8 * hf + f, 12);
+    const uint32_t s0 = f ? __builtin_amdgcn_alignbyte(sv[1], sv[0], 2) : sv[1];
+    const uint32_t s1 = f ? __builtin_amdgcn_alignbyte(sv[2], sv[1], 2) : sv[2];
+    uint16_t dv;
+    __builtin_memcpy(&dv, blk + 208, 2);
+    const float d = half_bits_to_float(dv);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        // sc[8 hf + 2t + l/16], l/16 = h/2
+        const int si = 2 * t + (h >> 1);
+        const uint32_t sw = si < 4 ? s0 : s1;
+        const float a = d * static_cast<float>(static_cast<int8_t>(sw >> (8 * (si & 3))));
+        const uint2 ql = (t & 1) ? qb : qa;
+        float w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t lb = ((i < 4 ? ql.x : ql.y) >> (8 * (i & 3))) & 0xFFu;
+            const uint32_t hb = ((i < 4 ? qh.x : qh.y) >> (8 * (i & 3))) & 0xFFu;
+            const int q = static_cast<int>(((lb >> (4 * (t >> 1))) & 15u) | (((hb >> (2 * t)) & 3u) << 4)) - 32;
+            w[i] = a * static_cast<float>(q);
+        }
+        const int64_t first = 256 * u + 128 * hf + 32 * t + 8 * h;
+        if constexpr (OUT == QMM_DTYPE_F32) {
+            float4* o = reinterpret_cast<float4*>(static_cast<float*>(out) + first);
+            o[0] = make_float4(w[0], w[1], w[2], w[3]);
+            o[1] = make_float4(w[4], w[5], w[6], w[7]);
+        } else {
+            uint32_t pk[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t lo = OUT == QMM_DTYPE_F16 ? float_to_half_bits(w[2 * i]) : float_to_bf16_bits(w[2 * i]);
+                const uint32_t hi = OUT == QMM_DTYPE_F16 ? float_to_half_bits(w[2 * i + 1]) : float_to_bf16_bits(w[2 * i + 1]);
+                pk[i] = lo | (hi << 16);
+            }
+            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + first) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        }
+    }
+}
+
 template <int T>
 hipError_t launch_t(const void* W, void* out, int out_dtype, int64_t n, hipStream_t stream) {
-    const dim3 block(256);
-    const dim3 grid(static_cast<unsigned>((n / 16 + 255) / 256));
+    // Q6_K: one lane per 32 outputs; the other formats: one lane per 16
+    const dim3 grid(static_cast<unsigned>((n / (T == QMM_TYPE_Q6_K ? 32 : 16) + 255) / 256));
     const uint8_t* w = static_cast<const uint8_t*>(W);
+    auto go = [&](auto oc) {
+        constexpr int OUT = decltype(oc)::value;
+        if constexpr (T == QMM_TYPE_Q6_K)
+            hipLaunchKernelGGL((dequant_q6k_kernel<OUT>), grid, dim3(256), 0, stream, w, out, n);
+        else
+            hipLaunchKernelGGL((dequant_kernel<T, OUT>), grid, dim3(256), 0, stream, w, out, n);
+    };
     switch (out_dtype) {
-        case QMM_DTYPE_F32:
-            hipLaunchKernelGGL((dequant_kernel<T, QMM_DTYPE_F32>), grid, block, 0, stream, w, out, n);
-            break;
-        case QMM_DTYPE_F16:
-            hipLaunchKernelGGL((dequant_kernel<T, QMM_DTYPE_F16>), grid, block, 0, stream, w, out, n);
-            break;
-        default:
-            hipLaunchKernelGGL((dequant_kernel<T, QMM_DTYPE_BF16>), grid, block, 0, stream, w, out, n);
-            break;
+        case QMM_DTYPE_F32: go(std::integral_constant<int, QMM_DTYPE_F32>{}); break;
+        case QMM_DTYPE_F16: go(std::integral_constant<int, QMM_DTYPE_F16>{}); break;
+        default: go(std::integral_constant<int, QMM_DTYPE_BF16>{}); break;
     }
     return hipGetLastError();
 }
