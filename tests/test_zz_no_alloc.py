@@ -29,8 +29,10 @@ def test_noalloc_matches_gemm_twice(cuda, a32):
     import qmm
     lib = qmm.lib()
     rng = np.random.default_rng(4242 + a32)
-    # each call smaller than the one before; the last runs the 32-row tile with K split 8 ways
-    cases = [(O.GGML_Q6_K, 512, 4096, 14336), (O.GGML_Q4_K, 64, 1024, 4096), (O.GGML_Q4_K, 24, 512, 8192)]
+    # each call smaller than the one before; the second runs the 256 x 256 tile (128 tiles, no K
+    # split, its output tile through LDS), the last the 32-row tile with K split 8 ways
+    cases = [(O.GGML_Q6_K, 512, 4096, 14336), (O.GGML_Q4_K, 256, 32768, 256), (O.GGML_Q4_K, 64, 1024, 4096),
+             (O.GGML_Q4_K, 24, 512, 8192)]
     for t, M, N, K in cases:
         print(f"noalloc case type={t} M={M} N={N} K={K} fp32_in={a32}", flush=True)
         raw = O.synth_weights(t, N, K, rng)
