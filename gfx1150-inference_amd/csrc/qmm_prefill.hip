@@ -828,8 +828,8 @@ template <class P, typename TC>
 __global__ __launch_bounds__(kWThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void prefill_wide_kernel(const _Float16* __restrict__ A16, int lda, PfSegs<TC> sg, float* __restrict__ part_base, int M,
                          int K, int klen, int tiles_m, int tiles_n, int ksplit) {
-    // two separate arrays (not one [2][...] array) so that the compiler's tracking of the direct
-    // loads into one of them adds no waits to the reads of the other
+    // one array per stage (not one [2][...] array); the step body is instantiated per stage, so each
+    // of its LDS addresses is a fixed offset into one array
     __shared__ __align__(16) u32x4p sA0[kWH * kWChunksPerHalf];
     __shared__ __align__(16) u32x4p sA1[kWH * kWChunksPerHalf];
 
