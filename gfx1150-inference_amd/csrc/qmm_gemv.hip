@@ -990,11 +990,12 @@ struct WinSlot {
     static constexpr int kBytes = kPieces * 16;
 };
 
-// 16 bytes at global address g -> LDS at m0 + 16 * lane (m0 = the wave-uniform `lds`).  The
-// compiler does not track these loads: the caller waits for them with an explicit vmcnt.
+// 16 bytes at global address g -> LDS at m0 + 16 * lane (m0 = the wave-uniform `lds`, an operand
+// that the compiler moves into m0).  The compiler does not track these loads: the caller waits for
+// them with an explicit vmcnt.
 __device__ __forceinline__ void win_direct_load16(const void* g, const void* lds) {
     const uint32_t la = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
-    __asm__ volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(la) : "memory", "m0");
+    __asm__ volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(la) : "memory");
 }
 
 template <int N>

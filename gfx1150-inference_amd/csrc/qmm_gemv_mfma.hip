@@ -411,11 +411,12 @@ template <>
 __device__ __forceinline__ void mstore<__half>(__half* p, float v) { *reinterpret_cast<uint16_t*>(p) = float_to_half_bits(v); }
 
 // Direct global -> LDS load of 16 bytes per lane (global_load_lds_dwordx4): lane l's bytes land at
-// LDS address m0 + 16 l.  The compiler does not track these loads; they are waited for with explicit
-// vmcnt counts (vector memory operations complete in issue order, so waiting until at most N remain
-// outstanding completes every operation issued before the last N).
+// LDS address m0 + 16 l (m0 is an operand, so the compiler sets it).  The compiler does not track
+// these loads; they are waited for with explicit vmcnt counts (vector memory operations complete in
+// issue order, so waiting until at most N remain outstanding completes every operation issued before
+// the last N).
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds_m0) {
-    __asm__ volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_m0) : "memory", "m0");
+    __asm__ volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_m0) : "memory");
 }
 template <int N>
 __device__ __forceinline__ void vm_wait() {

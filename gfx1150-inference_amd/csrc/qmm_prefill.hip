@@ -802,13 +802,14 @@ constexpr int kWThreads = 256;  // 4 waves, one per SIMD
 constexpr int kWChunksPerHalf = kWBM * 64 / 8;  // 16-byte chunks per 64-k half stage = 2048
 
 // Direct global -> LDS load of 16 bytes per lane (global_load_lds_dwordx4): lane l's bytes land
-// at the wave-uniform LDS address of `lds` plus 16 l.  Issued as inline assembly, so the
-// compiler's wait counting covers only the ordinary loads and LDS reads; the caller waits for
-// these with an explicit vmcnt(0) before the barrier that publishes the stage.  (Memory operations
-// unknown to the compiler can only make its own vmcnt / lgkmcnt waits wait longer.)
+// at the wave-uniform LDS address of `lds` (passed in m0 through an operand, so the compiler sets
+// m0) plus 16 l.  Issued as inline assembly, so the compiler's wait counting covers only the
+// ordinary loads and LDS reads; the caller waits for these with an explicit vmcnt(0) before the
+// barrier that publishes the stage.  (Memory operations unknown to the compiler can only make its
+// own vmcnt / lgkmcnt waits wait longer.)
 __device__ __forceinline__ void lds_direct_load16(const void* g, const u32x4p* lds) {
     const uint32_t la = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));  // LDS offset
-    __asm__ volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(la) : "memory", "m0");
+    __asm__ volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(la) : "memory");
 }
 
 // Instruction interleave of one wide sub-step: sixteen rounds of one MFMA, one LDS read (eight
