@@ -125,24 +125,27 @@ struct MQ4K {
     };
     __device__ static Pre prep(const Raw& r, int c) {
         Pre p;
+        // Sub-blocks j = 2c + g.  j < 4 (c < 2): 6-bit scale and min at byte j of words 1 and 2.
+        // j >= 4: low 4 bits in byte j - 4 of word 3 (scale: low nibble, min: high nibble), top 2 bits
+        // in bits 6..7 of byte j - 4 of words 1 and 2.  Per lane: the word of the low bits and the bit
+        // offsets (loop-invariant), then three field extracts per value.
+        const bool lo = c < 2;
+        const uint32_t ws = lo ? r.h.y : r.h.w, wm = lo ? r.h.z : r.h.w;
         uint32_t sc[2], mn[2];
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
-            const int sh = 8 * ((2 * c + g) & 3);
-            const uint32_t sc_lo = (r.h.y >> sh) & 63u;
-            const uint32_t mn_lo = (r.h.z >> sh) & 63u;
-            const uint32_t sc_hi = ((r.h.w >> sh) & 15u) | (((r.h.y >> (sh + 6)) & 3u) << 4);
-            const uint32_t mn_hi = ((r.h.w >> (sh + 4)) & 15u) | (((r.h.z >> (sh + 6)) & 3u) << 4);
-            sc[g] = c < 2 ? sc_lo : sc_hi;
-            mn[g] = c < 2 ? mn_lo : mn_hi;
+            const uint32_t b = 8 * ((2 * c + g) & 3);
+            const uint32_t top = b + (lo ? 4u : 6u);
+            sc[g] = __builtin_amdgcn_ubfe(ws, b, 4) | (__builtin_amdgcn_ubfe(r.h.y, top, 2) << 4);
+            mn[g] = __builtin_amdgcn_ubfe(wm, b + (lo ? 0u : 4u), 4) | (__builtin_amdgcn_ubfe(r.h.z, top, 2) << 4);
         }
-        const _Float16 s0 = static_cast<_Float16>(static_cast<float>(sc[0]));
-        const _Float16 s1 = static_cast<_Float16>(static_cast<float>(sc[1]));
+        const _Float16 s0 = static_cast<_Float16>(static_cast<uint16_t>(sc[0]));  // exact: < 64
+        const _Float16 s1 = static_cast<_Float16>(static_cast<uint16_t>(sc[1]));
         p.s_lo = pair_of(s0);
         p.o_lo = pair_of(s0 * static_cast<_Float16>(-1024.0f));
         p.s_hi = pair_of(s1 * static_cast<_Float16>(0.0625f));
         p.o_hi = pair_of(s1 * static_cast<_Float16>(-64.0f));
-        const _Float16 f0 = static_cast<_Float16>(static_cast<float>(mn[0])), f1 = static_cast<_Float16>(static_cast<float>(mn[1]));
+        const _Float16 f0 = static_cast<_Float16>(static_cast<uint16_t>(mn[0])), f1 = static_cast<_Float16>(static_cast<uint16_t>(mn[1]));
         const _Float16 r11 = static_cast<_Float16>(1.0f / 2048.0f), z = static_cast<_Float16>(0.0f);
         p.bu = mh8{f0, f1, f0 * r11, f1 * r11, z, z, z, z};
         p.d = half_bits_to_float(r.h.x);
