@@ -89,8 +89,10 @@ def test_dequant_synthetic_bit_exact(dev, t, out):
 @pytest.mark.parametrize("t", TYPES)
 @pytest.mark.parametrize("blocks", [1, 3, 9, 13, 257])
 def test_dequant_ragged_sizes_leave_tail_untouched(dev, t, blocks):
-    """Sizes that are not whole multiples of 256 weights (Q4_0 / Q8_0) or of eight super-blocks,
-    written into a larger buffer: values bit-exact, the sentinel past num_elements untouched."""
+    """Sizes that are not whole multiples of 256 weights (Q4_0 / Q8_0), of eight super-blocks or of
+    the 16-super-block batches the K-quant kernels stage through LDS (257 blocks: 16 batches, then
+    one block read straight from memory), written into a larger buffer: values bit-exact, the
+    sentinel past num_elements untouched."""
     import torch
     import qmm
     rng = np.random.default_rng(31 * blocks + t)
@@ -113,8 +115,9 @@ def test_dequant_ragged_sizes_leave_tail_untouched(dev, t, blocks):
 @pytest.mark.parametrize("t", TYPES)
 def test_dequant_weights_2_bytes_off_bit_exact(dev, t):
     """Packed weights starting 2 bytes past a 4-byte boundary (and at one), odd and even block
-    counts: the Q6_K dequantizer reads blocks that sit 2 bytes off a 4-byte boundary with aligned
-    loads and shifts them back, never below the first block.  Values bit-exact."""
+    counts: the Q6_K dequantizers read blocks that sit 2 bytes off a 4-byte boundary with aligned
+    reads and shift them back, never below the first block; 16-byte aligned K-quant weights go
+    through the LDS-staged kernels, the others straight from memory.  Values bit-exact."""
     import torch
     import qmm
     rng = np.random.default_rng(77 + t)
