@@ -421,6 +421,13 @@ __device__ __forceinline__ void mstore<__half>(__half* p, float v) { *reinterpre
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds_m0) {
     __asm__ volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_m0) : "memory");
 }
+// The same from a buffer (raw, stride 0): 16 bytes at voff of the resource, where a read at or past the
+// resource's size returns zeros; the base address and size live in scalar registers, so a lane's
+// address is one 32-bit offset.
+constexpr uint32_t kBufferWord3 = 0x00020000u;  // buffer resource word 3: raw dword access
+__device__ __forceinline__ void dma16b(mu4 rsrc, uint32_t voff, uint32_t lds_m0) {
+    __asm__ volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(lds_m0) : "memory");
+}
 template <int N>
 __device__ __forceinline__ void vm_wait() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -502,14 +509,15 @@ __global__ __launch_bounds__(64 * kSlots) void gemv_mfma_kernel(const TA* __rest
     const int qrows = (mr + 3) >> 2;  // lane quarters holding output rows
 
     // Per-lane constants of the chunk copies: instruction k moves this lane's piece q = 64 k + lane of the
-    // wave's two rows (row r = q / kRP, piece pc of it; the row's padding piece repeats its last piece).
-    int lane_off[CK::kInstr];
+    // wave's two rows (row r = q / kRP, piece pc of it; the row's padding piece repeats its last piece),
+    // at byte lane_vo[k] from the window's start in the first row.
+    uint32_t lane_vo[CK::kInstr];
     bool lane_r1[CK::kInstr];
 #pragma unroll
     for (int k = 0; k < CK::kInstr; ++k) {
         const int q = 64 * k + lane;
         lane_r1[k] = q >= CK::kRP;
-        lane_off[k] = 16 * min(q - (lane_r1[k] ? CK::kRP : 0), CK::kP - 1);
+        lane_vo[k] = 16 * min(q - (lane_r1[k] ? CK::kRP : 0), CK::kP - 1) + (lane_r1[k] ? row_bytes : 0);
     }
     // Issue cursor: batch start ib0 (row groups of this workgroup), its size ibs, window ij, row group iq
     // of the batch, ring slot islot.
@@ -522,18 +530,20 @@ __global__ __launch_bounds__(64 * kSlots) void gemv_mfma_kernel(const TA* __rest
         TC* Cs;
         int N, g0;
         seg_pick(sg, g, W, Cs, N, g0);
-        // the wave's two source rows (row 2w + 1 clamped to the segment's last row: then d1 = 0)
+        // the wave's two source rows (row 2w + 1 clamped to the segment's last row)
         const int r0 = min((g - g0) * kRows + 2 * w, N - 1);
         const int r1 = min(r0 + 1, N - 1);
-        const uint8_t* src0 = W + static_cast<size_t>(r0) * row_bytes;
-        const int d1 = (r1 - r0) * row_bytes;
         const int cb = ij * kSlots * F::kBlockBytes;
+        // the window of row r0 through the end of row r1 as a buffer: the last window's padding pieces
+        // (unused) read past a row's end into the next row or, past row r1, zeros; with one row left
+        // (r1 = r0) the second row's pieces read zeros (a row past the segment, never stored)
+        const uint64_t base = reinterpret_cast<uint64_t>(W + static_cast<size_t>(r0) * row_bytes + cb);
+        const mu4 rs = {static_cast<uint32_t>(base), static_cast<uint32_t>(base >> 32) & 0xFFFFu,
+                        static_cast<uint32_t>((r1 - r0 + 1) * row_bytes - cb), kBufferWord3};
         const uint32_t dst = ring_m0 + static_cast<uint32_t>(islot * CK::kBytes + 2 * w * CK::kRP * 16);
 #pragma unroll
-        for (int k = 0; k < CK::kInstr; ++k) {
-            const int off = min(cb + lane_off[k], row_bytes - 16) + (lane_r1[k] ? d1 : 0);
-            if (64 * k + 64 <= 2 * CK::kRP || 64 * k + lane < 2 * CK::kRP) dma16(src0 + off, dst + 64 * 16 * k);
-        }
+        for (int k = 0; k < CK::kInstr; ++k)
+            if (64 * k + 64 <= 2 * CK::kRP || 64 * k + lane < 2 * CK::kRP) dma16b(rs, lane_vo[k], dst + 64 * 16 * k);
         islot = islot + 1 == NB ? 0 : islot + 1;
         if (iq + 1 < ibs) {
             ++iq;
