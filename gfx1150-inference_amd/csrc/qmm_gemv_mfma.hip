@@ -10,12 +10,14 @@
 //     Q4_K the 16-byte header and the 32-byte qs chunk c (sub-blocks 2c, 2c + 1); Q6_K the
 //     (half c / 2, 16-column half c % 2) slice: 16 + 16 bytes of ql, 16 of qh, the 8 sub-scale bytes
 //     of that half and d.
-//   * Codes become exact f16 integers s * q: one v_and_or_b32 turns two codes into (1024 + q) or
-//     (1024 + 16q) (0x6400 | bits), one v_pk_fma_f16 with (s, -1024 s) or (s / 16, -64 s) leaves
-//     s * q exactly (|s * q| <= 2048, so no rounding).  Q4_K: s = the 6-bit sub-scale.  Q6_K: the
-//     6-bit code u = ul + 16 uh is split into its nibble ul and its 2-bit top uh, s = the int8
-//     sub-scale, and two MFMA chains add s * ul and s * uh (combined as T1 + 16 T2).  All products
-//     of the MFMA are exact; its fp32 sums round.
+//   * Q4_K codes become exact f16 integers s * q: one v_and_or_b32 turns two codes into (1024 + q)
+//     or (1024 + 16q) (0x6400 | bits), one v_pk_fma_f16 with (s, -1024 s) or (s / 16, -64 s) leaves
+//     s * q exactly (s the 6-bit sub-scale, |s * q| <= 945).  Q6_K: two v_perm make the f16 pairs
+//     (1024 + u) of the byte-assembled 6-bit codes, v_pk_add_f16 with -1056 leaves u - 32 exactly and
+//     v_pk_mul_f16 by the int8 sub-scale s gives s (u - 32), exact while |s (u - 32)| <= 2048 and
+//     otherwise rounded once (|s (u - 32)| <= 4096: an error of at most 1, below the f16 rounding of
+//     d s (u - 32) in the reference's dequantized weights).  The MFMA's products of these operands
+//     are exact; its fp32 sums round.
 //   * Per super-block and row: y += d * T - c2 * U, where U is a second MFMA over the per-group sums
 //     of the staged activations (held as f16 hi + lo pairs of sum / 32) against the group minima
 //     (Q4_K: the 6-bit mins, c2 = 32 dmin) or the sub-scales (Q6_K's code offset 32: c2 = 1024 d).
@@ -172,14 +174,13 @@ struct MQ4K {
 
 // Q6_K (reference block_q6_k, src/kernels/dequantize.hip:39-44): quarter c = (half hf = c / 2, column
 // half h = c % 2): weights 128 hf + 32 t + 16 h + j, t < 4, j < 16; sub-scale sc[8 hf + h + 2 t].
-// Step st = 2 t + (j >= 8).  The 6-bit code u (w = d sc (u - 32)) is assembled bytewise and two
-// v_perm make the f16 pairs (1024 + u); the int8 sub-scale is split as sc = 16 sh + sl (sl = sc & 15,
-// sh = sc >> 4), so that sl (u - 32) and sh (u - 32) are exact f16 integers (|.| <= 480, 256): two
-// chains, T = T1 + 16 T2, and the code offset needs no second sum.
+// Step st = 2 t + (j >= 8).  The 6-bit code u (w = d sc (u - 32)) is assembled bytewise, two v_perm
+// make the f16 pairs (1024 + u), and the B operand is sc (u - 32): one chain, and the code offset
+// needs no second sum.
 struct MQ6K {
     static constexpr int kType = QMM_TYPE_Q6_K;
     static constexpr int kBlockBytes = kBytesQ6_K;
-    static constexpr int kChains = 2;
+    static constexpr int kChains = 1;
     static constexpr bool kSums = false;
     static constexpr int kGroupK = 16;
     struct Raw {
@@ -206,10 +207,9 @@ struct MQ6K {
         return r;
     }
     struct Pre {
-        uint32_t sl[4], ol[4];  // (sl, sl), (-1056 sl, ..) per t
-        uint32_t sh[4], oh[4];  // (sh, sh), (-1056 sh, ..) per t
-        mh8 bu;                 // unused (no group sums)
-        float d, c2;            // d, 0
+        uint32_t s[4];  // (sc, sc) per t
+        mh8 bu;         // unused (no group sums)
+        float d, c2;    // d, 0
     };
     __device__ static Pre prep(const Raw& r, int c) {
         Pre p;
@@ -217,20 +217,15 @@ struct MQ6K {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const uint32_t w = t < 2 ? r.s0 : r.s1;
-            const int sc = static_cast<int8_t>(w >> (8 * (h + 2 * (t & 1))));
-            const _Float16 lo = static_cast<_Float16>(static_cast<float>(sc & 15));
-            const _Float16 hi = static_cast<_Float16>(static_cast<float>(sc >> 4));
-            p.sl[t] = pair_of(lo);
-            p.ol[t] = pair_of(lo * static_cast<_Float16>(-1056.0f));
-            p.sh[t] = pair_of(hi);
-            p.oh[t] = pair_of(hi * static_cast<_Float16>(-1056.0f));
+            const _Float16 sc = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>(w >> (8 * (h + 2 * (t & 1))))));
+            p.s[t] = pair_of(sc);
         }
         p.d = half_bits_to_float(r.d);
         p.c2 = 0.0f;
         return p;
     }
-    // B operands of step st: chain 0 sl (u - 32), chain 1 sh (u - 32); bytes 8 (st & 1) .. + 7 of the
-    // lane's slices (weights j = 8 (st & 1) + 0..7 of group t = st / 2).
+    // B operand of step st: sc (u - 32) for bytes 8 (st & 1) .. + 7 of the lane's slices (weights
+    // j = 8 (st & 1) + 0..7 of group t = st / 2).
     __device__ static void steps(const Raw& r, const Pre& p, int st, uint32_t mg, mh8 (&b)[kChains]) {
         const int t = st >> 1, jh = st & 1;
         const mu4& q = (t & 1) ? r.lb : r.la;
@@ -240,14 +235,19 @@ struct MQ6K {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const uint32_t lo4 = (t < 2 ? L[i] : L[i] >> 4) & 0x0F0F0F0Fu;
-            // bits 2t, 2t + 1 of each qh byte -> bits 4, 5
             const uint32_t hs = t == 0 ? H[i] << 4 : t == 1 ? H[i] << 2 : t == 2 ? H[i] : H[i] >> 2;
             const uint32_t u = andor(hs, 0x30303030u, lo4);
-            cd[2 * i] = __builtin_amdgcn_perm(mg, u, 0x07020500u);      // (1024 + u0, 1024 + u2)
-            cd[2 * i + 1] = __builtin_amdgcn_perm(mg, u, 0x07030501u);  // (1024 + u1, 1024 + u3)
+            cd[2 * i] = __builtin_amdgcn_perm(mg, u, 0x07020500u);
+            cd[2 * i + 1] = __builtin_amdgcn_perm(mg, u, 0x07030501u);
         }
-        b[0] = bop(cd[0], cd[1], cd[2], cd[3], p.sl[t], p.ol[t]);
-        b[1] = bop(cd[0], cd[1], cd[2], cd[3], p.sh[t], p.oh[t]);
+        // (1024 + u) - 1056 = u - 32 exactly, then times sc: one rounding where |sc (u - 32)| > 2048
+        const mh2 off = {static_cast<_Float16>(-1056.0f), static_cast<_Float16>(-1056.0f)};
+        const mh2 sv = as_mh2(p.s[t]);
+        const mh2 r0 = (as_mh2(cd[0]) + off) * sv, r1 = (as_mh2(cd[1]) + off) * sv;
+        const mh2 r2 = (as_mh2(cd[2]) + off) * sv, r3 = (as_mh2(cd[3]) + off) * sv;
+        const _Float16 __attribute__((ext_vector_type(4))) lo = __builtin_shufflevector(r0, r1, 0, 1, 2, 3);
+        const _Float16 __attribute__((ext_vector_type(4))) hi = __builtin_shufflevector(r2, r3, 0, 1, 2, 3);
+        b[0] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     }
 };
 
@@ -806,7 +806,9 @@ template <class F, int R, typename TA, typename TC>
 hipError_t mlaunch_ring(const void* A, const MSegs<TC>& sg, int nrg, int M, int K, bool a_vec, const MDev& di,
                         hipStream_t stream) {
     // ring of 3 or 4 chunks: fewer passes first, then more chunks in flight per CU (workgroups per CU
-    // times ring depth - 1), then the shallower ring
+    // times ring depth - 1), then the shallower ring.  Q6_K (one 26 KiB chunk of 16 rows x 8
+    // super-blocks) takes a ring of 2 where that lets two workgroups share a CU (M <= 4): the second
+    // workgroup's arithmetic then overlaps the first's waits (70B down at M = 4: 55 -> 51 us).
     const MPlan p3 = mplan<F, TA>(M, 3, di.max_lds), p4 = mplan<F, TA>(M, 4, di.max_lds);
     if (p3.rows == 0) return hipErrorNotSupported;
     hipError_t e;
@@ -816,6 +818,14 @@ hipError_t mlaunch_ring(const void* A, const MSegs<TC>& sg, int nrg, int M, int 
     if (p4.rows > 0) {
         if ((e = mocc(mkern<F, R, 4, TA, TC>(), mlds_bytes<F, TA>(p4.rows, 4, p4.bg), occ4)) != hipSuccess) return e;
         use4 = p4.passes < p3.passes || (p4.passes == p3.passes && p4.bg >= p3.bg && 3 * occ4 > 2 * occ3);
+    }
+    if constexpr (F::kType == QMM_TYPE_Q6_K) {
+        const MPlan p2 = mplan<F, TA>(M, 2, di.max_lds);  // (its rows per pass at most p3's)
+        int occ2 = 0;
+        if (p2.rows > 0 && p2.passes <= p3.passes) {
+            if ((e = mocc(mkern<F, R, 2, TA, TC>(), mlds_bytes<F, TA>(p2.rows, 2, p2.bg), occ2)) != hipSuccess) return e;
+            if (occ2 > occ3 && occ2 > occ4) return mlaunch<F, R, 2, TA, TC>(A, sg, nrg, M, K, a_vec, p2, occ2, di.cus, stream);
+        }
     }
     if (use4) return mlaunch<F, R, 4, TA, TC>(A, sg, nrg, M, K, a_vec, p4, occ4, di.cus, stream);
     return mlaunch<F, R, 3, TA, TC>(A, sg, nrg, M, K, a_vec, p3, occ3, di.cus, stream);
@@ -867,9 +877,9 @@ hipError_t mdtypes(int a_dtype, int c_dtype, const void* A, const void* const* W
 
 // Where the matrix-core GEMV runs.  Q4_K: from M = 2 (the v_dot2 GEMV is faster at M = 1; 70B gate
 // 28672 x 8192: 26 against 30 us), and at M = 1 too in row-identity mode.  Q6_K: from M = 3 (70B down
-// 8192 x 28672: 58 us at M = 1..8 against 41, 42, 72 and 98 us for v_dot2 at M = 1, 2, 4, 8: its decode
-// takes two MFMA chains and twice the VALU work of Q4_K); row-identity mode keeps Q6_K on v_dot2 for
-// every M, so that its M = 1 calls (decode) keep the faster kernel.
+// 8192 x 28672: 49-52 us at M = 3, 4 and 55-58 us at M = 8..16 against 41, 42, 72 and 98 us for v_dot2
+// at M = 1, 2, 4, 8: its decode takes about 1.5 times the VALU work of Q4_K); row-identity mode keeps
+// Q6_K on v_dot2 for every M, so that its M = 1 calls (decode) keep the faster kernel.
 int gemv_mfma_min_m(int ggml_type, bool identity) {
     if (ggml_type == QMM_TYPE_Q4_K) return identity ? 1 : 2;
     if (ggml_type == QMM_TYPE_Q6_K) return identity ? INT_MAX : 3;
