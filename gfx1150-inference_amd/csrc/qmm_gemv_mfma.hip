@@ -101,7 +101,6 @@ __device__ __forceinline__ mh8 bop(uint32_t c0, uint32_t c1, uint32_t c2, uint32
 struct MQ4K {
     static constexpr int kType = QMM_TYPE_Q4_K;
     static constexpr int kBlockBytes = kBytesQ4_K;
-    static constexpr int kChains = 1;
     static constexpr bool kSums = true;  // group minima: a second MFMA over the activations' group sums
     static constexpr int kGroupK = 32;
     struct Raw {
@@ -156,9 +155,8 @@ struct MQ4K {
         p.sh[4] = r.q1.x >> 8; p.sh[5] = r.q1.y >> 8; p.sh[6] = r.q1.z >> 8; p.sh[7] = r.q1.w >> 8;
         return p;
     }
-    // B operand of step t (chain 0): t < 4 low nibbles of dwords 2t, 2t + 1 of the chunk, t >= 4 the
-    // high nibbles of dwords 2(t - 4), 2(t - 4) + 1.
-    __device__ static void steps(const Raw& r, const Pre& p, int t, uint32_t mg, mh8 (&b)[kChains]) { b[0] = step(r, p, t, mg); }
+    // B operand of step t: t < 4 low nibbles of dwords 2t, 2t + 1 of the chunk, t >= 4 the high nibbles
+    // of dwords 2(t - 4), 2(t - 4) + 1.
     __device__ static mh8 step(const Raw& r, const Pre& p, int t, uint32_t mg) {
         const int j = t & 3;
         const mu4& q = j < 2 ? r.q0 : r.q1;
@@ -180,7 +178,6 @@ struct MQ4K {
 struct MQ6K {
     static constexpr int kType = QMM_TYPE_Q6_K;
     static constexpr int kBlockBytes = kBytesQ6_K;
-    static constexpr int kChains = 1;
     static constexpr bool kSums = false;
     static constexpr int kGroupK = 16;
     struct Raw {
@@ -226,7 +223,7 @@ struct MQ6K {
     }
     // B operand of step st: sc (u - 32) for bytes 8 (st & 1) .. + 7 of the lane's slices (weights
     // j = 8 (st & 1) + 0..7 of group t = st / 2).
-    __device__ static void steps(const Raw& r, const Pre& p, int st, uint32_t mg, mh8 (&b)[kChains]) {
+    __device__ static mh8 step(const Raw& r, const Pre& p, int st, uint32_t mg) {
         const int t = st >> 1, jh = st & 1;
         const mu4& q = (t & 1) ? r.lb : r.la;
         const uint32_t L[2] = {jh ? q.z : q.x, jh ? q.w : q.y};
@@ -247,7 +244,7 @@ struct MQ6K {
         const mh2 r2 = (as_mh2(cd[2]) + off) * sv, r3 = (as_mh2(cd[3]) + off) * sv;
         const _Float16 __attribute__((ext_vector_type(4))) lo = __builtin_shufflevector(r0, r1, 0, 1, 2, 3);
         const _Float16 __attribute__((ext_vector_type(4))) hi = __builtin_shufflevector(r2, r3, 0, 1, 2, 3);
-        b[0] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     }
 };
 
@@ -621,20 +618,13 @@ __global__ __launch_bounds__(64 * kSlots) void gemv_mfma_kernel(const TA* __rest
                         F::load(ring + cslot * CK::kBytes + n * CK::kRP * 16 + w * F::kBlockBytes, c);
                     const typename F::Pre p = F::prep(raw, c);
                     mf4 T = {0.0f, 0.0f, 0.0f, 0.0f};
-                    mf4 T2 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) {
-                        mh8 bw[F::kChains];
-                        F::steps(raw, p, t, mg, bw);
-                        T = mfma16(ao.a[t], bw[0], T);
-                        if constexpr (F::kChains == 2) T2 = mfma16(ao.a[t], bw[1], T2);
-                    }
+                    for (int t = 0; t < 8; ++t) T = mfma16(ao.a[t], F::step(raw, p, t, mg), T);
                     mf4 U = {0.0f, 0.0f, 0.0f, 0.0f};
                     if constexpr (F::kSums) U = mfma16(ao.s, p.bu, U);
 #pragma unroll
                     for (int r = 0; r < R; ++r) {
-                        float tv = T[r];
-                        if constexpr (F::kChains == 2) tv = __fmaf_rn(16.0f, T2[r], tv);
+                        const float tv = T[r];
                         const float uv = U[r];
                         float yn;
                         if (kF32 && eo[r] != 0) {
