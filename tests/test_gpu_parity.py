@@ -228,6 +228,29 @@ def test_gemv_dtypes(dev, t, a_dtype, c_dtype):
     assert O.max_rel_err(y, y64) <= GEMV_TOL
 
 
+@pytest.mark.parametrize("M", [3, 4, 16])
+def test_q6k_extreme_subscales_within_bound(dev, M):
+    """Q6_K blocks whose sub-scales are all -128 or 127 and whose 6-bit codes are 0, 15, 48 or 63
+    (ql and qh bytes all 0x00 or 0xFF), so most products s (u - 32) lie above 2048 in magnitude,
+    where the matrix-core GEMV's f16 operand s (u - 32) is rounded (M >= 3, K a multiple of 2048):
+    the result stays within the GEMV bar against fp64 on the exact weights, with fp16 activations
+    (the decode dtype) and with fp32 activations."""
+    rng = np.random.default_rng(4242 + M)
+    N, K = 64, 4096
+    blk = O.synth_weights(O.GGML_Q6_K, N, K, rng).reshape(-1, 210)
+    nb = blk.shape[0]
+    blk[:, 0:192] = np.where(rng.integers(0, 2, size=(nb, 192)) == 1, 0xFF, 0x00).astype(np.uint8)
+    blk[:, 192:208] = np.where(rng.integers(0, 2, size=(nb, 16)) == 1, 0x80, 0x7F).astype(np.uint8)
+    raw = blk.reshape(-1)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    for a_dtype in ("f16", "f32"):
+        xa = x.astype(np.float16).astype(np.float32) if a_dtype == "f16" else x
+        y64 = O.matmul_f64(O.GGML_Q6_K, xa, raw, N, K)
+        y = gemm(O.GGML_Q6_K, x, raw, N, K, dev, a_dtype=a_dtype)
+        err = O.max_rel_err(y, y64)
+        assert err <= GEMV_TOL, (M, a_dtype, err)
+
+
 @pytest.mark.parametrize("t", TYPES)
 def test_gemv_rows_bit_identical_across_m(dev, t):
     import qmm
