@@ -18,9 +18,9 @@
 //     otherwise rounded once (|s (u - 32)| <= 4096: an error of at most 1, below the f16 rounding of
 //     d s (u - 32) in the reference's dequantized weights).  The MFMA's products of these operands
 //     are exact; its fp32 sums round.
-//   * Per super-block and row: y += d * T - c2 * U, where U is a second MFMA over the per-group sums
-//     of the staged activations (held as f16 hi + lo pairs of sum / 32) against the group minima
-//     (Q4_K: the 6-bit mins, c2 = 32 dmin) or the sub-scales (Q6_K's code offset 32: c2 = 1024 d).
+//   * Per super-block and row: Q4_K y += d * T - c2 * U, where U is a second MFMA over the per-group
+//     sums of the staged activations (held as f16 hi + lo pairs of sum / 32) against the 6-bit group
+//     minima (c2 = 32 dmin); Q6_K y += d * T (its code offset is inside the B operand).
 //   * The K range of a row group is cut into 8 fixed slots (super-blocks sb with sb % 8 = slot), one
 //     per wave of the 8-wave workgroup; a wave adds its slot's super-blocks in order and the 8 slot
 //     sums are added in slot order through LDS.  Every row's arithmetic is therefore the same
@@ -92,9 +92,9 @@ __device__ __forceinline__ mh8 bop(uint32_t c0, uint32_t c1, uint32_t c2, uint32
 
 // ------------------------------------------------------------------------------------------------
 // Formats.  Lane quarter c's A fragment of MFMA step t starts at super-block k = k0(c, t) and covers 8
-// consecutive k in the pair order (0, 2), (1, 3), (4, 6), (5, 7).  Group sums: group j of kGroups
-// per super-block covers kGroupK consecutive k from gk(j); it lands in half hpos(j) (hi) and
-// hpos(j) + 4 (lo)... of the 8-half sum fragment of quarter gq(j).
+// consecutive k in the pair order (0, 2), (1, 3), (4, 6), (5, 7).  Q4_K's group sums (group_sums):
+// quarter c holds sub-blocks 2c and 2c + 1, their hi halves at 0, 1 and lo halves at 2, 3 of the sum
+// fragment.
 // ------------------------------------------------------------------------------------------------
 
 // Q4_K (reference block_q4_k, src/kernels/dequantize.hip:31-36; get_scale_min_k4 :52-65).
@@ -102,15 +102,10 @@ struct MQ4K {
     static constexpr int kType = QMM_TYPE_Q4_K;
     static constexpr int kBlockBytes = kBytesQ4_K;
     static constexpr bool kSums = true;  // group minima: a second MFMA over the activations' group sums
-    static constexpr int kGroupK = 32;
     struct Raw {
         mu4 h, q0, q1;
     };
     __device__ static int k0(int c, int t) { return 64 * c + 8 * t; }
-    // group j = sub-block j: quarter j / 2, hi at half j % 2, lo at half 2 + j % 2
-    __device__ static int gq(int j) { return j >> 1; }
-    __device__ static int hpos(int j) { return j & 1; }
-    __device__ static int lpos(int j) { return 2 + (j & 1); }
     __device__ static Raw load(const uint8_t* blk, int c) {
         Raw r;
         r.h = *reinterpret_cast<const mu4*>(blk);
@@ -179,15 +174,11 @@ struct MQ6K {
     static constexpr int kType = QMM_TYPE_Q6_K;
     static constexpr int kBlockBytes = kBytesQ6_K;
     static constexpr bool kSums = false;
-    static constexpr int kGroupK = 16;
     struct Raw {
         mu4 la, lb, qh;
         uint32_t s0, s1, d;
     };
     __device__ static int k0(int c, int st) { return 128 * (c >> 1) + 32 * (st >> 1) + 16 * (c & 1) + 8 * (st & 1); }
-    __device__ static int gq(int) { return 0; }
-    __device__ static int hpos(int) { return 0; }
-    __device__ static int lpos(int) { return 0; }
     __device__ static Raw load(const uint8_t* blk, int c) {
         const int hf = c >> 1, h = c & 1;
         Raw r;
@@ -232,10 +223,11 @@ struct MQ6K {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const uint32_t lo4 = (t < 2 ? L[i] : L[i] >> 4) & 0x0F0F0F0Fu;
+            // bits 2t, 2t + 1 of each qh byte -> bits 4, 5
             const uint32_t hs = t == 0 ? H[i] << 4 : t == 1 ? H[i] << 2 : t == 2 ? H[i] : H[i] >> 2;
             const uint32_t u = andor(hs, 0x30303030u, lo4);
-            cd[2 * i] = __builtin_amdgcn_perm(mg, u, 0x07020500u);
-            cd[2 * i + 1] = __builtin_amdgcn_perm(mg, u, 0x07030501u);
+            cd[2 * i] = __builtin_amdgcn_perm(mg, u, 0x07020500u);      // (1024 + u0, 1024 + u2)
+            cd[2 * i + 1] = __builtin_amdgcn_perm(mg, u, 0x07030501u);  // (1024 + u1, 1024 + u3)
         }
         // (1024 + u) - 1056 = u - 32 exactly, then times sc: one rounding where |sc (u - 32)| > 2048
         const mh2 off = {static_cast<_Float16>(-1056.0f), static_cast<_Float16>(-1056.0f)};
